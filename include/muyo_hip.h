@@ -1,0 +1,301 @@
+/*
+ * muyo_hip: the C ABI of the MI355X (gfx950) decode-step kernel set.
+ *
+ * Every entry point takes plain pointers and sizes: no HIP, torch or C++ types appear in the
+ * signatures, so the library binds from C, C++, ctypes, cgo or JNI alike. Device pointers are
+ * HIP device addresses; `stream` is a `hipStream_t` passed as `void*` (NULL = the default
+ * stream). Launches are asynchronous on `stream` unless stated otherwise.
+ *
+ * Per-op launchers. Each replaces one reference graph node: the node declared a shader, a
+ * push-constant block (muyo/LlamaContracts.h), its buffers in descriptor-binding order and a
+ * `vkCmdDispatch(x, y, z)`. The launcher takes exactly those, in that order, and computes what
+ * the node computed over the work domain that dispatch covered. The reference's shader
+ * workgroup shape is NOT reproduced: the kernels pick their own gfx950 geometry.
+ *
+ * Return value: 0 on success; a negative MUYO_E_* when the arguments break the contract (nothing
+ * is launched); a positive hipError_t when HIP rejects the launch. `muyo_last_error()` gives the
+ * message of the most recent failure on the calling thread.
+ *
+ * Ownership: the caller owns every buffer passed to a launcher; launchers do not retain
+ * pointers beyond the call. The decoder (below) owns the buffers it allocates.
+ */
+#ifndef MUYO_HIP_H
+#define MUYO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "muyo/LlamaContracts.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum
+{
+    MUYO_OK = 0,
+    MUYO_E_NULL = -1,        /* a required pointer is NULL */
+    MUYO_E_CONTRACT = -2,    /* a push-constant field is inconsistent (stride, fastdiv magic, ...) */
+    MUYO_E_DISPATCH = -3,    /* the dispatch shape is not one the op's shader accepts */
+    MUYO_E_UNSUPPORTED = -4, /* a feature of the contract this build does not implement */
+    MUYO_E_RANGE = -5,       /* a size or position is out of range */
+    MUYO_E_NOMEM = -6,       /* device allocation failed */
+    MUYO_E_STATE = -7        /* the object is not in a state that allows the call */
+};
+
+/* Message describing the last failure on this thread ("" if none). */
+const char* muyo_last_error(void);
+
+/* Library version string. */
+const char* muyo_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Per-op launchers (one per reference shader variant).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Specialisation constants of mul_mat_vec (src/LlamaContracts.h:102-107). blockSize is accepted
+ * and ignored (the kernel picks its own wave geometry); numRows scales the dispatch into rows;
+ * numCols must be 1 (one B column, the decode case). */
+typedef struct MuyoMatVecSpec
+{
+    uint32_t blockSize;
+    uint32_t numRows;
+    uint32_t numCols;
+} MuyoMatVecSpec;
+
+/* mul_mat_vec_f16_f32_f32 (CMakeLists.txt:168-172; shaders/llama/mul_mat_vec.comp:248-264).
+ * Replaces the GEMV node of src/MatVec.cpp:112-172 and the projection nodes of
+ * src/FullModel.cpp:133-175,237-253,347-418,474-485.
+ *   d[batch][row] = sum_k f32(A[batchA][row*ncols + k]) * B[batch][k]
+ *                   (+ FUSE0[...] if BIAS0) (+ FUSE1[...] if BIAS1)
+ * Rows computed: [0, min(numRows*x*z, strideD)); batches: y. As in the shader, the A row stride
+ * is `ncols` (strideA is not used for rows), batchA follows ne12/broadcast2/broadcast3, and the
+ * SCALE flags have no effect outside the expert-indexed variant. spec may be NULL (32/1/1). */
+int muyo_mul_mat_vec_f16_f32_f32(const LlamaMatVecPushConstants* pc, const MuyoMatVecSpec* spec, const void* a,
+                                 const float* b, float* d, const float* fuse0, const float* fuse1, uint32_t dispatch_x,
+                                 uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* mul_mat_vec_f32_f32_f32 (CMakeLists.txt:174-178): same contract with F32 A. This is the
+ * GQA-batched attention GEMV of src/FullModel.cpp:294-345 (scores over the key cache with
+ * dispatch x = position + 1, and values over the transposed value cache). */
+int muyo_mul_mat_vec_f32_f32_f32(const LlamaMatVecPushConstants* pc, const MuyoMatVecSpec* spec, const float* a,
+                                 const float* b, float* d, const float* fuse0, const float* fuse1, uint32_t dispatch_x,
+                                 uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* rms_norm_f32 (CMakeLists.txt:117-121; shaders/llama/rms_norm.comp:53-151). Replaces
+ * src/RmsNorm.cpp:112-160 and src/FullModel.cpp:215-247. One output row per dispatched
+ * workgroup (x = rows, y = channels, z = samples):
+ *   d = x * rsqrt(mean(x^2) + param1) [* w]   (w when do_multiply != 0)
+ * `partial_sums` is the shader's declared-but-unread binding 3 and may be NULL. */
+int muyo_rms_norm_f32(const LlamaAddPushConstants* pc, uint32_t do_multiply, const float* a, const float* b, float* d,
+                      float* partial_sums, uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z,
+                      void* stream);
+
+/* The same op with an fp16 weight row (the reference reads F32 norm weights; fp16 is the storage
+ * the decode workloads here use). The weight is widened exactly to f32 before the multiply. */
+int muyo_rms_norm_f32_f16w(const LlamaAddPushConstants* pc, uint32_t do_multiply, const float* a, const void* b,
+                           float* d, float* partial_sums, uint32_t dispatch_x, uint32_t dispatch_y,
+                           uint32_t dispatch_z, void* stream);
+
+/* add_f32 (CMakeLists.txt:110-115; shaders/llama/add.comp:23-46). Replaces
+ * src/ElementwiseAdd.cpp:100-190 and src/FullModel.cpp:250-284. d = a + b over the dispatched
+ * element range, B broadcast by modulo unless norepeat != 0. ADD_RMS is off (as compiled by the
+ * reference), so partial_sums is not written and may be NULL. Canonical dispatch: (1, ceil(ne/512), z). */
+int muyo_add_f32(const LlamaAddPushConstants* pc, uint32_t norepeat, const float* a, const float* b, float* d,
+                 float* partial_sums, uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* swiglu_f32 (CMakeLists.txt:130-134; shaders/llama/swiglu.comp + glu_main.glsl). Replaces
+ * src/Swiglu.cpp:100-160 and src/FullModel.cpp:287-327. d = silu(a) * b in the mode of
+ * `pc->mode`. Index quotients use the divisors the ne2_* fastdiv words encode (as the shader
+ * does); a word pair that is init_fastdiv_values of no divisor (e.g. zeroed) is MUYO_E_CONTRACT. */
+int muyo_swiglu_f32(const LlamaGluPushConstants* pc, const float* a, const float* b, float* d, uint32_t dispatch_x,
+                    uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* rope_neox_f32 (CMakeLists.txt:123-128; shaders/llama/rope_neox.comp, rope_funcs.glsl:76-114).
+ * Replaces src/Rope.cpp:95-160 and src/FullModel.cpp:179-212 (q rope and the k rope that writes
+ * into the key cache through nb11/dOffset). Positions are int32 per i2; `ff` is read only when
+ * hasFf != 0 and `set_rows` (uint32 pairs) only when setRowsStride != 0. */
+int muyo_rope_neox_f32(const LlamaRopePushConstants* pc, const float* x, const int32_t* positions, const float* ff,
+                       float* d, const uint32_t* set_rows, uint32_t dispatch_x, uint32_t dispatch_y,
+                       uint32_t dispatch_z, void* stream);
+
+/* soft_max_f32 (CMakeLists.txt:161-163; shaders/llama/soft_max.comp:41-172). Replaces
+ * src/SoftMax.cpp:75-140 and src/FullModel.cpp:331-349. Row r = z*262144 + y*512 + x of the
+ * dispatch, bounded by nrowsX: d = softmax(x*scale + slope*mask [, sink]). */
+int muyo_soft_max_f32(const LlamaSoftMaxPushConstants* pc, const float* x, const float* mask, const float* sinks,
+                      float* d, uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* argmax_f32 (CMakeLists.txt:148-150; shaders/llama/argmax.comp:20-60). Replaces
+ * src/Argmax.cpp:75-120 and src/FullModel.cpp:461-484. d[row] = index of the largest of the KX
+ * values of row `row` (< KY). Ties resolve to the LOWEST index, which is the rule of the host
+ * greedy scan the reference actually samples with (src/Sampler.cpp:32-43). */
+int muyo_argmax_f32(const LlamaGenericHeadPushConstants* pc, const float* a, int32_t* d, uint32_t dispatch_x,
+                    uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* get_rows_f16_f32 / get_rows_f32 (CMakeLists.txt:136-146; shaders/llama/get_rows.comp:8-42).
+ * Replace src/GetRows.cpp:95-150 and src/FullModel.cpp:424-458: d[i10][:] = f32(A[idx[i10]][:]).
+ * A row index outside [0, ne01) gives a zero row instead of an out-of-bounds read. */
+int muyo_get_rows_f16_f32(const LlamaAddPushConstants* pc, const void* a, const int32_t* b, float* d,
+                          uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+int muyo_get_rows_f32(const LlamaAddPushConstants* pc, const float* a, const int32_t* b, float* d, uint32_t dispatch_x,
+                      uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* cpy_f32_f32 (CMakeLists.txt:156-159; shaders/llama/copy.comp + generic_unary_head.glsl).
+ * Replaces the value-column append of src/FullModel.cpp:353-420 and src/KvCache.cpp:181-226:
+ * d[doff + dst_idx(i)] = a[aoff + src0_idx(i)], i < ne. As in the shader, the quotients of
+ * src0_idx/dst_idx use the divisors the fastdiv words encode (shifts packed outermost divisor
+ * first) and the offsets use the shapes; a pair that encodes no divisor is MUYO_E_CONTRACT and
+ * an index whose unsigned arithmetic would wrap is skipped. */
+int muyo_cpy_f32_f32(const LlamaCopyPushConstants* pc, const float* a, float* d, uint32_t dispatch_x,
+                     uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Decode-step attention over an fp16 KV cache (no single reference node: it replaces the
+ * k_rope -> kcache, v_copy -> vcache, attn_scores, attn_weights and attn_output nodes of
+ * src/FullModel.cpp:258-345 for one layer).
+ * Layout: kcache/vcache are [kv_heads][max_seq][head_dim] fp16; q is [heads][head_dim] f32.
+ * For every query head h (kv head h / (heads/kv_heads)):
+ *   out[h] = sum_{j<=pos} softmax_j(scale * q[h].k[j]) * v[j]
+ * `positions` is a device int32 (the cache row of the current token; keys 0..pos are read).
+ * The caller appends k/v of the current token before this call (muyo_kv_append_f16).
+ * ------------------------------------------------------------------------------------------- */
+int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* vcache, float* out,
+                                const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                uint32_t max_seq, float scale, void* stream);
+
+/* Rope k (NeoX, theta = pos * theta_scale^j) and append k and v of the current token, as fp16,
+ * at row `*position` of the [kv_heads][max_seq][head_dim] caches; q is roped into q_out. This
+ * is the q_rope + k_rope + v_copy node trio of src/FullModel.cpp:258-292 for an fp16 cache. */
+int muyo_rope_append_f16kv(const float* q, const float* k, const float* v, float* q_out, void* kcache, void* vcache,
+                           const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                           uint32_t max_seq, float theta_scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Decoder: the composed decode step (src/FullModel.cpp:487-1292 RunFullModel's graph plus its
+ * feedToken/sampleNext loop, minus GGUF loading and tokenisation). Device memory is owned by the
+ * decoder; the step is captured once into a hipGraph and replayed per token with the token and
+ * position held in device memory.
+ * ------------------------------------------------------------------------------------------- */
+
+typedef struct MuyoQwen2Config
+{
+    uint32_t layers;
+    uint32_t hidden;
+    uint32_t feedForward;
+    uint32_t heads;
+    uint32_t kvHeads;
+    uint32_t headDim;
+    uint32_t vocab;
+    uint32_t maxSeq;
+    float rmsEps;
+    float ropeBase;
+} MuyoQwen2Config;
+
+typedef struct MuyoDecoder MuyoDecoder;
+
+/* Tensor kinds a caller may address (per layer where noted). Shapes, row-major:
+ *   TOKEN_EMBD   fp16 [vocab][hidden]   (also the tied LM head)
+ *   OUTPUT_NORM  f32  [hidden]
+ *   ATTN_NORM    f32  [hidden]                               per layer
+ *   ATTN_QKV     fp16 [heads*hd + 2*kvHeads*hd][hidden]      per layer (q rows, then k, then v)
+ *   ATTN_QKV_B   f32  [heads*hd + 2*kvHeads*hd]              per layer
+ *   ATTN_OUTPUT  fp16 [hidden][heads*hd]                     per layer
+ *   FFN_NORM     f32  [hidden]                               per layer
+ *   FFN_GATE     fp16 [feedForward][hidden]                  per layer
+ *   FFN_UP       fp16 [feedForward][hidden]                  per layer
+ *   FFN_DOWN     fp16 [hidden][feedForward]                  per layer
+ *   KCACHE       fp16 [kvHeads][maxSeq][hd]                  per layer
+ *   VCACHE       fp16 [kvHeads][maxSeq][hd]                  per layer
+ *   LOGITS       f32  [vocab]                                (output of the last step) */
+enum
+{
+    MUYO_TENSOR_TOKEN_EMBD = 0,
+    MUYO_TENSOR_OUTPUT_NORM = 1,
+    MUYO_TENSOR_ATTN_NORM = 2,
+    MUYO_TENSOR_ATTN_QKV = 3,
+    MUYO_TENSOR_ATTN_QKV_B = 4,
+    MUYO_TENSOR_ATTN_OUTPUT = 5,
+    MUYO_TENSOR_FFN_NORM = 6,
+    MUYO_TENSOR_FFN_GATE = 7,
+    MUYO_TENSOR_FFN_UP = 8,
+    MUYO_TENSOR_FFN_DOWN = 9,
+    MUYO_TENSOR_KCACHE = 10,
+    MUYO_TENSOR_VCACHE = 11,
+    MUYO_TENSOR_LOGITS = 12
+};
+
+/* Allocate a decoder for `config` on the current HIP device. Caches are zeroed. */
+int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** out);
+void muyo_decoder_destroy(MuyoDecoder* decoder);
+
+/* Device address and byte size of one tensor. */
+int muyo_decoder_tensor(MuyoDecoder* decoder, uint32_t kind, uint32_t layer, void** device_ptr, uint64_t* bytes);
+
+/* Synchronous host<->device copies of a whole tensor (bytes must equal the tensor's size). */
+int muyo_decoder_upload(MuyoDecoder* decoder, uint32_t kind, uint32_t layer, const void* host, uint64_t bytes);
+int muyo_decoder_download(MuyoDecoder* decoder, uint32_t kind, uint32_t layer, void* host, uint64_t bytes);
+
+/* Fill every weight from the portable seeded generator (muyo_fill_normal_f16/f32 below):
+ * matrices and the embedding N(0, 0.02), biases N(0, 0.02), norm weights N(1, 0.1). Tensor t of
+ * layer l uses stream seed muyo_tensor_seed(seed, t, l). Caches are zeroed. */
+int muyo_decoder_fill_random(MuyoDecoder* decoder, uint64_t seed);
+
+/* Fill cache rows [0, positions) of every layer with N(0, 1) (seeded like fill_random, kinds
+ * KCACHE/VCACHE), and zero the rest. */
+int muyo_decoder_fill_kv_random(MuyoDecoder* decoder, uint32_t positions, uint64_t seed);
+
+/* One decode step, synchronous: feed `token` at cache row `position`, return the greedy next
+ * token (ties to the lowest index). Logits are left in the LOGITS tensor. */
+int muyo_decoder_step(MuyoDecoder* decoder, int32_t token, int32_t position, int32_t* next_token);
+
+/* Greedy generation fully on the device: feeds `token` at `position`, then feeds back each
+ * greedy token, for `count` steps, with no host round trip between steps (one hipGraph launch
+ * per step). ids[i] receives the i-th generated token. Synchronises `stream` before returning. */
+int muyo_decoder_generate(MuyoDecoder* decoder, int32_t token, int32_t position, uint32_t count, int32_t* ids,
+                          void* stream);
+
+/* Enqueue `count` greedy steps on `stream` without synchronising (for timing); the ids stay on
+ * the device and are fetched with muyo_decoder_generated_ids. */
+int muyo_decoder_generate_async(MuyoDecoder* decoder, int32_t token, int32_t position, uint32_t count, void* stream);
+int muyo_decoder_generated_ids(MuyoDecoder* decoder, int32_t* ids, uint32_t count);
+
+/* Number of kernel launches one step enqueues (for reporting). */
+uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* decoder);
+
+/* Kernels of one step, for per-kernel timing and profiling. */
+enum
+{
+    MUYO_KERNEL_EMBED = 0,     /* token row -> hidden f32 */
+    MUYO_KERNEL_QKV = 1,       /* rms_norm + q|k|v GEMV + bias + rope + cache append */
+    MUYO_KERNEL_ATTENTION = 2, /* GQA attention over cache rows 0..position */
+    MUYO_KERNEL_O_PROJ = 3,    /* o_proj GEMV + residual */
+    MUYO_KERNEL_GATE_UP = 4,   /* rms_norm + gate/up GEMV + swiglu */
+    MUYO_KERNEL_DOWN = 5,      /* down GEMV + residual */
+    MUYO_KERNEL_LM_HEAD = 6    /* rms_norm + tied LM head + greedy argmax (advances the state) */
+};
+
+/* Set the device-side token and position (stream-ordered) without running a step. */
+int muyo_decoder_set_state(MuyoDecoder* decoder, int32_t token, int32_t position, void* stream);
+
+/* Enqueue exactly one kernel of the step for `layer` (ignored for EMBED and LM_HEAD) on
+ * `stream`, with the decoder's buffers and current device state. */
+int muyo_decoder_enqueue_kernel(MuyoDecoder* decoder, uint32_t kernel, uint32_t layer, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * Synthetic-input helpers (portable seeded generator; bit-identical on host and device).
+ *   word(seed, i)   = mix64(mix64(seed) + i)            mix64 = SplitMix64's finaliser
+ *   uniform(i)      = (word >> 40) * 2^-23 - 1          in [-1, 1), exact in f32
+ *   normal(i)       = sum of the 12 32-bit halves of word(6i .. 6i+5) * 2^-32 - 6
+ *                     (Irwin-Hall: mean 0, variance 1), then mean + std * normal in double,
+ *                     rounded to f32 and (for f16) on to fp16, both round-to-nearest-even.
+ * ------------------------------------------------------------------------------------------- */
+int muyo_fill_normal_f16(void* d, uint64_t count, uint64_t seed, double mean, double std, void* stream);
+int muyo_fill_normal_f32(float* d, uint64_t count, uint64_t seed, double mean, double std, void* stream);
+int muyo_fill_uniform_f32(float* d, uint64_t count, uint64_t seed, void* stream);
+uint64_t muyo_tensor_seed(uint64_t seed, uint32_t kind, uint32_t layer);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* MUYO_HIP_H */

@@ -1,0 +1,774 @@
+// The decode-step executor behind the muyo_decoder_* C ABI.
+//
+// It plays the role of RunFullModel's render graph (src/FullModel.cpp:487-1010) plus its
+// feedToken/sampleNext loop (:1096-1117): one arena of device memory holds every weight, the
+// fp16 KV cache and the activations; one step is 2 + 5 * layers launches on one stream
+// (decode_kernels.hip). The first step runs eagerly; later steps replay a hipGraph captured
+// once, because everything that changes per token (token id, position, step counter) lives in
+// device memory and is advanced by the last kernel of the step. Greedy generation therefore
+// needs no host round trip between tokens.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+#include "decode_kernels.hpp"
+
+using namespace muyo;
+
+namespace
+{
+constexpr uint32_t kIdsCapacity = 4096;
+constexpr size_t kAlign = 256;
+
+size_t AlignUp(size_t value) { return (value + kAlign - 1) / kAlign * kAlign; }
+
+struct TensorSlot
+{
+    size_t offset = 0;
+    size_t bytes = 0;
+};
+
+enum LayerTensor
+{
+    kAttnNorm,
+    kQkv,
+    kQkvBias,
+    kOut,
+    kFfnNorm,
+    kGate,
+    kUp,
+    kDown,
+    kKCache,
+    kVCache,
+    kLayerTensorCount
+};
+
+LayerTensor ToLayerTensor(uint32_t kind)
+{
+    switch (kind)
+    {
+        case MUYO_TENSOR_ATTN_NORM:
+            return kAttnNorm;
+        case MUYO_TENSOR_ATTN_QKV:
+            return kQkv;
+        case MUYO_TENSOR_ATTN_QKV_B:
+            return kQkvBias;
+        case MUYO_TENSOR_ATTN_OUTPUT:
+            return kOut;
+        case MUYO_TENSOR_FFN_NORM:
+            return kFfnNorm;
+        case MUYO_TENSOR_FFN_GATE:
+            return kGate;
+        case MUYO_TENSOR_FFN_UP:
+            return kUp;
+        case MUYO_TENSOR_FFN_DOWN:
+            return kDown;
+        case MUYO_TENSOR_KCACHE:
+            return kKCache;
+        case MUYO_TENSOR_VCACHE:
+            return kVCache;
+        default:
+            return kLayerTensorCount;
+    }
+}
+
+/// Writes the device state of a new generation run (a kernel, so it is stream-ordered and can
+/// never race a pinned host buffer).
+__global__ void SetStateKernel(DecodeState* state, int32_t token, int32_t position)
+{
+    state->token = token;
+    state->position = position;
+    state->step = 0;
+    state->pad = 0;
+}
+}  // namespace
+
+struct MuyoDecoder
+{
+    MuyoQwen2Config config{};
+    DecodeDims dims{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+
+    char* arena = nullptr;
+    size_t arenaBytes = 0;
+    TensorSlot tokenEmbd, outputNorm, logits;
+    std::vector<TensorSlot> layers;  // layer * kLayerTensorCount + tensor
+
+    float* xA = nullptr;
+    float* xB = nullptr;
+    float* xMid = nullptr;
+    float* q = nullptr;
+    float* attnOut = nullptr;
+    float* act = nullptr;
+    DecodeState* state = nullptr;
+    int32_t* ids = nullptr;
+    DecodeScratch scratch{};
+
+    bool warm = false;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+
+    template <typename T>
+    T* At(const TensorSlot& slot) const
+    {
+        return reinterpret_cast<T*>(arena + slot.offset);
+    }
+
+    const TensorSlot& Layer(uint32_t layer, LayerTensor tensor) const
+    {
+        return layers[static_cast<size_t>(layer) * kLayerTensorCount + tensor];
+    }
+};
+
+namespace
+{
+int Validate(const MuyoQwen2Config& c)
+{
+    if (c.layers == 0 || c.hidden == 0 || c.feedForward == 0 || c.heads == 0 || c.kvHeads == 0 || c.headDim == 0 ||
+        c.vocab == 0 || c.maxSeq == 0)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: every dimension must be >= 1");
+    }
+    if (c.heads % c.kvHeads != 0 || c.heads / c.kvHeads > 8)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: heads must be a multiple of kvHeads with a group of at most 8");
+    }
+    if (c.headDim != 64 && c.headDim != 128)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: headDim must be 64 or 128 (got %u)", c.headDim);
+    }
+    const uint64_t qdim = static_cast<uint64_t>(c.heads) * c.headDim;
+    if (c.hidden % 8 != 0 || c.feedForward % 8 != 0 || qdim % 8 != 0)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: hidden, feedForward and heads*headDim must be multiples of 8");
+    }
+    if (static_cast<uint64_t>(std::max<uint64_t>({c.hidden, c.feedForward, qdim})) * 4 > 160 * 1024)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: a GEMV input longer than 40960 floats does not fit LDS");
+    }
+    if (c.maxSeq > (1u << 24))
+    {
+        return Fail(MUYO_E_RANGE, "decoder: maxSeq %u is too large", c.maxSeq);
+    }
+    return MUYO_OK;
+}
+
+size_t LayerTensorBytes(const MuyoQwen2Config& c, LayerTensor t)
+{
+    const size_t hd = c.headDim;
+    const size_t qkvRows = (static_cast<size_t>(c.heads) + 2 * c.kvHeads) * hd;
+    const size_t qdim = static_cast<size_t>(c.heads) * hd;
+    switch (t)
+    {
+        case kAttnNorm:
+        case kFfnNorm:
+            return static_cast<size_t>(c.hidden) * sizeof(float);
+        case kQkv:
+            return qkvRows * c.hidden * 2;
+        case kQkvBias:
+            return qkvRows * sizeof(float);
+        case kOut:
+            return static_cast<size_t>(c.hidden) * qdim * 2;
+        case kGate:
+        case kUp:
+        case kDown:
+            return static_cast<size_t>(c.feedForward) * c.hidden * 2;
+        case kKCache:
+        case kVCache:
+            return static_cast<size_t>(c.kvHeads) * c.maxSeq * hd * 2;
+        default:
+            return 0;
+    }
+}
+
+int Enqueue(MuyoDecoder* d, hipStream_t s)
+{
+    const MuyoQwen2Config& c = d->config;
+    const uint32_t qdim = c.heads * c.headDim;
+    auto failed = [](hipError_t status, const char* kernel, uint32_t layer)
+    {
+        return Fail(static_cast<int>(status), "decoder step: launching %s (layer %u) failed: %s (%d)", kernel, layer,
+                    hipGetErrorString(status), static_cast<int>(status));
+    };
+    hipError_t status = LaunchEmbed(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->xA, c.hidden, c.vocab);
+    if (status != hipSuccess)
+    {
+        return failed(status, "embed", 0);
+    }
+    float* x = d->xA;
+    float* other = d->xB;
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        status = LaunchQkvRopeAppend(s, d->dims, x, d->At<float>(d->Layer(l, kAttnNorm)),
+                                     d->At<uint16_t>(d->Layer(l, kQkv)), d->At<float>(d->Layer(l, kQkvBias)), d->state,
+                                     d->q, d->At<uint16_t>(d->Layer(l, kKCache)), d->At<uint16_t>(d->Layer(l, kVCache)));
+        if (status != hipSuccess)
+        {
+            return failed(status, "qkv", l);
+        }
+        status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(l, kKCache)),
+                                 d->At<uint16_t>(d->Layer(l, kVCache)), &d->state->position, d->attnOut, d->scratch);
+        if (status != hipSuccess)
+        {
+            return failed(status, "attention", l);
+        }
+        status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kOut)), d->attnOut, x, d->xMid, c.hidden, qdim);
+        if (status != hipSuccess)
+        {
+            return failed(status, "o_proj", l);
+        }
+        status = LaunchGateUpSwiGlu(s, d->dims, d->xMid, d->At<float>(d->Layer(l, kFfnNorm)),
+                                    d->At<uint16_t>(d->Layer(l, kGate)), d->At<uint16_t>(d->Layer(l, kUp)), d->act);
+        if (status != hipSuccess)
+        {
+            return failed(status, "gate_up", l);
+        }
+        status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kDown)), d->act, d->xMid, other, c.hidden,
+                                      c.feedForward);
+        if (status != hipSuccess)
+        {
+            return failed(status, "down", l);
+        }
+        std::swap(x, other);
+    }
+    status = LaunchLmHeadArgMax(s, d->dims, x, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
+                                d->At<float>(d->logits), d->state, d->ids, kIdsCapacity, d->scratch);
+    if (status != hipSuccess)
+    {
+        return failed(status, "lm_head", 0);
+    }
+    return MUYO_OK;
+}
+
+/// One step on `s`: eager the first time, graph replay afterwards.
+int RunStep(MuyoDecoder* d, hipStream_t s)
+{
+    if (!d->warm)
+    {
+        const int status = Enqueue(d, s);
+        if (status != MUYO_OK)
+        {
+            return status;
+        }
+        d->warm = true;
+        return MUYO_OK;
+    }
+    if (d->exec == nullptr)
+    {
+        // Capture on the decoder's own stream after everything queued on `s` has been ordered
+        // before it (the capture itself runs nothing).
+        MUYO_HIP_CHECK(hipStreamSynchronize(s));
+        MUYO_HIP_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed));
+        const int status = Enqueue(d, d->stream);
+        hipGraph_t graph = nullptr;
+        const hipError_t end = hipStreamEndCapture(d->stream, &graph);
+        if (status != MUYO_OK)
+        {
+            if (graph != nullptr)
+            {
+                (void)hipGraphDestroy(graph);
+            }
+            return status;
+        }
+        if (end != hipSuccess)
+        {
+            return HipStatus(end, "hipStreamEndCapture");
+        }
+        d->graph = graph;
+        MUYO_HIP_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+    }
+    MUYO_HIP_CHECK(hipGraphLaunch(d->exec, s));
+    return MUYO_OK;
+}
+
+int FillTensor(MuyoDecoder* d, const TensorSlot& slot, bool half, uint64_t seed, double mean, double stddev)
+{
+    if (half)
+    {
+        return muyo_fill_normal_f16(d->arena + slot.offset, slot.bytes / 2, seed, mean, stddev, d->stream);
+    }
+    return muyo_fill_normal_f32(reinterpret_cast<float*>(d->arena + slot.offset), slot.bytes / 4, seed, mean, stddev,
+                                d->stream);
+}
+}  // namespace
+
+extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** out)
+{
+    if (config == nullptr || out == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder_create: config and out are required");
+    }
+    *out = nullptr;
+    const int valid = Validate(*config);
+    if (valid != MUYO_OK)
+    {
+        return valid;
+    }
+    auto* d = new MuyoDecoder();
+    d->config = *config;
+    const MuyoQwen2Config& c = d->config;
+    d->dims.hidden = c.hidden;
+    d->dims.ffn = c.feedForward;
+    d->dims.heads = c.heads;
+    d->dims.kvHeads = c.kvHeads;
+    d->dims.headDim = c.headDim;
+    d->dims.vocab = c.vocab;
+    d->dims.maxSeq = c.maxSeq;
+    d->dims.eps = c.rmsEps;
+    // The same f32 host computations as src/FullModel.cpp:184 and :201.
+    d->dims.thetaScale = std::pow(c.ropeBase, -2.0F / static_cast<float>(c.headDim));
+    d->dims.attnScale = 1.0F / std::sqrt(static_cast<float>(c.headDim));
+
+    // Arena layout: embedding, output norm, logits, then each layer's tensors, then activations
+    // and scratch. Every tensor starts on a 256-byte boundary.
+    size_t cursor = 0;
+    auto place = [&cursor](size_t bytes)
+    {
+        TensorSlot slot{cursor, bytes};
+        cursor = AlignUp(cursor + bytes);
+        return slot;
+    };
+    d->tokenEmbd = place(static_cast<size_t>(c.vocab) * c.hidden * 2);
+    d->outputNorm = place(static_cast<size_t>(c.hidden) * 4);
+    d->logits = place(static_cast<size_t>(c.vocab) * 4);
+    d->layers.resize(static_cast<size_t>(c.layers) * kLayerTensorCount);
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        for (int t = 0; t < kLayerTensorCount; ++t)
+        {
+            d->layers[static_cast<size_t>(l) * kLayerTensorCount + t] =
+                place(LayerTensorBytes(c, static_cast<LayerTensor>(t)));
+        }
+    }
+    const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
+    const size_t group = c.heads / c.kvHeads;
+    const size_t chunks = AttnChunks(c.maxSeq);
+    const TensorSlot xA = place(c.hidden * 4);
+    const TensorSlot xB = place(c.hidden * 4);
+    const TensorSlot xMid = place(c.hidden * 4);
+    const TensorSlot q = place(qdim * 4);
+    const TensorSlot attnOut = place(qdim * 4);
+    const TensorSlot act = place(static_cast<size_t>(c.feedForward) * 4);
+    const TensorSlot state = place(sizeof(DecodeState));
+    const TensorSlot ids = place(kIdsCapacity * 4);
+    const size_t small = c.kvHeads * chunks * group;
+    const TensorSlot attnMax = place(small * 4);
+    const TensorSlot attnSum = place(small * 4);
+    const TensorSlot attnAcc = place(small * c.headDim * 4);
+    const TensorSlot attnCount = place(c.kvHeads * 4);
+    const TensorSlot argValue = place(kArgMaxBlocks * 4);
+    const TensorSlot argIndex = place(kArgMaxBlocks * 4);
+    const TensorSlot argCount = place(4);
+    d->arenaBytes = cursor;
+
+    hipError_t status = hipGetDevice(&d->device);
+    if (status == hipSuccess)
+    {
+        status = hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking);
+    }
+    if (status == hipSuccess)
+    {
+        status = hipMalloc(reinterpret_cast<void**>(&d->arena), d->arenaBytes);
+        if (status != hipSuccess)
+        {
+            d->arena = nullptr;
+            const int code = Fail(MUYO_E_NOMEM, "decoder_create: hipMalloc of %zu bytes failed", d->arenaBytes);
+            muyo_decoder_destroy(d);
+            return code;
+        }
+    }
+    if (status == hipSuccess)
+    {
+        status = hipMemsetAsync(d->arena, 0, d->arenaBytes, d->stream);
+    }
+    if (status == hipSuccess)
+    {
+        status = hipStreamSynchronize(d->stream);
+    }
+    if (status != hipSuccess)
+    {
+        const int code = HipStatus(status, "decoder_create");
+        muyo_decoder_destroy(d);
+        return code;
+    }
+    d->xA = d->At<float>(xA);
+    d->xB = d->At<float>(xB);
+    d->xMid = d->At<float>(xMid);
+    d->q = d->At<float>(q);
+    d->attnOut = d->At<float>(attnOut);
+    d->act = d->At<float>(act);
+    d->state = d->At<DecodeState>(state);
+    d->ids = d->At<int32_t>(ids);
+    d->scratch.attnMax = d->At<float>(attnMax);
+    d->scratch.attnSum = d->At<float>(attnSum);
+    d->scratch.attnAcc = d->At<float>(attnAcc);
+    d->scratch.attnCount = d->At<uint32_t>(attnCount);
+    d->scratch.argValue = d->At<float>(argValue);
+    d->scratch.argIndex = d->At<int32_t>(argIndex);
+    d->scratch.argCount = d->At<uint32_t>(argCount);
+    *out = d;
+    return MUYO_OK;
+}
+
+extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
+{
+    if (d == nullptr)
+    {
+        return;
+    }
+    if (d->exec != nullptr)
+    {
+        (void)hipGraphExecDestroy(d->exec);
+    }
+    if (d->graph != nullptr)
+    {
+        (void)hipGraphDestroy(d->graph);
+    }
+    if (d->stream != nullptr)
+    {
+        (void)hipStreamSynchronize(d->stream);
+    }
+    if (d->arena != nullptr)
+    {
+        (void)hipDeviceSynchronize();
+        (void)hipFree(d->arena);
+    }
+    if (d->stream != nullptr)
+    {
+        (void)hipStreamDestroy(d->stream);
+    }
+    delete d;
+}
+
+namespace
+{
+int Lookup(MuyoDecoder* d, uint32_t kind, uint32_t layer, TensorSlot& slot)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    switch (kind)
+    {
+        case MUYO_TENSOR_TOKEN_EMBD:
+            slot = d->tokenEmbd;
+            return MUYO_OK;
+        case MUYO_TENSOR_OUTPUT_NORM:
+            slot = d->outputNorm;
+            return MUYO_OK;
+        case MUYO_TENSOR_LOGITS:
+            slot = d->logits;
+            return MUYO_OK;
+        default:
+            break;
+    }
+    const LayerTensor t = ToLayerTensor(kind);
+    if (t == kLayerTensorCount)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: unknown tensor kind %u", kind);
+    }
+    if (layer >= d->config.layers)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: layer %u out of range (%u layers)", layer, d->config.layers);
+    }
+    slot = d->Layer(layer, t);
+    return MUYO_OK;
+}
+}  // namespace
+
+extern "C" int muyo_decoder_tensor(MuyoDecoder* d, uint32_t kind, uint32_t layer, void** device_ptr, uint64_t* bytes)
+{
+    TensorSlot slot;
+    const int status = Lookup(d, kind, layer, slot);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    if (device_ptr != nullptr)
+    {
+        *device_ptr = d->arena + slot.offset;
+    }
+    if (bytes != nullptr)
+    {
+        *bytes = slot.bytes;
+    }
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_upload(MuyoDecoder* d, uint32_t kind, uint32_t layer, const void* host, uint64_t bytes)
+{
+    TensorSlot slot;
+    const int status = Lookup(d, kind, layer, slot);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    if (host == nullptr || bytes != slot.bytes)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_upload: %llu bytes given, tensor holds %zu",
+                    static_cast<unsigned long long>(bytes), slot.bytes);
+    }
+    MUYO_HIP_CHECK(hipMemcpyAsync(d->arena + slot.offset, host, bytes, hipMemcpyHostToDevice, d->stream));
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_download(MuyoDecoder* d, uint32_t kind, uint32_t layer, void* host, uint64_t bytes)
+{
+    TensorSlot slot;
+    const int status = Lookup(d, kind, layer, slot);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    if (host == nullptr || bytes != slot.bytes)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_download: %llu bytes given, tensor holds %zu",
+                    static_cast<unsigned long long>(bytes), slot.bytes);
+    }
+    MUYO_HIP_CHECK(hipDeviceSynchronize());
+    MUYO_HIP_CHECK(hipMemcpy(host, d->arena + slot.offset, bytes, hipMemcpyDeviceToHost));
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_fill_random(MuyoDecoder* d, uint64_t seed)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    int status = FillTensor(d, d->tokenEmbd, true, muyo_tensor_seed(seed, MUYO_TENSOR_TOKEN_EMBD, 0), 0.0, 0.02);
+    if (status == MUYO_OK)
+    {
+        status = FillTensor(d, d->outputNorm, false, muyo_tensor_seed(seed, MUYO_TENSOR_OUTPUT_NORM, 0), 1.0, 0.1);
+    }
+    static const struct
+    {
+        uint32_t kind;
+        LayerTensor tensor;
+        bool half;
+        double mean;
+        double stddev;
+    } kPlan[] = {
+        {MUYO_TENSOR_ATTN_NORM, kAttnNorm, false, 1.0, 0.1}, {MUYO_TENSOR_ATTN_QKV, kQkv, true, 0.0, 0.02},
+        {MUYO_TENSOR_ATTN_QKV_B, kQkvBias, false, 0.0, 0.02}, {MUYO_TENSOR_ATTN_OUTPUT, kOut, true, 0.0, 0.02},
+        {MUYO_TENSOR_FFN_NORM, kFfnNorm, false, 1.0, 0.1},   {MUYO_TENSOR_FFN_GATE, kGate, true, 0.0, 0.02},
+        {MUYO_TENSOR_FFN_UP, kUp, true, 0.0, 0.02},           {MUYO_TENSOR_FFN_DOWN, kDown, true, 0.0, 0.02},
+    };
+    for (uint32_t l = 0; l < d->config.layers && status == MUYO_OK; ++l)
+    {
+        for (const auto& p : kPlan)
+        {
+            status = FillTensor(d, d->Layer(l, p.tensor), p.half, muyo_tensor_seed(seed, p.kind, l), p.mean, p.stddev);
+            if (status != MUYO_OK)
+            {
+                break;
+            }
+        }
+        if (status == MUYO_OK)
+        {
+            const TensorSlot& kc = d->Layer(l, kKCache);
+            const TensorSlot& vc = d->Layer(l, kVCache);
+            if (hipMemsetAsync(d->arena + kc.offset, 0, kc.bytes, d->stream) != hipSuccess ||
+                hipMemsetAsync(d->arena + vc.offset, 0, vc.bytes, d->stream) != hipSuccess)
+            {
+                status = HipStatus(hipGetLastError(), "decoder_fill_random: clearing the caches");
+            }
+        }
+    }
+    if (status == MUYO_OK)
+    {
+        MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    }
+    return status;
+}
+
+extern "C" int muyo_decoder_fill_kv_random(MuyoDecoder* d, uint32_t positions, uint64_t seed)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    const MuyoQwen2Config& c = d->config;
+    if (positions > c.maxSeq)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_fill_kv_random: %u positions exceed maxSeq %u", positions, c.maxSeq);
+    }
+    const size_t rowBytes = static_cast<size_t>(c.headDim) * 2;
+    const size_t headBytes = rowBytes * c.maxSeq;
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        for (uint32_t kind : {static_cast<uint32_t>(MUYO_TENSOR_KCACHE), static_cast<uint32_t>(MUYO_TENSOR_VCACHE)})
+        {
+            const TensorSlot& slot = d->Layer(l, ToLayerTensor(kind));
+            // Whole tensor from the generator, then rows at or past `positions` cleared.
+            int status = FillTensor(d, slot, true, muyo_tensor_seed(seed, kind, l), 0.0, 1.0);
+            if (status != MUYO_OK)
+            {
+                return status;
+            }
+            const size_t tail = headBytes - rowBytes * positions;
+            if (tail > 0)
+            {
+                for (uint32_t g = 0; g < c.kvHeads; ++g)
+                {
+                    MUYO_HIP_CHECK(hipMemsetAsync(d->arena + slot.offset + g * headBytes + rowBytes * positions, 0,
+                                                  tail, d->stream));
+                }
+            }
+        }
+    }
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_t position, uint32_t count,
+                                           void* stream)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    const MuyoQwen2Config& c = d->config;
+    if (token < 0 || static_cast<uint32_t>(token) >= c.vocab)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: token %d outside [0, %u)", token, c.vocab);
+    }
+    if (position < 0 || static_cast<uint64_t>(position) + count > c.maxSeq)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: positions %d..%d exceed the cache (%u rows)", position,
+                    position + static_cast<int32_t>(count) - 1, c.maxSeq);
+    }
+    if (count > kIdsCapacity)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: at most %u steps per call", kIdsCapacity);
+    }
+    hipStream_t s = stream != nullptr ? AsStream(stream) : d->stream;
+    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(1), 0, s, d->state, token, position);
+    MUYO_HIP_CHECK(hipGetLastError());
+    for (uint32_t i = 0; i < count; ++i)
+    {
+        const int status = RunStep(d, s);
+        if (status != MUYO_OK)
+        {
+            return status;
+        }
+    }
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_generated_ids(MuyoDecoder* d, int32_t* ids, uint32_t count)
+{
+    if (d == nullptr || ids == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder_generated_ids: decoder and ids are required");
+    }
+    if (count > kIdsCapacity)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_generated_ids: at most %u ids", kIdsCapacity);
+    }
+    MUYO_HIP_CHECK(hipDeviceSynchronize());
+    MUYO_HIP_CHECK(hipMemcpy(ids, d->ids, static_cast<size_t>(count) * 4, hipMemcpyDeviceToHost));
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_generate(MuyoDecoder* d, int32_t token, int32_t position, uint32_t count, int32_t* ids,
+                                     void* stream)
+{
+    const int status = muyo_decoder_generate_async(d, token, position, count, stream);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    MUYO_HIP_CHECK(hipStreamSynchronize(stream != nullptr ? AsStream(stream) : d->stream));
+    return ids != nullptr ? muyo_decoder_generated_ids(d, ids, count) : MUYO_OK;
+}
+
+extern "C" int muyo_decoder_step(MuyoDecoder* d, int32_t token, int32_t position, int32_t* next_token)
+{
+    int32_t next = 0;
+    const int status = muyo_decoder_generate(d, token, position, 1, &next, nullptr);
+    if (status == MUYO_OK && next_token != nullptr)
+    {
+        *next_token = next;
+    }
+    return status;
+}
+
+extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
+{
+    return d == nullptr ? 0u : 2u + 5u * d->config.layers;
+}
+
+extern "C" int muyo_decoder_set_state(MuyoDecoder* d, int32_t token, int32_t position, void* stream)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    if (token < 0 || static_cast<uint32_t>(token) >= d->config.vocab || position < 0 ||
+        static_cast<uint32_t>(position) >= d->config.maxSeq)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_set_state: token %d / position %d out of range", token, position);
+    }
+    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(1), 0, stream != nullptr ? AsStream(stream) : d->stream, d->state,
+                       token, position);
+    return LaunchStatus("decoder_set_state");
+}
+
+extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint32_t layer, void* stream)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    const MuyoQwen2Config& c = d->config;
+    if (layer >= c.layers)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: layer %u out of range", layer);
+    }
+    hipStream_t s = stream != nullptr ? AsStream(stream) : d->stream;
+    const uint32_t qdim = c.heads * c.headDim;
+    hipError_t status;
+    switch (kernel)
+    {
+        case MUYO_KERNEL_EMBED:
+            status = LaunchEmbed(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->xA, c.hidden, c.vocab);
+            break;
+        case MUYO_KERNEL_QKV:
+            status = LaunchQkvRopeAppend(s, d->dims, d->xA, d->At<float>(d->Layer(layer, kAttnNorm)),
+                                         d->At<uint16_t>(d->Layer(layer, kQkv)),
+                                         d->At<float>(d->Layer(layer, kQkvBias)), d->state, d->q,
+                                         d->At<uint16_t>(d->Layer(layer, kKCache)),
+                                         d->At<uint16_t>(d->Layer(layer, kVCache)));
+            break;
+        case MUYO_KERNEL_ATTENTION:
+            status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(layer, kKCache)),
+                                     d->At<uint16_t>(d->Layer(layer, kVCache)), &d->state->position, d->attnOut,
+                                     d->scratch);
+            break;
+        case MUYO_KERNEL_O_PROJ:
+            status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(layer, kOut)), d->attnOut, d->xA, d->xMid,
+                                          c.hidden, qdim);
+            break;
+        case MUYO_KERNEL_GATE_UP:
+            status = LaunchGateUpSwiGlu(s, d->dims, d->xMid, d->At<float>(d->Layer(layer, kFfnNorm)),
+                                        d->At<uint16_t>(d->Layer(layer, kGate)), d->At<uint16_t>(d->Layer(layer, kUp)),
+                                        d->act);
+            break;
+        case MUYO_KERNEL_DOWN:
+            status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(layer, kDown)), d->act, d->xMid, d->xB,
+                                          c.hidden, c.feedForward);
+            break;
+        case MUYO_KERNEL_LM_HEAD:
+            status = LaunchLmHeadArgMax(s, d->dims, d->xA, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
+                                        d->At<float>(d->logits), d->state, d->ids, kIdsCapacity, d->scratch);
+            break;
+        default:
+            return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: unknown kernel %u", kernel);
+    }
+    return status == hipSuccess ? MUYO_OK : HipStatus(status, "decoder_enqueue_kernel");
+}

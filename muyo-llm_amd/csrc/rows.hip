@@ -1,0 +1,506 @@
+// Row reductions: rms_norm_f32, soft_max_f32, argmax_f32.
+//
+// Each row is owned by one wave64 (rms_norm, soft_max) or one workgroup (argmax over a long
+// row). Sums and maxima are reduced with cross-lane shuffles; rows that fit are kept in
+// registers between passes, longer rows are re-read (the re-read hits L2, so HBM traffic stays
+// one read and one write per element).
+#include <algorithm>
+#include <cfloat>
+
+#include "common.hpp"
+
+namespace muyo
+{
+namespace
+{
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+
+// ------------------------------------------------------------------------------------------------
+// rms_norm (shaders/llama/rms_norm.comp:53-151, do_multiply spec id 1).
+
+struct RmsArgs
+{
+    uint32_t ncols;
+    uint32_t nrows;      // dispatch x
+    uint32_t nchannels;  // dispatch y
+    uint32_t total;      // x * y * z
+    uint32_t nb01, nb02, nb03;
+    uint32_t ne10, ne11, ne12, ne13;
+    uint32_t nb11, nb12, nb13;
+    uint32_t aoff, boff, doff;
+    float eps;
+    uint32_t multiply;
+};
+
+template <typename WT>
+__device__ __forceinline__ float WeightAt(const WT* w, uint64_t i);
+
+template <>
+__device__ __forceinline__ float WeightAt<float>(const float* w, uint64_t i)
+{
+    return w[i];
+}
+
+template <>
+__device__ __forceinline__ float WeightAt<uint16_t>(const uint16_t* w, uint64_t i)
+{
+    return HalfBitsToFloat(w[i]);
+}
+
+__device__ __forceinline__ uint32_t ModIfNeeded(uint32_t a, uint32_t b) { return b == 0 ? 0 : a % b; }
+
+template <typename WT>
+__global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ a, const WT* __restrict__ w,
+                                                      float* __restrict__ d, RmsArgs p)
+{
+    const uint32_t flat = blockIdx.x * kWaves + threadIdx.x / kWave;
+    if (flat >= p.total)
+    {
+        return;  // whole wave exits together
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t row = flat % p.nrows;
+    const uint32_t channel = (flat / p.nrows) % p.nchannels;
+    const uint32_t sample = flat / (p.nrows * p.nchannels);
+    const uint64_t aOff = static_cast<uint64_t>(sample) * p.nb03 + static_cast<uint64_t>(channel) * p.nb02 +
+                          static_cast<uint64_t>(row) * p.nb01 + p.aoff;
+    const uint64_t bOff = static_cast<uint64_t>(ModIfNeeded(row, p.ne11)) * p.nb11 +
+                          static_cast<uint64_t>(ModIfNeeded(channel, p.ne12)) * p.nb12 +
+                          static_cast<uint64_t>(ModIfNeeded(sample, p.ne13)) * p.nb13 + p.boff;
+    const uint64_t dOff = static_cast<uint64_t>(flat) * p.ncols + p.doff;
+    const float* x = a + aOff;
+    float* y = d + dOff;
+
+    const bool vec = ((aOff | dOff | p.ncols) & 3u) == 0;
+    float sum = 0.0f;
+    if (vec)
+    {
+        const uint32_t n4 = p.ncols / 4;
+        for (uint32_t i = lane; i < n4; i += kWave)
+        {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            sum = fmaf(v.x, v.x, sum);
+            sum = fmaf(v.y, v.y, sum);
+            sum = fmaf(v.z, v.z, sum);
+            sum = fmaf(v.w, v.w, sum);
+        }
+    }
+    else
+    {
+        for (uint32_t i = lane; i < p.ncols; i += kWave)
+        {
+            sum = fmaf(x[i], x[i], sum);
+        }
+    }
+    sum = GroupSum<kWave>(sum);
+    const float scale = 1.0f / sqrtf(sum / static_cast<float>(p.ncols) + p.eps);
+
+    const bool wrap = p.ncols > p.ne10;
+    if (vec && !wrap && p.multiply && (bOff & 3u) == 0 && sizeof(WT) == 4)
+    {
+        const uint32_t n4 = p.ncols / 4;
+        const float4* w4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + bOff);
+        for (uint32_t i = lane; i < n4; i += kWave)
+        {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            const float4 g = w4[i];
+            float4 o;
+            o.x = scale * v.x * g.x;
+            o.y = scale * v.y * g.y;
+            o.z = scale * v.z * g.z;
+            o.w = scale * v.w * g.w;
+            reinterpret_cast<float4*>(y)[i] = o;
+        }
+        return;
+    }
+    for (uint32_t i = lane; i < p.ncols; i += kWave)
+    {
+        float value = scale * x[i];
+        if (p.multiply)
+        {
+            value *= WeightAt<WT>(w, bOff + (wrap ? i % p.ne10 : i));
+        }
+        y[i] = value;
+    }
+}
+
+template <typename WT>
+int LaunchRmsNorm(const char* name, const LlamaAddPushConstants* pc, uint32_t doMultiply, const float* a,
+                  const WT* b, float* d, uint32_t gx, uint32_t gy, uint32_t gz, void* stream)
+{
+    if (pc == nullptr || a == nullptr || d == nullptr || (doMultiply && b == nullptr))
+    {
+        return Fail(MUYO_E_NULL, "%s: push constants, A, D (and B when multiplying) are required", name);
+    }
+    if (gx == 0 || gy == 0 || gz == 0 || pc->ne00 == 0)
+    {
+        return MUYO_OK;
+    }
+    if (doMultiply && pc->ne10 == 0)
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: ne10 (weight length) must be >= 1", name);
+    }
+    const uint64_t total = static_cast<uint64_t>(gx) * gy * gz;
+    if (total > 0xFFFFFFFFull / kWave)
+    {
+        return Fail(MUYO_E_DISPATCH, "%s: dispatch too large", name);
+    }
+    RmsArgs p{};
+    p.ncols = pc->ne00;
+    p.nrows = gx;
+    p.nchannels = gy;
+    p.total = static_cast<uint32_t>(total);
+    p.nb01 = pc->nb01;
+    p.nb02 = pc->nb02;
+    p.nb03 = pc->nb03;
+    p.ne10 = pc->ne10;
+    p.ne11 = pc->ne11;
+    p.ne12 = pc->ne12;
+    p.ne13 = pc->ne13;
+    p.nb11 = pc->nb11;
+    p.nb12 = pc->nb12;
+    p.nb13 = pc->nb13;
+    p.aoff = pc->misalignOffsets >> 16;
+    p.boff = (pc->misalignOffsets >> 8) & 0xFFu;
+    p.doff = pc->misalignOffsets & 0xFFu;
+    p.eps = pc->param1;
+    p.multiply = doMultiply ? 1u : 0u;
+    hipLaunchKernelGGL((RmsNormRows<WT>), dim3(CeilDiv(total, kWaves)), dim3(kBlock), 0, AsStream(stream), a, b, d,
+                       p);
+    return LaunchStatus(name);
+}
+
+// ------------------------------------------------------------------------------------------------
+// soft_max (shaders/llama/soft_max.comp:41-172).
+
+struct SoftMaxArgs
+{
+    uint32_t kx, ky;
+    uint32_t ne01, ne02, ne12, ne13;
+    uint32_t nb11, nb12, nb13;
+    float scale, maxBias, m0, m1;
+    uint32_t nHeadLog2;
+    uint32_t nrowsX;
+    uint32_t hasSinks;
+    uint32_t gx, gy, gz;  // dispatch
+};
+
+/// Row index of dispatch slot `slot` (z*262144 + y*512 + x for the workgroup it stands for).
+__device__ __forceinline__ bool SlotRow(uint32_t slot, uint32_t gx, uint32_t gy, uint32_t& row)
+{
+    const uint32_t x = slot % gx;
+    const uint32_t y = (slot / gx) % gy;
+    const uint32_t z = slot / (gx * gy);
+    row = z * 262144u + y * 512u + x;
+    return true;
+}
+
+constexpr int kSoftMaxCache = 16;  // float4 per lane kept in registers (rows up to 4096)
+
+__global__ __launch_bounds__(kBlock) void SoftMaxRows(const float* __restrict__ xIn, const float* __restrict__ mask,
+                                                      const float* __restrict__ sinks, float* __restrict__ d,
+                                                      SoftMaxArgs p)
+{
+    const uint32_t slot = blockIdx.x * kWaves + threadIdx.x / kWave;
+    if (slot >= p.gx * p.gy * p.gz)
+    {
+        return;
+    }
+    uint32_t rowx;
+    SlotRow(slot, p.gx, p.gy, rowx);
+    if (rowx >= p.nrowsX)
+    {
+        return;
+    }
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t i03 = rowx / (p.ne01 * p.ne02);
+    const uint32_t i02 = (rowx - i03 * p.ne01 * p.ne02) / p.ne01;
+    const uint32_t i01 = rowx % p.ne01;
+    uint64_t rowyStart = 0;
+    if (p.ky > 0)
+    {
+        rowyStart = static_cast<uint64_t>(i01) * p.nb11 + static_cast<uint64_t>(i02 % p.ne12) * p.nb12 +
+                    static_cast<uint64_t>(i03 % p.ne13) * p.nb13;
+    }
+    float slope = 1.0f;
+    if (p.maxBias > 0.0f)
+    {
+        const uint32_t h = (rowx / p.ne01) % p.ne02;
+        const float base = h < p.nHeadLog2 ? p.m0 : p.m1;
+        const uint32_t e = h < p.nHeadLog2 ? h + 1 : 2 * (h - p.nHeadLog2) + 1;
+        slope = powf(base, static_cast<float>(e));
+    }
+    const float* x = xIn + static_cast<uint64_t>(rowx) * p.kx;
+    float* y = d + static_cast<uint64_t>(rowx) * p.kx;
+    const bool vec = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15u) == 0 &&
+                     (p.kx & 3u) == 0 && p.ky == 0;
+    const uint32_t n4 = p.kx / 4;
+
+    float maxValue = p.hasSinks ? sinks[i02] : -INFINITY;
+    if (vec && n4 <= static_cast<uint32_t>(kSoftMaxCache * kWave))
+    {
+        float4 cache[kSoftMaxCache];
+#pragma unroll
+        for (int k = 0; k < kSoftMaxCache; ++k)
+        {
+            const uint32_t i = lane + k * kWave;
+            if (i < n4)
+            {
+                float4 v = reinterpret_cast<const float4*>(x)[i];
+                v.x *= p.scale;
+                v.y *= p.scale;
+                v.z *= p.scale;
+                v.w *= p.scale;
+                cache[k] = v;
+                maxValue = fmaxf(maxValue, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+            }
+        }
+        maxValue = GroupMax<kWave>(maxValue);
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kSoftMaxCache; ++k)
+        {
+            const uint32_t i = lane + k * kWave;
+            if (i < n4)
+            {
+                float4 v = cache[k];
+                v.x = expf(v.x - maxValue);
+                v.y = expf(v.y - maxValue);
+                v.z = expf(v.z - maxValue);
+                v.w = expf(v.w - maxValue);
+                sum += (v.x + v.y) + (v.z + v.w);
+                cache[k] = v;
+            }
+        }
+        sum = GroupSum<kWave>(sum);
+        if (p.hasSinks)
+        {
+            sum += expf(sinks[i02] - maxValue);
+        }
+        const float rcp = 1.0f / sum;
+#pragma unroll
+        for (int k = 0; k < kSoftMaxCache; ++k)
+        {
+            const uint32_t i = lane + k * kWave;
+            if (i < n4)
+            {
+                float4 v = cache[k];
+                v.x *= rcp;
+                v.y *= rcp;
+                v.z *= rcp;
+                v.w *= rcp;
+                reinterpret_cast<float4*>(y)[i] = v;
+            }
+        }
+        return;
+    }
+
+    // General path: three passes over the row (re-reads hit cache).
+    for (uint32_t c = lane; c < p.kx; c += kWave)
+    {
+        const float b = p.ky > 0 ? mask[rowyStart + c] : 0.0f;
+        maxValue = fmaxf(maxValue, x[c] * p.scale + slope * b);
+    }
+    maxValue = GroupMax<kWave>(maxValue);
+    float sum = 0.0f;
+    for (uint32_t c = lane; c < p.kx; c += kWave)
+    {
+        const float b = p.ky > 0 ? mask[rowyStart + c] : 0.0f;
+        sum += expf(x[c] * p.scale + slope * b - maxValue);
+    }
+    sum = GroupSum<kWave>(sum);
+    if (p.hasSinks)
+    {
+        sum += expf(sinks[i02] - maxValue);
+    }
+    const float rcp = 1.0f / sum;
+    for (uint32_t c = lane; c < p.kx; c += kWave)
+    {
+        const float b = p.ky > 0 ? mask[rowyStart + c] : 0.0f;
+        y[c] = expf(x[c] * p.scale + slope * b - maxValue) * rcp;
+    }
+}
+
+/// Checks a (x, y, z) row dispatch of the `z*262144 + y*512 + x` form: with y or z in use, x and
+/// y must stay within 512 so distinct workgroups name distinct rows.
+int CheckRowDispatch(const char* name, uint32_t gx, uint32_t gy, uint32_t gz)
+{
+    if ((gy > 1 || gz > 1) && (gx > 512 || gy > 512))
+    {
+        return Fail(MUYO_E_DISPATCH, "%s: dispatch (%u, %u, %u) overlaps rows (x and y must be <= 512 when y or z > 1)",
+                    name, gx, gy, gz);
+    }
+    return MUYO_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// argmax (shaders/llama/argmax.comp:20-60), ties to the lowest index.
+
+struct ArgMaxArgs
+{
+    uint32_t kx, ky;
+    uint32_t gx, gy, gz;
+};
+
+__global__ __launch_bounds__(kBlock) void ArgMaxRows(const float* __restrict__ a, int32_t* __restrict__ d,
+                                                     ArgMaxArgs p)
+{
+    __shared__ float bestValue[kWaves];
+    __shared__ int32_t bestIndex[kWaves];
+    uint32_t row;
+    SlotRow(blockIdx.x, p.gx, p.gy, row);
+    if (row >= p.ky)
+    {
+        return;
+    }
+    const float* x = a + static_cast<uint64_t>(row) * p.kx;
+    float value = -INFINITY;
+    int32_t index = 0x7FFFFFFF;
+    const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+    uint32_t start = 0;
+    if (vec)
+    {
+        const uint32_t n4 = p.kx / 4;
+        for (uint32_t i = threadIdx.x; i < n4; i += kBlock)
+        {
+            const float4 v = reinterpret_cast<const float4*>(x)[i];
+            const int32_t base = static_cast<int32_t>(i * 4);
+            // Within one thread indices only grow, so strict '>' keeps the lowest on ties.
+            if (v.x > value) { value = v.x; index = base; }
+            if (v.y > value) { value = v.y; index = base + 1; }
+            if (v.z > value) { value = v.z; index = base + 2; }
+            if (v.w > value) { value = v.w; index = base + 3; }
+        }
+        start = n4 * 4;
+    }
+    for (uint32_t i = start + threadIdx.x; i < p.kx; i += kBlock)
+    {
+        if (x[i] > value)
+        {
+            value = x[i];
+            index = static_cast<int32_t>(i);
+        }
+    }
+    GroupArgMax<kWave>(value, index);
+    const int wave = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0)
+    {
+        bestValue[wave] = value;
+        bestIndex[wave] = index;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        float v = bestValue[0];
+        int32_t idx = bestIndex[0];
+        for (int w = 1; w < kWaves; ++w)
+        {
+            if (bestValue[w] > v || (bestValue[w] == v && bestIndex[w] < idx))
+            {
+                v = bestValue[w];
+                idx = bestIndex[w];
+            }
+        }
+        // An all -inf (or empty) row has no strict maximum: the host scan returns index 0.
+        d[row] = idx == 0x7FFFFFFF ? 0 : idx;
+    }
+}
+}  // namespace
+}  // namespace muyo
+
+using namespace muyo;
+
+extern "C" int muyo_rms_norm_f32(const LlamaAddPushConstants* pc, uint32_t do_multiply, const float* a,
+                                 const float* b, float* d, float* /*partial_sums*/, uint32_t dispatch_x,
+                                 uint32_t dispatch_y, uint32_t dispatch_z, void* stream)
+{
+    return LaunchRmsNorm<float>("rms_norm_f32", pc, do_multiply, a, b, d, dispatch_x, dispatch_y, dispatch_z, stream);
+}
+
+extern "C" int muyo_rms_norm_f32_f16w(const LlamaAddPushConstants* pc, uint32_t do_multiply, const float* a,
+                                      const void* b, float* d, float* /*partial_sums*/, uint32_t dispatch_x,
+                                      uint32_t dispatch_y, uint32_t dispatch_z, void* stream)
+{
+    return LaunchRmsNorm<uint16_t>("rms_norm_f32_f16w", pc, do_multiply, a, static_cast<const uint16_t*>(b), d,
+                                   dispatch_x, dispatch_y, dispatch_z, stream);
+}
+
+extern "C" int muyo_soft_max_f32(const LlamaSoftMaxPushConstants* pc, const float* x, const float* mask,
+                                 const float* sinks, float* d, uint32_t dispatch_x, uint32_t dispatch_y,
+                                 uint32_t dispatch_z, void* stream)
+{
+    const char* name = "soft_max_f32";
+    if (pc == nullptr || x == nullptr || d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: push constants, X and D are required", name);
+    }
+    if ((pc->KY > 0 && mask == nullptr) || (pc->hasSinks && sinks == nullptr))
+    {
+        return Fail(MUYO_E_NULL, "%s: the mask (KY > 0) or sinks (hasSinks) binding is NULL", name);
+    }
+    if (dispatch_x == 0 || dispatch_y == 0 || dispatch_z == 0 || pc->KX == 0)
+    {
+        return MUYO_OK;
+    }
+    if (pc->ne01 == 0 || pc->ne02 == 0 || (pc->KY > 0 && (pc->ne12 == 0 || pc->ne13 == 0)))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: ne01, ne02 (and ne12, ne13 with a mask) must be >= 1", name);
+    }
+    const int check = CheckRowDispatch(name, dispatch_x, dispatch_y, dispatch_z);
+    if (check != MUYO_OK)
+    {
+        return check;
+    }
+    SoftMaxArgs p{};
+    p.kx = pc->KX;
+    p.ky = pc->KY;
+    p.ne01 = pc->ne01;
+    p.ne02 = pc->ne02;
+    p.ne12 = pc->ne12;
+    p.ne13 = pc->ne13;
+    p.nb11 = pc->nb11;
+    p.nb12 = pc->nb12;
+    p.nb13 = pc->nb13;
+    p.scale = pc->scale;
+    p.maxBias = pc->maxBias;
+    p.m0 = pc->m0;
+    p.m1 = pc->m1;
+    p.nHeadLog2 = pc->nHeadLog2;
+    p.nrowsX = pc->nrowsX;
+    p.hasSinks = pc->hasSinks;
+    p.gx = dispatch_x;
+    p.gy = dispatch_y;
+    p.gz = dispatch_z;
+    const uint64_t slots = static_cast<uint64_t>(dispatch_x) * dispatch_y * dispatch_z;
+    hipLaunchKernelGGL(SoftMaxRows, dim3(CeilDiv(slots, kWaves)), dim3(kBlock), 0, AsStream(stream), x, mask, sinks, d,
+                       p);
+    return LaunchStatus(name);
+}
+
+extern "C" int muyo_argmax_f32(const LlamaGenericHeadPushConstants* pc, const float* a, int32_t* d,
+                               uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream)
+{
+    const char* name = "argmax_f32";
+    if (pc == nullptr || a == nullptr || d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: push constants, A and D are required", name);
+    }
+    if (dispatch_x == 0 || dispatch_y == 0 || dispatch_z == 0)
+    {
+        return MUYO_OK;
+    }
+    const int check = CheckRowDispatch(name, dispatch_x, dispatch_y, dispatch_z);
+    if (check != MUYO_OK)
+    {
+        return check;
+    }
+    const uint64_t slots = static_cast<uint64_t>(dispatch_x) * dispatch_y * dispatch_z;
+    if (slots > 0x7FFFFFFFull)
+    {
+        return Fail(MUYO_E_DISPATCH, "%s: dispatch too large", name);
+    }
+    ArgMaxArgs p{pc->KX, pc->KY, dispatch_x, dispatch_y, dispatch_z};
+    hipLaunchKernelGGL(ArgMaxRows, dim3(static_cast<uint32_t>(slots)), dim3(kBlock), 0, AsStream(stream), a, d, p);
+    return LaunchStatus(name);
+}

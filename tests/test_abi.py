@@ -1,0 +1,105 @@
+"""The C-ABI boundary, checked on the CPU: the library loads, exports every symbol the header
+declares, the contract structs have the reference's sizes, and argument errors are reported
+before anything touches a GPU."""
+import ctypes
+import pathlib
+import re
+import subprocess
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "muyo_hip.h"
+CONTRACTS = ROOT / "include" / "muyo" / "LlamaContracts.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(muyo_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(mh):
+    lib_path = mh.LIB_PATH
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib_path)], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r" T (muyo_\w+)", out.stdout))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+    lib = mh.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name)
+    assert set(mh.exported_symbols()) == set(declared_symbols())
+
+
+def test_header_compiles_as_c_and_sizes_match(tmp_path, mh):
+    """The contract header is plain C (for cgo/JNI/ctypes) and its sizes are the reference's."""
+    probe = tmp_path / "probe.c"
+    probe.write_text(
+        '#include <stdio.h>\n#include "muyo_hip.h"\nint main(void){printf("%zu %zu %zu %zu %zu %zu %zu\\n",'
+        "sizeof(LlamaAddPushConstants), sizeof(LlamaMatVecPushConstants), sizeof(LlamaRopePushConstants),"
+        "sizeof(LlamaGluPushConstants), sizeof(LlamaGenericHeadPushConstants), sizeof(LlamaSoftMaxPushConstants),"
+        "sizeof(LlamaCopyPushConstants)); return 0;}\n")
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(probe), "-o", str(exe)],
+                   check=True)
+    sizes = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    # src/LlamaContracts.h:41,87,156,202,235,277 and src/FullModel.cpp:364.
+    assert sizes == [29 * 4, 13 * 4, 30 * 4, 27 * 4, 6 * 4, 17 * 4, 30 * 4]
+    for cls, words in mh.CONTRACT_WORDS.items():
+        assert ctypes.sizeof(cls) == 4 * words
+
+
+def test_fastdiv_magic_is_exact_division(mh):
+    """init_fastdiv_values (src/Swiglu.cpp:46-54): (mulhi(n, mp) + n) >> L == n / d for n < 2^31."""
+    for d in (1, 2, 3, 7, 64, 600, 896, 2048, 4864, 131072, 4096 * 4864):
+        mp, shift = mh.init_fastdiv(d)
+        for n in (0, 1, d - 1, d, d + 1, 12345, 2**20 + 7, 2**31 - 1):
+            assert ((((n * mp) >> 32) + n) >> shift) == n // d, (d, n)
+
+
+def test_value_column_packing_order(mh):
+    """src/FullModel.cpp:398-408: shifts packed outermost divisor first (Finding F12)."""
+    pc = mh.value_column_push_constants(128, 64, 2048, 5)
+    _, l012 = mh.init_fastdiv(64 * 2048)
+    _, l0 = mh.init_fastdiv(2048)
+    assert pc.ne1_Ls & 0xFF == l012 and (pc.ne1_Ls >> 16) & 0xFF == l0
+    assert pc.misalignOffsets == 5
+
+
+def test_argument_errors_without_a_gpu(mh):
+    lib = mh.load()
+    pc = mh.mat_vec_push_constants(8, 8)
+    assert lib.muyo_mul_mat_vec_f16_f32_f32(mh.ref(pc), None, None, None, None, None, None, 8, 1, 1, 0) == mh.MUYO_E_NULL
+    assert b"required" in lib.muyo_last_error()
+    assert lib.muyo_rms_norm_f32(None, 1, None, None, None, None, 1, 1, 1, 0) == mh.MUYO_E_NULL
+    glu = mh.glu_push_constants(600)
+    glu.ne2_012mp ^= 1
+    fake = ctypes.c_void_p(16)
+    assert lib.muyo_swiglu_f32(mh.ref(glu), fake, fake, fake, 1, 2, 1, 0) == mh.MUYO_E_CONTRACT
+    glu = mh.glu_push_constants(600)
+    assert lib.muyo_swiglu_f32(mh.ref(glu), fake, fake, fake, 2, 2, 1, 0) == mh.MUYO_E_DISPATCH
+    cfg = mh.qwen2_config(1, 896, 4864, 14, 2, 96, 1000, 64)
+    handle = ctypes.c_void_p()
+    assert lib.muyo_decoder_create(mh.ref(cfg), ctypes.byref(handle)) == mh.MUYO_E_UNSUPPORTED
+    assert not handle.value
+
+
+def test_step_bytes_match_the_published_derivation():
+    """BASELINE.md section 2 (derived, not published): 987,922,432 B of fp16 weights at the
+    0.5B shape and 12,288 B of fp16 KV per position."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    import muyo_hip as mh
+
+    s = dict(mh.QWEN25_05B)
+    b1, b2 = bench.step_bytes(s, 1024), bench.step_bytes(s, 1025)
+    assert b2 - b1 == 12_288
+    weights = s["layers"] * 2 * (1152 * 896 + 896 * 896 + 2 * 4864 * 896 + 896 * 4864) + 2 * 151936 * 896
+    assert weights == 987_922_432
+    # + KV rows 0..1024 (12.6 MB) + f32 activations, biases, norms and logits (2.6 MB)
+    assert 987_922_432 + 12_288 * 1025 < b1 < 987_922_432 + 12_288 * 1025 + 3_000_000
+    s7 = dict(mh.QWEN25_7B)
+    w7 = s7["layers"] * 2 * (4608 * 3584 + 3584 * 3584 + 3 * 18944 * 3584) + 2 * 152064 * 3584
+    assert w7 == 14_140_571_648

@@ -1,0 +1,133 @@
+"""Decode-step parity on the GPU: the fused, graph-replayed decoder against the CPU oracle.
+
+Both sides draw every weight and the pre-filled KV cache from the same portable generator, so
+they start from identical bits (checked). The bar: greedy token ids identical over 32 steps on
+the Qwen2.5-0.5B shape, per-step logits within 1e-3 (mixed form), cache rows bit-exact in place.
+"""
+import numpy as np
+import pytest
+
+from conftest import close, worst
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, max_seq=256)
+
+
+def make_pair(mh, orc, shape, seed, kv_positions=0, kv_seed=7):
+    cfg = mh.qwen2_config(**shape)
+    dec = mh.Decoder(cfg)
+    dec.fill_random(seed)
+    model = orc.Model(**shape)
+    model.fill_random(seed)
+    if kv_positions:
+        dec.fill_kv_random(kv_positions, kv_seed)
+        model.fill_kv_random(kv_positions, kv_seed)
+    return dec, model
+
+
+def download(dec, kind, layer, like):
+    out = np.empty_like(like)
+    dec.download(kind, layer, out)
+    return out
+
+
+def test_decoder_weights_match_oracle_bits(mh, gpu, orc):
+    dec, model = make_pair(mh, orc, SMALL, seed=3, kv_positions=100, kv_seed=4)
+    with dec:
+        for (kind, layer), arr in model.t.items():
+            assert np.array_equal(download(dec, kind, layer, arr), arr), (kind, layer)
+
+
+def test_decoder_small_steps_match_oracle(mh, gpu, orc):
+    dec, model = make_pair(mh, orc, SMALL, seed=11, kv_positions=30, kv_seed=12)
+    with dec:
+        token = 17
+        for i in range(12):
+            pos = 30 + i
+            got = dec.step(token, pos)
+            want, logits, (top1, top2) = model.step(token, pos)
+            gpu_logits = download(dec, "LOGITS", 0, np.empty(SMALL["vocab"], np.float32))
+            assert close(gpu_logits, logits, 1e-3) == 0, f"step {i}"
+            assert worst(gpu_logits, logits) < 1e-4
+            assert got == want, f"step {i}: gpu {got} oracle {want} (margin {top1 - top2:.3g})"
+            token = got
+        # The appended cache rows hold the same fp16 values (bit-exact up to last-bit rounding).
+        for layer in range(SMALL["layers"]):
+            for kind in ("KCACHE", "VCACHE"):
+                ref = model.t[(kind, layer)]
+                got_cache = download(dec, kind, layer, ref)
+                assert np.array_equal(got_cache[:, :30], ref[:, :30])
+                assert np.array_equal(got_cache[:, 42:], ref[:, 42:])
+                diff = np.abs(orc.half_to_float(got_cache[:, 30:42]) - orc.half_to_float(ref[:, 30:42]))
+                assert diff.max() <= 2e-3 * (1 + np.abs(orc.half_to_float(ref[:, 30:42])).max())
+
+
+def test_decoder_graph_replay_matches_eager_steps(mh, gpu, orc):
+    """generate() (one hipGraph launch per token, ids fed back on the device) == step-by-step."""
+    cfg = mh.qwen2_config(**SMALL)
+    with mh.Decoder(cfg) as dec:
+        dec.fill_random(21)
+        dec.fill_kv_random(10, 22)
+        ids = dec.generate(5, 10, 20)
+        dec.fill_kv_random(10, 22)
+        again = dec.generate(5, 10, 20)
+        dec.fill_kv_random(10, 22)
+        token, stepped = 5, []
+        for i in range(20):
+            token = dec.step(token, 10 + i)
+            stepped.append(token)
+    assert ids == again == stepped
+
+
+def test_decoder_05b_greedy_32_steps(mh, gpu, orc, capsys):
+    """Qwen2.5-0.5B shape, KV pre-filled to p = 128, 32 greedy tokens from a seeded random id."""
+    orc.set_threads(16)
+    shape = mh.QWEN25_05B
+    dec, model = make_pair(mh, orc, shape, seed=2026, kv_positions=128, kv_seed=2027)
+    start = int(orc.uniform_f32(1, 99)[0] * 0.5 * shape["vocab"] + 0.5 * shape["vocab"])
+    with dec:
+        ids = dec.generate(start, 128, 32)
+    want, margins = model.greedy(start, 128, 32)
+    with capsys.disabled():
+        print(f"\n[0.5b greedy] start {start} ids {ids[:8]}... min top1-top2 margin {min(margins):.3g}")
+    assert ids == want
+
+
+@pytest.mark.parametrize("position", [1024, 2047])
+def test_decoder_05b_single_step_long_cache(mh, gpu, orc, position):
+    orc.set_threads(16)
+    shape = mh.QWEN25_05B
+    dec, model = make_pair(mh, orc, shape, seed=7, kv_positions=position, kv_seed=8)
+    with dec:
+        got = dec.step(151643, position)
+        want, logits, _ = model.step(151643, position)
+        gpu_logits = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+    assert close(gpu_logits, logits, 1e-3) == 0
+    assert got == want
+
+
+def test_decoder_7b_shape_two_layers(mh, gpu, orc):
+    """Qwen2.5-7B widths (hidden 3584, ffn 18944, 28/4 heads, head_dim 128, vocab 152064), 2 layers."""
+    orc.set_threads(16)
+    shape = dict(mh.QWEN25_7B, layers=2)
+    dec, model = make_pair(mh, orc, shape, seed=70, kv_positions=2040, kv_seed=71)
+    with dec:
+        ids = dec.generate(1000, 2040, 8)
+        gpu_logits = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+    token, want = 1000, []
+    for i in range(8):
+        token, logits, _ = model.step(token, 2040 + i)
+        want.append(token)
+    assert ids == want
+    assert close(gpu_logits, logits, 1e-3) == 0  # the last step, at cache row 2047
+
+
+def test_decoder_rejects_out_of_range(mh, gpu):
+    cfg = mh.qwen2_config(**SMALL)
+    with mh.Decoder(cfg) as dec:
+        lib = mh.load()
+        assert lib.muyo_decoder_generate_async(dec.handle, SMALL["vocab"], 0, 1, 0) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_generate_async(dec.handle, 0, SMALL["max_seq"] - 2, 3, 0) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_generate_async(dec.handle, 0, -1, 1, 0) == mh.MUYO_E_RANGE
+        assert dec.launches_per_step() == 2 + 5 * SMALL["layers"]
