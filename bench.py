@@ -220,7 +220,7 @@ def main() -> int:
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "bytes_per_step": total_bytes // args.steps,
         "roofline": {
-            "kernel": "FusedMatVec<16,1,rms_norm,LmHeadEpi> (final norm + tied LM head 151936x896 + argmax)",
+            "kernel": "FusedMatVec<16,8,1,NormStage,LmHeadEpi> (final norm + tied LM head 151936x896 + argmax)",
             "bound": "hbm",
             "achieved": round(lm_gbs, 1),
             "peak": HBM_PEAK_GBS,

@@ -265,13 +265,15 @@ uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* decoder);
 /* Kernels of one step, for per-kernel timing and profiling. */
 enum
 {
-    MUYO_KERNEL_EMBED = 0,     /* token row -> hidden f32 */
+    MUYO_KERNEL_EMBED = 0,     /* previous step's greedy id, step bookkeeping, token row -> hidden f32
+                                  (advances the state) */
     MUYO_KERNEL_QKV = 1,       /* rms_norm + q|k|v GEMV + bias + rope + cache append */
-    MUYO_KERNEL_ATTENTION = 2, /* GQA attention over cache rows 0..position */
-    MUYO_KERNEL_O_PROJ = 3,    /* o_proj GEMV + residual */
+    MUYO_KERNEL_ATTENTION = 2, /* GQA attention over cache rows 0..position (chunk partials, and their
+                                  merge when o_proj does not merge them) */
+    MUYO_KERNEL_O_PROJ = 3,    /* [attention merge +] o_proj GEMV + residual */
     MUYO_KERNEL_GATE_UP = 4,   /* rms_norm + gate/up GEMV + swiglu */
     MUYO_KERNEL_DOWN = 5,      /* down GEMV + residual */
-    MUYO_KERNEL_LM_HEAD = 6    /* rms_norm + tied LM head + greedy argmax (advances the state) */
+    MUYO_KERNEL_LM_HEAD = 6    /* rms_norm + tied LM head + per-workgroup argmax partials */
 };
 
 /* Set the device-side token and position (stream-ordered) without running a step. */

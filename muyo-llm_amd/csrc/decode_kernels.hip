@@ -1,26 +1,29 @@
 // Fused decode-step kernels for gfx950.
 //
-// One Qwen2 layer is five launches (the reference records 18 nodes per layer,
-// src/FullModel.cpp:227-453):
-//   1. QkvRopeAppend : rms_norm prologue -> fused q|k|v GEMV + bias -> NeoX rope of q and k ->
-//                      q to a buffer, k and v appended as fp16 at the position's cache row
-//   2. Attention     : split over 64-key chunks of the fp16 cache; each block computes scores,
-//                      a chunk-local softmax and P.V for the whole GQA group of its KV head;
-//                      the last block to finish merges the chunks (flash-decoding)
-//   3. MatVecResidual: o_proj GEMV + residual add
-//   4. GateUpSwiGlu  : rms_norm prologue -> gate and up GEMV rows -> silu(g)*u
-//   5. MatVecResidual: down GEMV + residual add
-// and the step ends with LmHeadArgMax: final rms_norm -> tied LM head -> logits + greedy
-// argmax (ties to the lowest index) -> next token, position and step advanced on the device.
+// One step (the reference records 18 nodes per layer, src/FullModel.cpp:227-498):
+//   BeginStep      : greedy id of the previous step from the LM head's per-workgroup partials,
+//                    step bookkeeping (position, generated-id ring), embedding row -> f32 x
+//   per layer:
+//   QkvRopeAppend  : rms_norm prologue -> fused q|k|v GEMV + bias -> NeoX rope of q and k ->
+//                    q to a buffer, k and v appended as fp16 at the position's cache row
+//   Attention      : one workgroup per (256-key chunk, kv head); 64-key tiles of the fp16 cache
+//                    staged in LDS (next tile prefetched), online softmax, P.V for the whole GQA
+//                    group; chunk partials (max, sum, P.V) to scratch
+//   [AttentionMerge: combine the chunk partials, when o_proj does not do it itself]
+//   OProj          : [merge prologue] o_proj GEMV + residual add
+//   GateUpSwiGlu   : rms_norm prologue -> gate and up GEMV rows -> silu(g)*u
+//   Down           : down GEMV + residual add
+//   LmHeadArgMax   : final rms_norm prologue -> tied LM head -> logits + per-workgroup argmax
 //
-// GEMV core: the activation is staged once per workgroup in LDS (normalised in place when the
-// op has an rms_norm prologue); a wave64 splits into segments of LPR lanes, each segment
-// streaming one fp16 weight row in 16-byte chunks; segment sums reduce across lanes; the
-// segments of one "unit" (1 or 2 rows) meet in the unit's leader lane for the epilogue.
+// GEMV core (gemv_core.hpp): the activation is staged once per workgroup in LDS; a wave64
+// splits into segments of LPR lanes, each segment streaming one fp16 weight row in 16-byte
+// chunks with all of a lane's loads in flight at once; the first batch is requested before the
+// activation is staged and the next row's batch before the current row's reduction.
 #include <algorithm>
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
+#include "gemv_core.hpp"
 
 namespace muyo
 {
@@ -29,128 +32,183 @@ namespace
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr uint32_t kMaxLds = 160 * 1024;
+constexpr int kStageVec = 8;           // float4 per thread per staging round (rows <= 8192 floats)
+constexpr int kMaxGroup = 8;           // query heads per kv head
+constexpr uint32_t kBlocksPerCu = 4;   // GEMV grid cap: enough waves in flight, no second round
+constexpr uint32_t kMergeChunks = 8;   // chunks the o_proj prologue merges (max_seq <= 2048)
+constexpr uint32_t kMergeItems = 4;    // q channels per thread in that prologue (q dim <= 1024)
 
-__device__ __forceinline__ uint32_t SplitSlot(uint32_t i, uint32_t nchunks)
+uint32_t GemvBlockCap()
 {
-    const uint32_t c = i >> 3;
-    const uint32_t r = i & 7u;
-    return r < 4 ? c * 4 + r : (nchunks + c) * 4 + (r - 4);
-}
-
-/// Stage n floats (n % 8 == 0) into LDS in the split chunk layout; with kNorm, scale them by
-/// rsqrt(mean(x^2) + eps) and the norm weight (order: (scale * x) * w, as rms_norm.comp:122).
-template <bool kNorm>
-__device__ __forceinline__ void StageActivation(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
-                                                float eps, float4* xs)
-{
-    __shared__ float partial[kWaves];
-    float* flat = reinterpret_cast<float*>(xs);
-    const uint32_t nchunks = n / 8;
-    float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < n; i += kBlock)
+    static uint32_t cap = 0;
+    if (cap == 0)
     {
-        const float v = x[i];
-        flat[SplitSlot(i, nchunks)] = v;
-        if (kNorm)
+        int device = 0;
+        int cus = 0;
+        if (hipGetDevice(&device) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
         {
-            ss = fmaf(v, v, ss);
+            cus = 256;
         }
+        cap = static_cast<uint32_t>(cus) * kBlocksPerCu;
     }
-    if (kNorm)
-    {
-        ss = GroupSum<kWave>(ss);
-        if ((threadIdx.x & (kWave - 1)) == 0)
-        {
-            partial[threadIdx.x / kWave] = ss;
-        }
-        __syncthreads();
-        const float total = (partial[0] + partial[1]) + (partial[2] + partial[3]);
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
-        for (uint32_t i = threadIdx.x; i < n; i += kBlock)
-        {
-            const uint32_t slot = SplitSlot(i, nchunks);
-            flat[slot] = (scale * flat[slot]) * w[i];
-        }
-    }
-    __syncthreads();
+    return cap;
 }
 
-__device__ __forceinline__ float Dot8(const uint16_t* __restrict__ row, uint32_t chunk, const float4* __restrict__ lo,
-                                      const float4* __restrict__ hi, float acc)
-{
-    float w[8];
-    LoadHalf8(row + static_cast<uint64_t>(chunk) * 8, w);
-    const float4 x0 = lo[chunk];
-    const float4 x1 = hi[chunk];
-    acc = fmaf(w[0], x0.x, acc);
-    acc = fmaf(w[1], x0.y, acc);
-    acc = fmaf(w[2], x0.z, acc);
-    acc = fmaf(w[3], x0.w, acc);
-    acc = fmaf(w[4], x1.x, acc);
-    acc = fmaf(w[5], x1.y, acc);
-    acc = fmaf(w[6], x1.z, acc);
-    acc = fmaf(w[7], x1.w, acc);
-    return acc;
-}
+// ------------------------------------------------------------------------------------------------
+// Activation staging policies (each fills the LDS split layout and ends synchronised).
 
-/// This lane's share of one row's dot product (not yet reduced across the segment).
-template <int kLpr>
-__device__ __forceinline__ float SegmentPartial(const uint16_t* __restrict__ row, uint32_t nchunks, uint32_t lir,
-                                                const float4* __restrict__ lo, const float4* __restrict__ hi)
+struct PlainStage
 {
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    uint32_t c = lir;
-    for (; c + 3 * kLpr < nchunks; c += 4 * kLpr)
-    {
-        a0 = Dot8(row, c, lo, hi, a0);
-        a1 = Dot8(row, c + kLpr, lo, hi, a1);
-        a2 = Dot8(row, c + 2 * kLpr, lo, hi, a2);
-        a3 = Dot8(row, c + 3 * kLpr, lo, hi, a3);
-    }
-    for (; c < nchunks; c += kLpr)
-    {
-        a0 = Dot8(row, c, lo, hi, a0);
-    }
-    return (a0 + a1) + (a2 + a3);
-}
-
-struct NoTail
-{
+    const float* x;
+    __device__ void Run(float4* xs, uint32_t n) const { StageSplit<kBlock, kStageVec, false>(x, nullptr, n, 0.0f, xs); }
 };
 
-/// Generic fused GEMV: units of kNr rows, an epilogue per unit, an optional block tail.
-template <int kLpr, int kNr, bool kNorm, class Epi>
-__global__ __launch_bounds__(kBlock) void FusedMatVec(const float* __restrict__ x, const float* __restrict__ normW,
-                                                      uint32_t cols, float eps, Epi epi)
+struct NormStage
+{
+    const float* x;
+    const float* w;
+    float eps;
+    __device__ void Run(float4* xs, uint32_t n) const { StageSplit<kBlock, kStageVec, true>(x, w, n, eps, xs); }
+};
+
+/// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
+/// sum_c e^(m_c - M) l_c (flash-decoding's combine).
+struct MergeStage
+{
+    const int32_t* position;
+    const float* attnMax;
+    const float* attnSum;
+    const float* attnAcc;
+    uint32_t heads, group, headDim, maxChunks;
+
+    __device__ void Run(float4* xs, uint32_t n) const
+    {
+        __shared__ float chunkMax[kBlock];
+        __shared__ float chunkSum[kBlock];
+        __shared__ float weight[kBlock];
+        // Positions outside the cache are rejected on the host; clamping keeps every read in bounds.
+        const uint32_t pos = static_cast<uint32_t>(max(*position, 0));
+        const uint32_t chunks = min((pos + kAttnChunk) / kAttnChunk, maxChunks);
+        const uint32_t nchunks = n / 8;
+        // Per-(head, chunk) max and sum, and this thread's accumulators, all requested at once.
+        if (threadIdx.x < heads * chunks)
+        {
+            const uint32_t h = threadIdx.x / chunks;
+            const uint32_t c = threadIdx.x % chunks;
+            const uint64_t slot = (static_cast<uint64_t>(h / group) * maxChunks + c) * group + h % group;
+            chunkMax[threadIdx.x] = attnMax[slot];
+            chunkSum[threadIdx.x] = attnSum[slot];
+        }
+        float acc[kMergeItems][kMergeChunks];
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k)
+        {
+            const uint32_t item = min(threadIdx.x + k * kBlock, n - 1);
+            const uint32_t h = item / headDim;
+            const uint32_t d = item % headDim;
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeChunks; ++c)
+            {
+                const uint32_t cc = min(c, chunks - 1);
+                const uint64_t slot = (static_cast<uint64_t>(h / group) * maxChunks + cc) * group + h % group;
+                acc[k][c] = attnAcc[slot * headDim + d];
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x < heads)
+        {
+            const uint32_t h = threadIdx.x;
+            float m = -INFINITY;
+            for (uint32_t c = 0; c < chunks; ++c)
+            {
+                m = fmaxf(m, chunkMax[h * chunks + c]);
+            }
+            float den = 0.0f;
+            for (uint32_t c = 0; c < chunks; ++c)
+            {
+                const float e = expf(chunkMax[h * chunks + c] - m);
+                weight[h * chunks + c] = e;
+                den = fmaf(e, chunkSum[h * chunks + c], den);
+            }
+            const float inv = 1.0f / den;
+            for (uint32_t c = 0; c < chunks; ++c)
+            {
+                weight[h * chunks + c] *= inv;
+            }
+        }
+        __syncthreads();
+        float* flat = reinterpret_cast<float*>(xs);
+#pragma unroll
+        for (uint32_t k = 0; k < kMergeItems; ++k)
+        {
+            const uint32_t item = threadIdx.x + k * kBlock;
+            if (item < n)
+            {
+                const uint32_t h = item / headDim;
+                float out = 0.0f;
+#pragma unroll
+                for (uint32_t c = 0; c < kMergeChunks; ++c)
+                {
+                    if (c < chunks)
+                    {
+                        out = fmaf(weight[h * chunks + c], acc[k][c], out);
+                    }
+                }
+                flat[SplitSlot(item, nchunks)] = out;
+            }
+        }
+        __syncthreads();
+    }
+};
+
+// ------------------------------------------------------------------------------------------------
+// Fused GEMV: units of kNr rows, a staging policy, an epilogue per unit, an optional block tail.
+
+template <int kLpr, int kCpl, int kNr, class Stage, class Epi>
+__global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage, Epi epi)
 {
     extern __shared__ float4 xs[];
     const uint32_t nchunks = cols / 8;
-    StageActivation<kNorm>(x, normW, cols, eps, xs);
-    const float4* lo = xs;
-    const float4* hi = xs + nchunks;
-
     constexpr int kSegs = kWave / kLpr;
     constexpr int kUnits = kSegs / kNr;
     static_assert(kUnits >= 1, "a wave must hold at least one unit");
     const int lane = threadIdx.x & (kWave - 1);
     const int segment = lane / kLpr;
-    const int lir = lane % kLpr;
+    const uint32_t lir = lane % kLpr;
     const int unitInWave = segment / kNr;
     const int part = segment % kNr;
     const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const uint32_t waves = gridDim.x * kWaves;
+    const uint32_t stride = gridDim.x * kWaves * kUnits;
     const uint32_t units = epi.Units();
+
+    // Weights do not depend on the activation: start streaming them before it is staged.
+    uint32_t first = wave * kUnits;
+    half8 w[kCpl];
+    if (first + unitInWave < units)
+    {
+        LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
+    }
+    stage.Run(xs, cols);
+    const float4* lo = xs;
+    const float4* hi = xs + nchunks;
 
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
-    for (uint32_t first = wave * kUnits; first < units; first += waves * kUnits)
+    for (; first < units; first += stride)
     {
         const uint32_t unit = first + unitInWave;
-        const bool valid = unit < units && segment < kUnits * kNr;
+        const bool valid = unit < units;
         float dot = 0.0f;
         if (valid)
         {
-            dot = SegmentPartial<kLpr>(epi.Row(unit, part), nchunks, lir, lo, hi);
+            dot = RowDot<kLpr, kCpl>(epi.Row(unit, part), nchunks, lir, w, lo, hi);
+        }
+        // The next unit's first batch goes out before this unit's reduction and epilogue.
+        const uint32_t next = first + stride + unitInWave;
+        if (next < units)
+        {
+            LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, w);
         }
         dot = GroupSum<kLpr>(dot);
         float sums[kNr];
@@ -183,6 +241,7 @@ struct QkvEpi
 
     __device__ uint32_t Units() const { return (heads + 2 * kvHeads) * headDim / 2; }
 
+    /// Rope units pair rows (j, j + hd/2) of one q or k head; value units pair adjacent rows.
     __device__ uint32_t RowOf(uint32_t unit, int part) const
     {
         const uint32_t half = headDim / 2;
@@ -208,6 +267,7 @@ struct QkvEpi
         const float s1 = s[1] + bias[RowOf(unit, 1)];
         if (unit < ropeUnits)
         {
+            // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
             const uint32_t head = unit / half;
             const uint32_t j = unit % half;
             const float theta = static_cast<float>(pos) * powf(thetaScale, static_cast<float>(j));
@@ -229,7 +289,7 @@ struct QkvEpi
         }
         else if (pos >= 0 && static_cast<uint32_t>(pos) < maxSeq)
         {
-            const uint32_t channel = 2 * (unit - ropeUnits);  // within kvHeads*headDim
+            const uint32_t channel = 2 * (unit - ropeUnits);  // within kvHeads * headDim
             const uint32_t g = channel / headDim;
             const uint64_t base = (static_cast<uint64_t>(g) * maxSeq + pos) * headDim + channel % headDim;
             vcache[base] = FloatToHalfBits(s0);
@@ -267,22 +327,49 @@ struct GateUpEpi
     }
     __device__ void Finish(uint32_t unit, const float* s, float&, int32_t&) const
     {
-        act[unit] = s[0] / (1.0f + expf(-s[0])) * s[1];
+        act[unit] = s[0] / (1.0f + expf(-s[0])) * s[1];  // swiglu.comp's op
     }
     __device__ void Tail(float, int32_t) const {}
 };
+
+/// Better (value, index) under "larger value, then lower index" (the host greedy scan's rule).
+__device__ __forceinline__ bool Better(float v, int32_t i, float bestV, int32_t bestI)
+{
+    return v > bestV || (v == bestV && i < bestI);
+}
+
+/// Reduce (value, index) over a 256-thread block; the result lands in thread 0.
+__device__ __forceinline__ void BlockArgMax(float& value, int32_t& index)
+{
+    __shared__ float waveValue[kWaves];
+    __shared__ int32_t waveIndex[kWaves];
+    GroupArgMax<kWave>(value, index);
+    if ((threadIdx.x & (kWave - 1)) == 0)
+    {
+        waveValue[threadIdx.x / kWave] = value;
+        waveIndex[threadIdx.x / kWave] = index;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+    {
+        for (int k = 1; k < kWaves; ++k)
+        {
+            if (Better(waveValue[k], waveIndex[k], value, index))
+            {
+                value = waveValue[k];
+                index = waveIndex[k];
+            }
+        }
+    }
+}
 
 struct LmHeadEpi
 {
     const uint16_t* table;
     float* logits;
-    DecodeState* state;
-    int32_t* ids;
-    uint32_t idsCap;
-    uint32_t rows, cols;
     float* argValue;
     int32_t* argIndex;
-    uint32_t* argCount;
+    uint32_t rows, cols;
 
     __device__ uint32_t Units() const { return rows; }
     __device__ const uint16_t* Row(uint32_t unit, int) const { return table + static_cast<uint64_t>(unit) * cols; }
@@ -296,83 +383,13 @@ struct LmHeadEpi
             bestIndex = static_cast<int32_t>(unit);
         }
     }
-
     __device__ void Tail(float value, int32_t index) const
     {
-        __shared__ float waveValue[kWaves];
-        __shared__ int32_t waveIndex[kWaves];
-        __shared__ int isLast;
-        GroupArgMax<kWave>(value, index);
-        const int lane = threadIdx.x & (kWave - 1);
-        const int wave = threadIdx.x / kWave;
-        if (lane == 0)
-        {
-            waveValue[wave] = value;
-            waveIndex[wave] = index;
-        }
-        __syncthreads();
+        BlockArgMax(value, index);
         if (threadIdx.x == 0)
         {
-            float v = waveValue[0];
-            int32_t i = waveIndex[0];
-            for (int k = 1; k < kWaves; ++k)
-            {
-                if (waveValue[k] > v || (waveValue[k] == v && waveIndex[k] < i))
-                {
-                    v = waveValue[k];
-                    i = waveIndex[k];
-                }
-            }
-            argValue[blockIdx.x] = v;
-            argIndex[blockIdx.x] = i;
-            __threadfence();
-            isLast = atomicAdd(argCount, 1u) == gridDim.x - 1;
-        }
-        __syncthreads();
-        if (!isLast)
-        {
-            return;
-        }
-        __threadfence();
-        float v = -INFINITY;
-        int32_t i = 0x7FFFFFFF;
-        for (uint32_t b = threadIdx.x; b < gridDim.x; b += kBlock)
-        {
-            const float bv = __builtin_nontemporal_load(argValue + b);
-            const int32_t bi = __builtin_nontemporal_load(argIndex + b);
-            if (bv > v || (bv == v && bi < i))
-            {
-                v = bv;
-                i = bi;
-            }
-        }
-        GroupArgMax<kWave>(v, i);
-        __syncthreads();
-        if (lane == 0)
-        {
-            waveValue[wave] = v;
-            waveIndex[wave] = i;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0)
-        {
-            v = waveValue[0];
-            i = waveIndex[0];
-            for (int k = 1; k < kWaves; ++k)
-            {
-                if (waveValue[k] > v || (waveValue[k] == v && waveIndex[k] < i))
-                {
-                    v = waveValue[k];
-                    i = waveIndex[k];
-                }
-            }
-            const int32_t next = i == 0x7FFFFFFF ? 0 : i;
-            const uint32_t step = state->step;
-            ids[step % idsCap] = next;
-            state->token = next;
-            state->position = state->position + 1;
-            state->step = step + 1;
-            *argCount = 0;
+            argValue[blockIdx.x] = value;
+            argIndex[blockIdx.x] = index;
         }
     }
 };
@@ -380,26 +397,23 @@ struct LmHeadEpi
 // ------------------------------------------------------------------------------------------------
 // Launch helpers for the fused GEMV.
 
-int PickLpr(uint32_t nchunks, int nr)
+template <int kLpr, int kCpl, int kNr, class Stage, class Epi>
+hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
+                        const Stage& stage, const Epi& epi, uint32_t* blocksOut)
 {
-    int lpr = nchunks <= 64 ? 8 : (nchunks <= 128 ? 16 : (nchunks <= 256 ? 32 : 64));
-    if (nr == 2 && lpr > 32)
+    const uint32_t unitsPerBlock = kWaves * ((kWave / kLpr) / kNr);
+    const uint32_t blocks = std::max(1u, std::min(CeilDiv(units, unitsPerBlock), blockCap));
+    if (blocksOut != nullptr)
     {
-        lpr = 32;
+        *blocksOut = blocks;
+        return hipSuccess;
     }
-    return lpr;
-}
-
-template <int kLpr, int kNr, bool kNorm, class Epi>
-hipError_t LaunchFusedT(hipStream_t s, uint32_t blocks, size_t lds, const float* x, const float* normW,
-                        uint32_t cols, float eps, const Epi& epi)
-{
     // Opt in to more than the default 64 KB of dynamic LDS only when a launch needs it.
     static size_t configured = 64 * 1024;
     if (lds > configured)
     {
         const hipError_t status =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&FusedMatVec<kLpr, kNr, kNorm, Epi>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&FusedMatVec<kLpr, kCpl, kNr, Stage, Epi>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
         if (status != hipSuccess)
         {
@@ -407,49 +421,114 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t blocks, size_t lds, const float*
         }
         configured = lds;
     }
-    hipLaunchKernelGGL((FusedMatVec<kLpr, kNr, kNorm, Epi>), dim3(blocks), dim3(kBlock), lds, s, x, normW, cols, eps,
+    hipLaunchKernelGGL((FusedMatVec<kLpr, kCpl, kNr, Stage, Epi>), dim3(blocks), dim3(kBlock), lds, s, cols, stage,
                        epi);
     return hipGetLastError();
 }
 
-template <int kNr, bool kNorm, class Epi>
-hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, const float* x, const float* normW,
-                       uint32_t cols, float eps, const Epi& epi)
+/// Launches (or, with blocksOut, only sizes) the fused GEMV for a row of `cols` fp16 weights.
+template <int kNr, class Stage, class Epi>
+hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_t cols, const Stage& stage,
+                       const Epi& epi, uint32_t* blocksOut = nullptr)
 {
     if (cols % 8 != 0 || static_cast<size_t>(cols) * sizeof(float) > kMaxLds)
     {
         return hipErrorInvalidValue;
     }
-    const uint32_t nchunks = cols / 8;
-    const int lpr = PickLpr(nchunks, kNr);
-    const uint32_t unitsPerBlock = kWaves * ((kWave / lpr) / kNr);
-    const uint32_t blocks = std::max(1u, std::min(CeilDiv(units, unitsPerBlock), blockCap));
+    const RowShape shape = PickRowShape(cols / 8, kNr);
     const size_t lds = static_cast<size_t>(cols) * sizeof(float);
-    switch (lpr)
-    {
-        case 8:
-            return LaunchFusedT<8, kNr, kNorm>(s, blocks, lds, x, normW, cols, eps, epi);
-        case 16:
-            return LaunchFusedT<16, kNr, kNorm>(s, blocks, lds, x, normW, cols, eps, epi);
-        case 32:
-            return LaunchFusedT<32, kNr, kNorm>(s, blocks, lds, x, normW, cols, eps, epi);
-        default:
-            if constexpr (kNr == 1)
-            {
-                return LaunchFusedT<64, kNr, kNorm>(s, blocks, lds, x, normW, cols, eps, epi);
-            }
-            return hipErrorInvalidValue;
+#define MUYO_FUSED_CASE(L, C)                                                                                \
+    if (shape.lpr == L && shape.cpl == C)                                                                    \
+    {                                                                                                        \
+        return LaunchFusedT<L, C, kNr, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);    \
     }
+    MUYO_FUSED_CASE(8, 8)
+    MUYO_FUSED_CASE(16, 8)
+    MUYO_FUSED_CASE(32, 8)
+    MUYO_FUSED_CASE(32, 16)
+    if constexpr (kNr == 1)
+    {
+        MUYO_FUSED_CASE(64, 8)
+        MUYO_FUSED_CASE(64, 12)
+        MUYO_FUSED_CASE(64, 16)
+    }
+#undef MUYO_FUSED_CASE
+    return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------------------------------------------
-// Embedding gather.
+// Step bookkeeping.
 
-__global__ __launch_bounds__(kBlock) void EmbedKernel(const uint16_t* __restrict__ table,
-                                                      const DecodeState* __restrict__ state, float* __restrict__ x,
-                                                      uint32_t hidden, uint32_t vocab)
+/// Greedy id of the previous step: the best of the LM head's per-workgroup partials.
+__device__ __forceinline__ int32_t ReduceArgMaxPartials(const float* __restrict__ argValue,
+                                                        const int32_t* __restrict__ argIndex, uint32_t argBlocks)
 {
-    const int32_t token = state->token;
+    __shared__ int32_t token;
+    float v = -INFINITY;
+    int32_t i = 0x7FFFFFFF;
+    constexpr int kPerThread = kArgMaxBlocks / kBlock;
+    float values[kPerThread];
+    int32_t indices[kPerThread];
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        const uint32_t b = min(threadIdx.x + k * kBlock, argBlocks - 1);
+        values[k] = argValue[b];
+        indices[k] = argIndex[b];
+    }
+#pragma unroll
+    for (int k = 0; k < kPerThread; ++k)
+    {
+        if (threadIdx.x + k * kBlock < argBlocks && Better(values[k], indices[k], v, i))
+        {
+            v = values[k];
+            i = indices[k];
+        }
+    }
+    BlockArgMax(v, i);
+    if (threadIdx.x == 0)
+    {
+        token = i == 0x7FFFFFFF ? 0 : i;  // no finite logit at all: the host scan returns 0
+    }
+    __syncthreads();
+    return token;
+}
+
+__global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, float* argValue, int32_t* argIndex,
+                                                         int32_t token, int32_t position, uint32_t argBlocks)
+{
+    for (uint32_t b = threadIdx.x; b < argBlocks; b += kBlock)
+    {
+        argValue[b] = b == 0 ? 0.0f : -INFINITY;
+        argIndex[b] = b == 0 ? token : 0x7FFFFFFF;
+    }
+    if (threadIdx.x == 0)
+    {
+        state->token = token;
+        state->position = position;
+        state->start = position;
+        state->step = 0;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __restrict__ table, DecodeState* state,
+                                                          const float* __restrict__ argValue,
+                                                          const int32_t* __restrict__ argIndex, uint32_t argBlocks,
+                                                          float* __restrict__ x, int32_t* __restrict__ ids,
+                                                          uint32_t idsCap, uint32_t hidden, uint32_t vocab)
+{
+    const int32_t token = ReduceArgMaxPartials(argValue, argIndex, argBlocks);
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+    {
+        const uint32_t step = state->step;
+        if (step > 0)
+        {
+            ids[(step - 1) % idsCap] = token;
+        }
+        state->token = token;
+        state->position = state->start + static_cast<int32_t>(step);
+        state->step = step + 1;
+    }
     const bool ok = token >= 0 && static_cast<uint32_t>(token) < vocab;
     const uint16_t* row = table + static_cast<uint64_t>(ok ? token : 0) * hidden;
     for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < hidden; i += gridDim.x * kBlock)
@@ -458,28 +537,45 @@ __global__ __launch_bounds__(kBlock) void EmbedKernel(const uint16_t* __restrict
     }
 }
 
-// ------------------------------------------------------------------------------------------------
-// Attention over the fp16 cache, one block per (64-key chunk, kv head).
+__global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, const float* __restrict__ argValue,
+                                                         const int32_t* __restrict__ argIndex, uint32_t argBlocks,
+                                                         int32_t* __restrict__ ids, uint32_t idsCap)
+{
+    const int32_t token = ReduceArgMaxPartials(argValue, argIndex, argBlocks);
+    if (threadIdx.x == 0)
+    {
+        const uint32_t step = state->step;
+        if (step > 0)
+        {
+            ids[(step - 1) % idsCap] = token;
+        }
+        state->token = token;
+    }
+}
 
-constexpr int kMaxGroup = 8;
+// ------------------------------------------------------------------------------------------------
+// Attention over the fp16 cache: one workgroup per (256-key chunk, kv head).
 
 template <int kHd>
 __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc,
-                                                         const int32_t* __restrict__ position, float* __restrict__ out,
-                                                         uint32_t group, uint32_t maxSeq, float scale,
-                                                         DecodeScratch sc)
+                                                         const int32_t* __restrict__ position, uint32_t group,
+                                                         uint32_t maxSeq, float scale, DecodeScratch sc)
 {
-    constexpr int kLpk = kHd / 8;             // lanes per key row (16 bytes each)
+    constexpr int kRowChunks = kHd / 8;                  // 16-byte pieces per cache row
+    constexpr int kPieces = kAttnTile * kRowChunks;      // per K (or V) tile
+    constexpr int kPiecesPerThread = kPieces / kBlock;   // 2 (hd 64) or 4 (hd 128)
+    constexpr int kLpk = kRowChunks;                     // lanes per key in the score pass
     constexpr int kKeysPerWave = kWave / kLpk;
-    constexpr int kKeysPerPass = kKeysPerWave * kWaves;
-    constexpr int kKeyGroups = kBlock / kHd;  // P.V: threads per column
-    __shared__ float qs[kMaxGroup * kHd];
-    __shared__ float scores[kMaxGroup][kAttnChunk];
-    __shared__ float chunkMax[kMaxGroup];
-    __shared__ float chunkSum[kMaxGroup];
-    __shared__ float reduce[kKeyGroups > 1 ? (kKeyGroups - 1) * kMaxGroup * kHd : 1];
-    __shared__ int isLast;
+    constexpr int kItems = kMaxGroup * kHd / kBlock;     // (head, channel) items per thread
+    static_assert(kPieces % kBlock == 0 && (kMaxGroup * kHd) % kBlock == 0, "tile must split over the block");
+    __shared__ half8 kS[kPieces];
+    __shared__ half8 vS[kPieces];
+    __shared__ __align__(16) float qs[kMaxGroup * kHd];
+    __shared__ float probs[kMaxGroup][kAttnTile];
+    __shared__ float runMax[kMaxGroup];
+    __shared__ float runSum[kMaxGroup];
+    __shared__ float rescale[kMaxGroup];
 
     const int32_t pos = *position;
     if (pos < 0 || static_cast<uint32_t>(pos) >= maxSeq)
@@ -494,185 +590,195 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         return;
     }
     const uint32_t g = blockIdx.y;
-    const uint32_t maxChunks = gridDim.x;
-    const uint32_t j0 = chunk * kAttnChunk;
-    const uint32_t jn = min(kAttnChunk, keys - j0);
+    const uint32_t c0 = chunk * kAttnChunk;
+    const uint32_t cn = min(kAttnChunk, keys - c0);
+    const uint32_t tiles = (cn + kAttnTile - 1) / kAttnTile;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
+    const half8* kBase = reinterpret_cast<const half8*>(kc + static_cast<uint64_t>(g) * maxSeq * kHd);
+    const half8* vBase = reinterpret_cast<const half8*>(vc + static_cast<uint64_t>(g) * maxSeq * kHd);
 
+    // Tile loads: rows past the last key read the last key instead (always in bounds); their
+    // probabilities are zero, so they add nothing.
+    half8 kr[kPiecesPerThread];
+    half8 vr[kPiecesPerThread];
+    auto loadTile = [&](uint32_t t) {
+#pragma unroll
+        for (int i = 0; i < kPiecesPerThread; ++i)
+        {
+            const uint32_t piece = threadIdx.x + i * kBlock;
+            const uint32_t key = min(c0 + t * kAttnTile + piece / kRowChunks, keys - 1);
+            const uint64_t offset = static_cast<uint64_t>(key) * kRowChunks + piece % kRowChunks;
+            kr[i] = kBase[offset];
+            vr[i] = vBase[offset];
+        }
+    };
+    loadTile(0);
     for (uint32_t i = threadIdx.x; i < group * kHd; i += kBlock)
     {
         qs[i] = q[static_cast<uint64_t>(g) * group * kHd + i];
     }
-    __syncthreads();
-
-    // Scores: kLpk lanes per key, every lane dots its 8 channels with all heads of the group.
-    const uint16_t* kBase = kc + (static_cast<uint64_t>(g) * maxSeq + j0) * kHd;
-    const int l8 = lane % kLpk;
-    for (uint32_t jb = 0; jb < jn; jb += kKeysPerPass)
+    if (threadIdx.x < kMaxGroup)
     {
-        const uint32_t j = jb + wave * kKeysPerWave + lane / kLpk;
-        float part[kMaxGroup];
+        runMax[threadIdx.x] = -INFINITY;
+        runSum[threadIdx.x] = 0.0f;
+    }
+    float acc[kItems];
 #pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
+    for (int k = 0; k < kItems; ++k)
+    {
+        acc[k] = 0.0f;
+    }
+    const uint16_t* vFlat = reinterpret_cast<const uint16_t*>(vS);
+    const int slice = lane % kLpk;
+
+    for (uint32_t t = 0; t < tiles; ++t)
+    {
+        const uint32_t tn = min(kAttnTile, cn - t * kAttnTile);
+        __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+        for (int i = 0; i < kPiecesPerThread; ++i)
         {
-            part[h] = 0.0f;
+            kS[threadIdx.x + i * kBlock] = kr[i];
+            vS[threadIdx.x + i * kBlock] = vr[i];
         }
-        if (j < jn)
+        __syncthreads();
+        if (t + 1 < tiles)
         {
-            float k8[8];
-            LoadHalf8(kBase + static_cast<uint64_t>(j) * kHd + l8 * 8, k8);
+            loadTile(t + 1);  // in flight while this tile is computed
+        }
+
+        // Scores: kLpk lanes per key, each lane one 16-byte slice against every head of the group.
+        for (uint32_t jb = wave * kKeysPerWave; jb < kAttnTile; jb += kWaves * kKeysPerWave)
+        {
+            const uint32_t j = jb + lane / kLpk;
+            const half8 k8 = kS[j * kRowChunks + slice];
 #pragma unroll
             for (int h = 0; h < kMaxGroup; ++h)
             {
+                float part = 0.0f;
                 if (h < static_cast<int>(group))
                 {
-                    const float* qh = qs + h * kHd + l8 * 8;
-                    float acc = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                    {
-                        acc = fmaf(qh[e], k8[e], acc);
-                    }
-                    part[h] = acc;
+                    const float4 q0 = *reinterpret_cast<const float4*>(qs + h * kHd + slice * 8);
+                    const float4 q1 = *reinterpret_cast<const float4*>(qs + h * kHd + slice * 8 + 4);
+                    part = DotChunk(k8, q0, q1, 0.0f);
                 }
-            }
-        }
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-        {
-            part[h] = GroupSum<kLpk>(part[h]);
-        }
-        if (j < jn && l8 == 0)
-        {
-            for (uint32_t h = 0; h < group; ++h)
-            {
-                scores[h][j] = part[h] * scale;
-            }
-        }
-    }
-    __syncthreads();
-
-    // Chunk-local softmax numerators, one wave per head.
-    for (uint32_t h = wave; h < group; h += kWaves)
-    {
-        float m = -INFINITY;
-        for (uint32_t j = lane; j < jn; j += kWave)
-        {
-            m = fmaxf(m, scores[h][j]);
-        }
-        m = GroupMax<kWave>(m);
-        float l = 0.0f;
-        for (uint32_t j = lane; j < jn; j += kWave)
-        {
-            const float p = expf(scores[h][j] - m);
-            scores[h][j] = p;
-            l += p;
-        }
-        l = GroupSum<kWave>(l);
-        if (lane == 0)
-        {
-            chunkMax[h] = m;
-            chunkSum[h] = l;
-        }
-    }
-    __syncthreads();
-
-    // P.V: thread (keyGroup, column) sums keys keyGroup, keyGroup + kKeyGroups, ...
-    const uint32_t column = threadIdx.x % kHd;
-    const uint32_t keyGroup = threadIdx.x / kHd;
-    const uint16_t* vBase = vc + (static_cast<uint64_t>(g) * maxSeq + j0) * kHd;
-    float acc[kMaxGroup];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-    {
-        acc[h] = 0.0f;
-    }
-    for (uint32_t j = keyGroup; j < jn; j += kKeyGroups)
-    {
-        const float v = HalfBitsToFloat(vBase[static_cast<uint64_t>(j) * kHd + column]);
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-        {
-            if (h < static_cast<int>(group))
-            {
-                acc[h] = fmaf(scores[h][j], v, acc[h]);
-            }
-        }
-    }
-    if (kKeyGroups > 1)
-    {
-        if (keyGroup > 0)
-        {
-            for (uint32_t h = 0; h < group; ++h)
-            {
-                reduce[((keyGroup - 1) * kMaxGroup + h) * kHd + column] = acc[h];
+                part = GroupSum<kLpk>(part);
+                if (slice == 0 && h < static_cast<int>(group))
+                {
+                    probs[h][j] = j < tn ? part * scale : -INFINITY;
+                }
             }
         }
         __syncthreads();
-        if (keyGroup == 0)
+
+        // Online softmax, one wave per head (a tile is 64 keys: one per lane).
+        for (uint32_t h = wave; h < group; h += kWaves)
         {
-            for (int kg = 1; kg < kKeyGroups; ++kg)
+            const float v = probs[h][lane];
+            const float tileMax = GroupMax<kWave>(v);
+            const float oldMax = runMax[h];
+            const float newMax = fmaxf(oldMax, tileMax);
+            const float p = lane < static_cast<int>(tn) ? expf(v - newMax) : 0.0f;
+            const float tileSum = GroupSum<kWave>(p);
+            probs[h][lane] = p;
+            if (lane == 0)
             {
-                for (uint32_t h = 0; h < group; ++h)
+                const float factor = expf(oldMax - newMax);  // 0 for the first tile
+                rescale[h] = factor;
+                runSum[h] = runSum[h] * factor + tileSum;
+                runMax[h] = newMax;
+            }
+        }
+        __syncthreads();
+
+        // P.V: thread item (head, channel), accumulators rescaled to the running max.
+#pragma unroll
+        for (int k = 0; k < kItems; ++k)
+        {
+            const uint32_t item = threadIdx.x + k * kBlock;
+            if (item < group * kHd)
+            {
+                const uint32_t h = item / kHd;
+                const uint32_t d = item % kHd;
+                float a0 = acc[k] * rescale[h];
+                float a1 = 0.0f;
+                uint32_t j = 0;
+                for (; j + 1 < tn; j += 2)
                 {
-                    acc[h] += reduce[((kg - 1) * kMaxGroup + h) * kHd + column];
+                    a0 = fmaf(probs[h][j], HalfBitsToFloat(vFlat[j * kHd + d]), a0);
+                    a1 = fmaf(probs[h][j + 1], HalfBitsToFloat(vFlat[(j + 1) * kHd + d]), a1);
                 }
+                if (j < tn)
+                {
+                    a0 = fmaf(probs[h][j], HalfBitsToFloat(vFlat[j * kHd + d]), a0);
+                }
+                acc[k] = a0 + a1;
             }
         }
     }
 
-    // Publish this chunk's partials.
-    const uint64_t slot = static_cast<uint64_t>(g) * maxChunks + chunk;
-    if (keyGroup == 0)
+    // Publish this chunk's partials (read after the kernel boundary).
+    const uint64_t slot = static_cast<uint64_t>(g) * gridDim.x + chunk;
+#pragma unroll
+    for (int k = 0; k < kItems; ++k)
     {
-        for (uint32_t h = 0; h < group; ++h)
+        const uint32_t item = threadIdx.x + k * kBlock;
+        if (item < group * kHd)
         {
-            sc.attnAcc[(slot * group + h) * kHd + column] = acc[h];
+            sc.attnAcc[(slot * group + item / kHd) * kHd + item % kHd] = acc[k];
         }
     }
     if (threadIdx.x < group)
     {
-        sc.attnMax[slot * group + threadIdx.x] = chunkMax[threadIdx.x];
-        sc.attnSum[slot * group + threadIdx.x] = chunkSum[threadIdx.x];
+        sc.attnMax[slot * group + threadIdx.x] = runMax[threadIdx.x];
+        sc.attnSum[slot * group + threadIdx.x] = runSum[threadIdx.x];
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0)
-    {
-        isLast = atomicAdd(sc.attnCount + g, 1u) == chunks - 1;
-    }
-    __syncthreads();
-    if (!isLast)
-    {
-        return;
-    }
-    __threadfence();
+}
 
-    // Merge the chunks of this kv head: out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.
-    for (uint32_t item = threadIdx.x; item < group * kHd; item += kBlock)
+/// Combine the chunk partials of every query head: one workgroup per head, a thread per channel.
+__global__ __launch_bounds__(128) void AttentionMergeKernel(const int32_t* __restrict__ position, DecodeScratch sc,
+                                                            float* __restrict__ out, uint32_t group, uint32_t headDim,
+                                                            uint32_t maxChunks)
+{
+    const uint32_t h = blockIdx.x;
+    const uint32_t g = h / group;
+    const uint32_t hh = h % group;
+    const uint32_t pos = static_cast<uint32_t>(max(*position, 0));
+    const uint32_t chunks = min((pos + kAttnChunk) / kAttnChunk, maxChunks);
+    float m[kMaxAttnChunks];
+    float l[kMaxAttnChunks];
+    float a[kMaxAttnChunks];
+    for (uint32_t d = threadIdx.x; d < headDim; d += blockDim.x)
     {
-        const uint32_t h = item / kHd;
-        const uint32_t d = item % kHd;
-        const uint64_t base = static_cast<uint64_t>(g) * maxChunks;
-        float m = -INFINITY;
-        for (uint32_t c = 0; c < chunks; ++c)
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
         {
-            m = fmaxf(m, __builtin_nontemporal_load(sc.attnMax + (base + c) * group + h));
+            const uint32_t cc = min(c, chunks - 1);
+            const uint64_t slot = (static_cast<uint64_t>(g) * maxChunks + cc) * group + hh;
+            m[c] = sc.attnMax[slot];
+            l[c] = sc.attnSum[slot];
+            a[c] = sc.attnAcc[slot * headDim + d];
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+        {
+            mx = c < chunks ? fmaxf(mx, m[c]) : mx;
         }
         float num = 0.0f;
         float den = 0.0f;
-        for (uint32_t c = 0; c < chunks; ++c)
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
         {
-            const float e = expf(__builtin_nontemporal_load(sc.attnMax + (base + c) * group + h) - m);
-            num = fmaf(e, __builtin_nontemporal_load(sc.attnAcc + ((base + c) * group + h) * kHd + d), num);
-            den = fmaf(e, __builtin_nontemporal_load(sc.attnSum + (base + c) * group + h), den);
+            if (c < chunks)
+            {
+                const float e = expf(m[c] - mx);
+                num = fmaf(e, a[c], num);
+                den = fmaf(e, l[c], den);
+            }
         }
-        out[(static_cast<uint64_t>(g) * group + h) * kHd + d] = num / den;
-    }
-    if (threadIdx.x == 0)
-    {
-        sc.attnCount[g] = 0;
+        out[static_cast<uint64_t>(h) * headDim + d] = num / den;
     }
 }
 
@@ -729,10 +835,45 @@ __global__ __launch_bounds__(kBlock) void RopeAppendKernel(const float* __restri
 }
 }  // namespace
 
-hipError_t LaunchEmbed(hipStream_t s, const uint16_t* table, const DecodeState* state, float* x, uint32_t hidden,
-                       uint32_t vocab)
+uint32_t LmHeadBlocks(const DecodeDims& dims)
 {
-    hipLaunchKernelGGL(EmbedKernel, dim3(CeilDiv(hidden, kBlock)), dim3(kBlock), 0, s, table, state, x, hidden, vocab);
+    uint32_t blocks = 0;
+    LmHeadEpi epi{};
+    epi.rows = dims.vocab;
+    (void)LaunchFused<1>(nullptr, dims.vocab, std::min(kArgMaxBlocks, GemvBlockCap()), dims.hidden,
+                         NormStage{nullptr, nullptr, 0.0f}, epi, &blocks);
+    return blocks;
+}
+
+bool MergeInOProj(const DecodeDims& dims)
+{
+    const uint32_t qdim = dims.heads * dims.headDim;
+    return AttnChunks(dims.maxSeq) <= kMergeChunks && qdim <= kMergeItems * kBlock &&
+           dims.heads * AttnChunks(dims.maxSeq) <= static_cast<uint32_t>(kBlock);
+}
+
+hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
+                          int32_t position, uint32_t argBlocks)
+{
+    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex, token,
+                       position, argBlocks);
+    return hipGetLastError();
+}
+
+hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* state, const DecodeScratch& scratch,
+                           uint32_t argBlocks, float* x, int32_t* ids, uint32_t idsCap, uint32_t hidden,
+                           uint32_t vocab)
+{
+    hipLaunchKernelGGL(BeginStepKernel, dim3(CeilDiv(hidden, kBlock)), dim3(kBlock), 0, s, table, state,
+                       scratch.argValue, scratch.argIndex, argBlocks, x, ids, idsCap, hidden, vocab);
+    return hipGetLastError();
+}
+
+hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, uint32_t argBlocks,
+                          int32_t* ids, uint32_t idsCap)
+{
+    hipLaunchKernelGGL(FinalizeKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex,
+                       argBlocks, ids, idsCap);
     return hipGetLastError();
 }
 
@@ -743,14 +884,15 @@ hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const floa
     QkvEpi epi{wqkv,        bias,       state,         qOut,         kcache, vcache, dims.hidden, dims.heads,
                dims.kvHeads, dims.headDim, dims.maxSeq, dims.thetaScale};
     const uint32_t units = (dims.heads + 2 * dims.kvHeads) * dims.headDim / 2;
-    return LaunchFused<2, true>(s, units, 4096, x, normW, dims.hidden, dims.eps, epi);
+    return LaunchFused<2>(s, units, GemvBlockCap(), dims.hidden, NormStage{x, normW, dims.eps}, epi);
 }
 
 hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
-                           const uint16_t* vcache, const int32_t* position, float* out, const DecodeScratch& scratch)
+                           const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch)
 {
     const uint32_t group = dims.heads / dims.kvHeads;
-    if (group == 0 || group > static_cast<uint32_t>(kMaxGroup) || dims.heads % dims.kvHeads != 0)
+    if (group == 0 || group > static_cast<uint32_t>(kMaxGroup) || dims.heads % dims.kvHeads != 0 ||
+        AttnChunks(dims.maxSeq) > kMaxAttnChunks)
     {
         return hipErrorInvalidValue;
     }
@@ -758,11 +900,11 @@ hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q
     switch (dims.headDim)
     {
         case 64:
-            hipLaunchKernelGGL(AttentionChunk<64>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, out, group,
+            hipLaunchKernelGGL(AttentionChunk<64>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group,
                                dims.maxSeq, dims.attnScale, scratch);
             break;
         case 128:
-            hipLaunchKernelGGL(AttentionChunk<128>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, out, group,
+            hipLaunchKernelGGL(AttentionChunk<128>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group,
                                dims.maxSeq, dims.attnScale, scratch);
             break;
         default:
@@ -771,27 +913,44 @@ hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q
     return hipGetLastError();
 }
 
+hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const int32_t* position,
+                                const DecodeScratch& scratch, float* out)
+{
+    hipLaunchKernelGGL(AttentionMergeKernel, dim3(dims.heads), dim3(std::min<uint32_t>(dims.headDim, 128)), 0, s,
+                       position, scratch, out, dims.heads / dims.kvHeads, dims.headDim, AttnChunks(dims.maxSeq));
+    return hipGetLastError();
+}
+
+hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const int32_t* position,
+                             const DecodeScratch& scratch, const float* residual, float* out)
+{
+    const uint32_t qdim = dims.heads * dims.headDim;
+    MergeStage stage{position,   scratch.attnMax,           scratch.attnSum, scratch.attnAcc,
+                     dims.heads, dims.heads / dims.kvHeads, dims.headDim,    AttnChunks(dims.maxSeq)};
+    ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
+    return LaunchFused<1>(s, dims.hidden, GemvBlockCap(), qdim, stage, epi);
+}
+
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols)
 {
     ResidualEpi epi{w, residual, out, rows, cols};
-    return LaunchFused<1, false>(s, rows, 4096, x, nullptr, cols, 0.0f, epi);
+    return LaunchFused<1>(s, rows, GemvBlockCap(), cols, PlainStage{x}, epi);
 }
 
 hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                               const uint16_t* wgate, const uint16_t* wup, float* act)
 {
     GateUpEpi epi{wgate, wup, act, dims.ffn, dims.hidden};
-    return LaunchFused<2, true>(s, dims.ffn, 4096, x, normW, dims.hidden, dims.eps, epi);
+    return LaunchFused<2>(s, dims.ffn, GemvBlockCap(), dims.hidden, NormStage{x, normW, dims.eps}, epi);
 }
 
 hipError_t LaunchLmHeadArgMax(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
-                              const uint16_t* table, float* logits, DecodeState* state, int32_t* ids, uint32_t idsCap,
-                              const DecodeScratch& scratch)
+                              const uint16_t* table, float* logits, const DecodeScratch& scratch)
 {
-    LmHeadEpi epi{table,        logits,         state,           ids, idsCap, dims.vocab, dims.hidden,
-                  scratch.argValue, scratch.argIndex, scratch.argCount};
-    return LaunchFused<1, true>(s, dims.vocab, kArgMaxBlocks, x, normW, dims.hidden, dims.eps, epi);
+    LmHeadEpi epi{table, logits, scratch.argValue, scratch.argIndex, dims.vocab, dims.hidden};
+    return LaunchFused<1>(s, dims.vocab, std::min(kArgMaxBlocks, GemvBlockCap()), dims.hidden,
+                          NormStage{x, normW, dims.eps}, epi);
 }
 
 hipError_t LaunchRopeAppend(hipStream_t s, const float* q, const float* k, const float* v, float* qOut,
@@ -815,10 +974,7 @@ namespace
 struct AttentionScratchOwner
 {
     DecodeScratch scratch{};
-    uint32_t kvHeads = 0;
-    uint32_t chunks = 0;
-    uint32_t group = 0;
-    uint32_t headDim = 0;
+    size_t floats = 0;
     int device = -1;
 };
 
@@ -829,7 +985,9 @@ int EnsureAttentionScratch(uint32_t kvHeads, uint32_t chunks, uint32_t group, ui
     int device = 0;
     MUYO_HIP_CHECK(hipGetDevice(&device));
     AttentionScratchOwner& o = g_attentionScratch;
-    if (o.device == device && o.kvHeads >= kvHeads && o.chunks == chunks && o.group >= group && o.headDim >= headDim)
+    const size_t small = static_cast<size_t>(kvHeads) * chunks * group;
+    const size_t floats = 2 * small + small * headDim;
+    if (o.device == device && o.floats >= floats)
     {
         return MUYO_OK;
     }
@@ -837,23 +995,17 @@ int EnsureAttentionScratch(uint32_t kvHeads, uint32_t chunks, uint32_t group, ui
     {
         (void)hipFree(o.scratch.attnMax);
         o.scratch = DecodeScratch{};
+        o.floats = 0;
     }
-    const size_t small = static_cast<size_t>(kvHeads) * chunks * group;
-    const size_t bytes = (2 * small + small * headDim) * sizeof(float) + kvHeads * sizeof(uint32_t) + 256;
-    char* base = nullptr;
-    if (hipMalloc(reinterpret_cast<void**>(&base), bytes) != hipSuccess)
+    float* base = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&base), floats * sizeof(float)) != hipSuccess)
     {
-        return Fail(MUYO_E_NOMEM, "attention scratch: hipMalloc(%zu) failed", bytes);
+        return Fail(MUYO_E_NOMEM, "attention scratch: hipMalloc(%zu) failed", floats * sizeof(float));
     }
-    MUYO_HIP_CHECK(hipMemset(base, 0, bytes));
-    o.scratch.attnMax = reinterpret_cast<float*>(base);
-    o.scratch.attnSum = o.scratch.attnMax + small;
-    o.scratch.attnAcc = o.scratch.attnSum + small;
-    o.scratch.attnCount = reinterpret_cast<uint32_t*>(o.scratch.attnAcc + small * headDim);
-    o.kvHeads = kvHeads;
-    o.chunks = chunks;
-    o.group = group;
-    o.headDim = headDim;
+    o.scratch.attnMax = base;
+    o.scratch.attnSum = base + small;
+    o.scratch.attnAcc = base + 2 * small;
+    o.floats = floats;
     o.device = device;
     return MUYO_OK;
 }
@@ -869,9 +1021,11 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
         return Fail(MUYO_E_NULL, "%s: q, caches, out and position are required", name);
     }
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
-        max_seq == 0)
+        max_seq == 0 || max_seq > kMaxAttnChunks * kAttnChunk)
     {
-        return Fail(MUYO_E_UNSUPPORTED, "%s: needs heads %% kv_heads == 0, group <= 8, head_dim 64 or 128", name);
+        return Fail(MUYO_E_UNSUPPORTED,
+                    "%s: needs heads %% kv_heads == 0, group <= 8, head_dim 64 or 128, max_seq <= %u", name,
+                    kMaxAttnChunks * kAttnChunk);
     }
     const int status = EnsureAttentionScratch(kv_heads, AttnChunks(max_seq), heads / kv_heads, head_dim);
     if (status != MUYO_OK)
@@ -884,9 +1038,12 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
     dims.headDim = head_dim;
     dims.maxSeq = max_seq;
     dims.attnScale = scale;
-    const hipError_t launched = LaunchAttention(AsStream(stream), dims, q, static_cast<const uint16_t*>(kcache),
-                                                static_cast<const uint16_t*>(vcache), position, out,
-                                                g_attentionScratch.scratch);
+    hipError_t launched = LaunchAttention(AsStream(stream), dims, q, static_cast<const uint16_t*>(kcache),
+                                          static_cast<const uint16_t*>(vcache), position, g_attentionScratch.scratch);
+    if (launched == hipSuccess)
+    {
+        launched = LaunchAttentionMerge(AsStream(stream), dims, position, g_attentionScratch.scratch, out);
+    }
     return launched == hipSuccess ? MUYO_OK : HipStatus(launched, name);
 }
 

@@ -1,4 +1,10 @@
-// Fused decode-step kernels (one Qwen2 layer = five launches) and their host-side launchers.
+// Fused decode-step kernels and their host-side launchers.
+//
+// No kernel communicates across its own workgroups (on gfx950 an agent-scope release fence
+// serialises device-wide, ~60 ns per workgroup): every cross-workgroup reduction is split at a
+// kernel boundary. The LM head leaves per-workgroup (max, index) partials that the next step's
+// first kernel (or a finalize kernel) reduces; attention leaves per-chunk softmax partials that
+// the o_proj kernel's prologue (or a small merge kernel) combines.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -22,42 +28,62 @@ struct DecodeDims
     float attnScale;   // 1/sqrt(headDim)
 };
 
-/// Device-resident per-step state (token and position of the step being decoded).
+/// Device-resident state of a generation run. `token` and `position` are those of the step
+/// being decoded; BeginStep derives them at the start of every step.
 struct DecodeState
 {
     int32_t token;
     int32_t position;
-    uint32_t step;   // index into the generated-ids ring
-    uint32_t pad;
+    int32_t start;  // cache row of the run's first step
+    uint32_t step;  // steps begun in this run
 };
 
-/// Scratch the split attention and the argmax need (owned by the caller, zeroed once).
+/// Scratch shared by the kernels of one decoder (sized for its model).
 struct DecodeScratch
 {
-    float* attnMax;        // [kvHeads][chunks][group]
-    float* attnSum;        // [kvHeads][chunks][group]
-    float* attnAcc;        // [kvHeads][chunks][group][headDim]
-    uint32_t* attnCount;   // [kvHeads]   arrival counters, reset by the last block
-    float* argValue;       // [argBlocks]
-    int32_t* argIndex;     // [argBlocks]
-    uint32_t* argCount;    // [1]
+    float* attnMax;     // [kvHeads][chunks][group]        chunk-local softmax max
+    float* attnSum;     // [kvHeads][chunks][group]        chunk-local softmax sum
+    float* attnAcc;     // [kvHeads][chunks][group][hd]    chunk-local P.V
+    float* argValue;    // [kArgMaxBlocks]                 per-workgroup LM-head max
+    int32_t* argIndex;  // [kArgMaxBlocks]                 and its (lowest) index
 };
 
-constexpr uint32_t kAttnChunk = 64;     // keys per attention block
-constexpr uint32_t kArgMaxBlocks = 1024;  // LM-head grid cap (partials for the argmax)
+constexpr uint32_t kAttnTile = 64;    // keys per LDS tile
+constexpr uint32_t kAttnChunk = 256;  // keys per attention workgroup (4 tiles)
+constexpr uint32_t kArgMaxBlocks = 1024;
+constexpr uint32_t kMaxAttnChunks = 32;  // max_seq up to 8192
 
 inline uint32_t AttnChunks(uint32_t maxSeq) { return (maxSeq + kAttnChunk - 1) / kAttnChunk; }
 
+/// Workgroups of the LM-head kernel (each leaves one argmax partial).
+uint32_t LmHeadBlocks(const DecodeDims& dims);
+
+/// True when o_proj merges the attention partials in its prologue (small models).
+bool MergeInOProj(const DecodeDims& dims);
+
 // Launchers. All return hipGetLastError() after the launch.
-hipError_t LaunchEmbed(hipStream_t s, const uint16_t* table, const DecodeState* state, float* x, uint32_t hidden,
-                       uint32_t vocab);
+hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
+                          int32_t position, uint32_t argBlocks);
+
+hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* state, const DecodeScratch& scratch,
+                           uint32_t argBlocks, float* x, int32_t* ids, uint32_t idsCap, uint32_t hidden,
+                           uint32_t vocab);
+
+hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, uint32_t argBlocks,
+                          int32_t* ids, uint32_t idsCap);
 
 hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                                const uint16_t* wqkv, const float* bias, const DecodeState* state, float* qOut,
                                uint16_t* kcache, uint16_t* vcache);
 
 hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
-                           const uint16_t* vcache, const int32_t* position, float* out, const DecodeScratch& scratch);
+                           const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch);
+
+hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const int32_t* position,
+                                const DecodeScratch& scratch, float* out);
+
+hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const int32_t* position,
+                             const DecodeScratch& scratch, const float* residual, float* out);
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols);
@@ -66,8 +92,7 @@ hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float
                               const uint16_t* wgate, const uint16_t* wup, float* act);
 
 hipError_t LaunchLmHeadArgMax(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
-                              const uint16_t* table, float* logits, DecodeState* state, int32_t* ids, uint32_t idsCap,
-                              const DecodeScratch& scratch);
+                              const uint16_t* table, float* logits, const DecodeScratch& scratch);
 
 /// Rope q/k and append k/v (fp16) at the position's cache row, from separate q/k/v vectors.
 hipError_t LaunchRopeAppend(hipStream_t s, const float* q, const float* k, const float* v, float* qOut,

@@ -3,10 +3,11 @@
 // It plays the role of RunFullModel's render graph (src/FullModel.cpp:487-1010) plus its
 // feedToken/sampleNext loop (:1096-1117): one arena of device memory holds every weight, the
 // fp16 KV cache and the activations; one step is 2 + 5 * layers launches on one stream
-// (decode_kernels.hip). The first step runs eagerly; later steps replay a hipGraph captured
-// once, because everything that changes per token (token id, position, step counter) lives in
-// device memory and is advanced by the last kernel of the step. Greedy generation therefore
-// needs no host round trip between tokens.
+// (6 per layer when the attention partials need their own merge kernel; decode_kernels.hip).
+// The first step runs eagerly; later steps replay a hipGraph captured once, because everything
+// that changes per token (token id, position, step counter) lives in device memory: the first
+// kernel of a step reduces the previous step's argmax partials into its token and advances the
+// position. Greedy generation therefore needs no host round trip between tokens.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -74,15 +75,6 @@ LayerTensor ToLayerTensor(uint32_t kind)
     }
 }
 
-/// Writes the device state of a new generation run (a kernel, so it is stream-ordered and can
-/// never race a pinned host buffer).
-__global__ void SetStateKernel(DecodeState* state, int32_t token, int32_t position)
-{
-    state->token = token;
-    state->position = position;
-    state->step = 0;
-    state->pad = 0;
-}
 }  // namespace
 
 struct MuyoDecoder
@@ -106,6 +98,8 @@ struct MuyoDecoder
     DecodeState* state = nullptr;
     int32_t* ids = nullptr;
     DecodeScratch scratch{};
+    uint32_t argBlocks = 0;     // LM-head workgroups = argmax partials per step
+    bool mergeInOProj = false;  // o_proj's prologue merges the attention partials
 
     bool warm = false;
     hipGraph_t graph = nullptr;
@@ -149,9 +143,10 @@ int Validate(const MuyoQwen2Config& c)
     {
         return Fail(MUYO_E_UNSUPPORTED, "decoder: a GEMV input longer than 40960 floats does not fit LDS");
     }
-    if (c.maxSeq > (1u << 24))
+    if (c.maxSeq > kMaxAttnChunks * kAttnChunk)
     {
-        return Fail(MUYO_E_RANGE, "decoder: maxSeq %u is too large", c.maxSeq);
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: maxSeq %u exceeds %u (%u attention chunks of %u keys)", c.maxSeq,
+                    kMaxAttnChunks * kAttnChunk, kMaxAttnChunks, kAttnChunk);
     }
     return MUYO_OK;
 }
@@ -184,61 +179,100 @@ size_t LayerTensorBytes(const MuyoQwen2Config& c, LayerTensor t)
     }
 }
 
+int LaunchFailed(hipError_t status, const char* kernel, uint32_t layer)
+{
+    return Fail(static_cast<int>(status), "decoder step: launching %s (layer %u) failed: %s (%d)", kernel, layer,
+                hipGetErrorString(status), static_cast<int>(status));
+}
+
+hipError_t EnqueueEmbed(MuyoDecoder* d, hipStream_t s)
+{
+    return LaunchBeginStep(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->scratch, d->argBlocks, d->xA, d->ids,
+                           kIdsCapacity, d->config.hidden, d->config.vocab);
+}
+
+hipError_t EnqueueQkv(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* x)
+{
+    return LaunchQkvRopeAppend(s, d->dims, x, d->At<float>(d->Layer(l, kAttnNorm)), d->At<uint16_t>(d->Layer(l, kQkv)),
+                               d->At<float>(d->Layer(l, kQkvBias)), d->state, d->q,
+                               d->At<uint16_t>(d->Layer(l, kKCache)), d->At<uint16_t>(d->Layer(l, kVCache)));
+}
+
+hipError_t EnqueueAttention(MuyoDecoder* d, hipStream_t s, uint32_t l)
+{
+    hipError_t status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(l, kKCache)),
+                                        d->At<uint16_t>(d->Layer(l, kVCache)), &d->state->position, d->scratch);
+    if (status == hipSuccess && !d->mergeInOProj)
+    {
+        status = LaunchAttentionMerge(s, d->dims, &d->state->position, d->scratch, d->attnOut);
+    }
+    return status;
+}
+
+hipError_t EnqueueOProj(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* residual, float* out)
+{
+    const uint16_t* wo = d->At<uint16_t>(d->Layer(l, kOut));
+    if (d->mergeInOProj)
+    {
+        return LaunchOProjMerged(s, d->dims, wo, &d->state->position, d->scratch, residual, out);
+    }
+    return LaunchMatVecResidual(s, wo, d->attnOut, residual, out, d->config.hidden, d->config.heads * d->config.headDim);
+}
+
+hipError_t EnqueueGateUp(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* x)
+{
+    return LaunchGateUpSwiGlu(s, d->dims, x, d->At<float>(d->Layer(l, kFfnNorm)), d->At<uint16_t>(d->Layer(l, kGate)),
+                              d->At<uint16_t>(d->Layer(l, kUp)), d->act);
+}
+
+hipError_t EnqueueDown(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* residual, float* out)
+{
+    return LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kDown)), d->act, residual, out, d->config.hidden,
+                                d->config.feedForward);
+}
+
+hipError_t EnqueueLmHead(MuyoDecoder* d, hipStream_t s, const float* x)
+{
+    return LaunchLmHeadArgMax(s, d->dims, x, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
+                              d->At<float>(d->logits), d->scratch);
+}
+
 int Enqueue(MuyoDecoder* d, hipStream_t s)
 {
-    const MuyoQwen2Config& c = d->config;
-    const uint32_t qdim = c.heads * c.headDim;
-    auto failed = [](hipError_t status, const char* kernel, uint32_t layer)
-    {
-        return Fail(static_cast<int>(status), "decoder step: launching %s (layer %u) failed: %s (%d)", kernel, layer,
-                    hipGetErrorString(status), static_cast<int>(status));
-    };
-    hipError_t status = LaunchEmbed(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->xA, c.hidden, c.vocab);
+    hipError_t status = EnqueueEmbed(d, s);
     if (status != hipSuccess)
     {
-        return failed(status, "embed", 0);
+        return LaunchFailed(status, "embed", 0);
     }
     float* x = d->xA;
     float* other = d->xB;
-    for (uint32_t l = 0; l < c.layers; ++l)
+    for (uint32_t l = 0; l < d->config.layers; ++l)
     {
-        status = LaunchQkvRopeAppend(s, d->dims, x, d->At<float>(d->Layer(l, kAttnNorm)),
-                                     d->At<uint16_t>(d->Layer(l, kQkv)), d->At<float>(d->Layer(l, kQkvBias)), d->state,
-                                     d->q, d->At<uint16_t>(d->Layer(l, kKCache)), d->At<uint16_t>(d->Layer(l, kVCache)));
-        if (status != hipSuccess)
+        if ((status = EnqueueQkv(d, s, l, x)) != hipSuccess)
         {
-            return failed(status, "qkv", l);
+            return LaunchFailed(status, "qkv", l);
         }
-        status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(l, kKCache)),
-                                 d->At<uint16_t>(d->Layer(l, kVCache)), &d->state->position, d->attnOut, d->scratch);
-        if (status != hipSuccess)
+        if ((status = EnqueueAttention(d, s, l)) != hipSuccess)
         {
-            return failed(status, "attention", l);
+            return LaunchFailed(status, "attention", l);
         }
-        status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kOut)), d->attnOut, x, d->xMid, c.hidden, qdim);
-        if (status != hipSuccess)
+        if ((status = EnqueueOProj(d, s, l, x, d->xMid)) != hipSuccess)
         {
-            return failed(status, "o_proj", l);
+            return LaunchFailed(status, "o_proj", l);
         }
-        status = LaunchGateUpSwiGlu(s, d->dims, d->xMid, d->At<float>(d->Layer(l, kFfnNorm)),
-                                    d->At<uint16_t>(d->Layer(l, kGate)), d->At<uint16_t>(d->Layer(l, kUp)), d->act);
-        if (status != hipSuccess)
+        if ((status = EnqueueGateUp(d, s, l, d->xMid)) != hipSuccess)
         {
-            return failed(status, "gate_up", l);
+            return LaunchFailed(status, "gate_up", l);
         }
-        status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kDown)), d->act, d->xMid, other, c.hidden,
-                                      c.feedForward);
-        if (status != hipSuccess)
+        if ((status = EnqueueDown(d, s, l, d->xMid, other)) != hipSuccess)
         {
-            return failed(status, "down", l);
+            return LaunchFailed(status, "down", l);
         }
         std::swap(x, other);
     }
-    status = LaunchLmHeadArgMax(s, d->dims, x, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
-                                d->At<float>(d->logits), d->state, d->ids, kIdsCapacity, d->scratch);
-    if (status != hipSuccess)
+    if ((status = EnqueueLmHead(d, s, x)) != hipSuccess)
     {
-        return failed(status, "lm_head", 0);
+        return LaunchFailed(status, "lm_head", 0);
     }
     return MUYO_OK;
 }
@@ -358,10 +392,8 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot attnMax = place(small * 4);
     const TensorSlot attnSum = place(small * 4);
     const TensorSlot attnAcc = place(small * c.headDim * 4);
-    const TensorSlot attnCount = place(c.kvHeads * 4);
     const TensorSlot argValue = place(kArgMaxBlocks * 4);
     const TensorSlot argIndex = place(kArgMaxBlocks * 4);
-    const TensorSlot argCount = place(4);
     d->arenaBytes = cursor;
 
     hipError_t status = hipGetDevice(&d->device);
@@ -405,10 +437,10 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->scratch.attnMax = d->At<float>(attnMax);
     d->scratch.attnSum = d->At<float>(attnSum);
     d->scratch.attnAcc = d->At<float>(attnAcc);
-    d->scratch.attnCount = d->At<uint32_t>(attnCount);
     d->scratch.argValue = d->At<float>(argValue);
     d->scratch.argIndex = d->At<int32_t>(argIndex);
-    d->scratch.argCount = d->At<uint32_t>(argCount);
+    d->argBlocks = LmHeadBlocks(d->dims);
+    d->mergeInOProj = MergeInOProj(d->dims);
     *out = d;
     return MUYO_OK;
 }
@@ -646,9 +678,8 @@ extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_
     {
         return Fail(MUYO_E_RANGE, "decoder: at most %u steps per call", kIdsCapacity);
     }
-    hipStream_t s = stream != nullptr ? AsStream(stream) : d->stream;
-    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(1), 0, s, d->state, token, position);
-    MUYO_HIP_CHECK(hipGetLastError());
+    hipStream_t s = AsStream(stream);
+    MUYO_HIP_CHECK(LaunchSetState(s, d->state, d->scratch, token, position, d->argBlocks));
     for (uint32_t i = 0; i < count; ++i)
     {
         const int status = RunStep(d, s);
@@ -657,6 +688,8 @@ extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_
             return status;
         }
     }
+    // The last step's id: its argmax partials reduced by a one-workgroup kernel.
+    MUYO_HIP_CHECK(LaunchFinalize(s, d->state, d->scratch, d->argBlocks, d->ids, kIdsCapacity));
     return MUYO_OK;
 }
 
@@ -683,7 +716,7 @@ extern "C" int muyo_decoder_generate(MuyoDecoder* d, int32_t token, int32_t posi
     {
         return status;
     }
-    MUYO_HIP_CHECK(hipStreamSynchronize(stream != nullptr ? AsStream(stream) : d->stream));
+    MUYO_HIP_CHECK(hipStreamSynchronize(AsStream(stream)));
     return ids != nullptr ? muyo_decoder_generated_ids(d, ids, count) : MUYO_OK;
 }
 
@@ -700,7 +733,7 @@ extern "C" int muyo_decoder_step(MuyoDecoder* d, int32_t token, int32_t position
 
 extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
 {
-    return d == nullptr ? 0u : 2u + 5u * d->config.layers;
+    return d == nullptr ? 0u : 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
 }
 
 extern "C" int muyo_decoder_set_state(MuyoDecoder* d, int32_t token, int32_t position, void* stream)
@@ -714,9 +747,8 @@ extern "C" int muyo_decoder_set_state(MuyoDecoder* d, int32_t token, int32_t pos
     {
         return Fail(MUYO_E_RANGE, "decoder_set_state: token %d / position %d out of range", token, position);
     }
-    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(1), 0, stream != nullptr ? AsStream(stream) : d->stream, d->state,
-                       token, position);
-    return LaunchStatus("decoder_set_state");
+    const hipError_t status = LaunchSetState(AsStream(stream), d->state, d->scratch, token, position, d->argBlocks);
+    return status == hipSuccess ? MUYO_OK : HipStatus(status, "decoder_set_state");
 }
 
 extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint32_t layer, void* stream)
@@ -730,42 +762,30 @@ extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint
     {
         return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: layer %u out of range", layer);
     }
-    hipStream_t s = stream != nullptr ? AsStream(stream) : d->stream;
-    const uint32_t qdim = c.heads * c.headDim;
+    hipStream_t s = AsStream(stream);
     hipError_t status;
     switch (kernel)
     {
         case MUYO_KERNEL_EMBED:
-            status = LaunchEmbed(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->xA, c.hidden, c.vocab);
+            status = EnqueueEmbed(d, s);
             break;
         case MUYO_KERNEL_QKV:
-            status = LaunchQkvRopeAppend(s, d->dims, d->xA, d->At<float>(d->Layer(layer, kAttnNorm)),
-                                         d->At<uint16_t>(d->Layer(layer, kQkv)),
-                                         d->At<float>(d->Layer(layer, kQkvBias)), d->state, d->q,
-                                         d->At<uint16_t>(d->Layer(layer, kKCache)),
-                                         d->At<uint16_t>(d->Layer(layer, kVCache)));
+            status = EnqueueQkv(d, s, layer, d->xA);
             break;
         case MUYO_KERNEL_ATTENTION:
-            status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(layer, kKCache)),
-                                     d->At<uint16_t>(d->Layer(layer, kVCache)), &d->state->position, d->attnOut,
-                                     d->scratch);
+            status = EnqueueAttention(d, s, layer);
             break;
         case MUYO_KERNEL_O_PROJ:
-            status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(layer, kOut)), d->attnOut, d->xA, d->xMid,
-                                          c.hidden, qdim);
+            status = EnqueueOProj(d, s, layer, d->xA, d->xMid);
             break;
         case MUYO_KERNEL_GATE_UP:
-            status = LaunchGateUpSwiGlu(s, d->dims, d->xMid, d->At<float>(d->Layer(layer, kFfnNorm)),
-                                        d->At<uint16_t>(d->Layer(layer, kGate)), d->At<uint16_t>(d->Layer(layer, kUp)),
-                                        d->act);
+            status = EnqueueGateUp(d, s, layer, d->xMid);
             break;
         case MUYO_KERNEL_DOWN:
-            status = LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(layer, kDown)), d->act, d->xMid, d->xB,
-                                          c.hidden, c.feedForward);
+            status = EnqueueDown(d, s, layer, d->xMid, d->xB);
             break;
         case MUYO_KERNEL_LM_HEAD:
-            status = LaunchLmHeadArgMax(s, d->dims, d->xA, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
-                                        d->At<float>(d->logits), d->state, d->ids, kIdsCapacity, d->scratch);
+            status = EnqueueLmHead(d, s, d->xA);
             break;
         default:
             return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: unknown kernel %u", kernel);

@@ -13,6 +13,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "gemv_core.hpp"
 
 namespace muyo
 {
@@ -186,6 +187,70 @@ __global__ __launch_bounds__(kBlock) void MatVecFast(const AT* __restrict__ a, c
     }
 }
 
+/// fp16 A: every lane's chunks of a row issued as one batch (gemv_core.hpp); the first batch is
+/// requested before B is staged, and the next row's batch before this row's reduction.
+template <int kLpr, int kCpl>
+__global__ __launch_bounds__(kBlock) void MatVecFastF16(const uint16_t* __restrict__ a, const float* __restrict__ b,
+                                                        float* __restrict__ d, const float* __restrict__ fuse0,
+                                                        const float* __restrict__ fuse1, MatVecGeometry g)
+{
+    extern __shared__ float4 xs[];
+    const uint32_t nchunks = g.ncols / 8;
+    constexpr int kRowsPerWave = kWave / kLpr;
+    constexpr uint32_t kBatch = kLpr * kCpl;
+    uint64_t aOff, bOff, dOff;
+    BatchOffsets(g, blockIdx.y, aOff, bOff, dOff);
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t segment = lane / kLpr;
+    const uint32_t lir = lane % kLpr;
+    const uint32_t stride = gridDim.x * kWavesPerBlock * kRowsPerWave;
+    const uint16_t* aBase = a + aOff;
+
+    uint32_t first = (blockIdx.x * kWavesPerBlock + threadIdx.x / kWave) * kRowsPerWave;
+    half8 w[kCpl];
+    if (first + segment < g.rows)
+    {
+        LoadBatch<kLpr, kCpl>(aBase + static_cast<uint64_t>(first + segment) * g.ncols, 0, nchunks, lir, w);
+    }
+    StageSplit<kBlock, 8, false>(b + bOff, nullptr, g.ncols, 0.0f, xs);
+    const float4* lo = xs;
+    const float4* hi = xs + nchunks;
+
+    for (; first < g.rows; first += stride)
+    {
+        const uint32_t row = first + segment;
+        float acc = 0.0f;
+        if (row < g.rows)
+        {
+            acc = DotBatch<kLpr, kCpl>(w, 0, nchunks, lir, lo, hi, 0.0f);
+            for (uint32_t base = kBatch; base < nchunks; base += kBatch)
+            {
+                LoadBatch<kLpr, kCpl>(aBase + static_cast<uint64_t>(row) * g.ncols, base, nchunks, lir, w);
+                acc = DotBatch<kLpr, kCpl>(w, base, nchunks, lir, lo, hi, acc);
+            }
+        }
+        if (first + stride + segment < g.rows)
+        {
+            LoadBatch<kLpr, kCpl>(aBase + static_cast<uint64_t>(first + stride + segment) * g.ncols, 0, nchunks, lir,
+                                  w);
+        }
+        acc = GroupSum<kLpr>(acc);
+        if (lir == 0 && row < g.rows)
+        {
+            float value = acc;
+            if (g.fusion & LLAMA_MAT_VEC_FUSION_BIAS0)
+            {
+                value += fuse0[dOff + row];
+            }
+            if (g.fusion & LLAMA_MAT_VEC_FUSION_BIAS1)
+            {
+                value += fuse1[dOff + row];
+            }
+            d[dOff + row] = value;
+        }
+    }
+}
+
 /// Any alignment, any ncols: one wave per row, scalar loads, B read from global memory.
 template <typename AT>
 __device__ __forceinline__ float LoadAsFloat(const AT* p);
@@ -257,22 +322,63 @@ int PickLanesPerRow(uint32_t nchunks)
 
 constexpr uint32_t kMaxLdsBytes = 160 * 1024;
 
+template <typename Kernel>
+hipError_t PrepareLds(Kernel kernel, size_t lds)
+{
+    if (lds > 64 * 1024)
+    {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   static_cast<int>(lds));
+    }
+    return hipSuccess;
+}
+
 template <int kLpr, typename AT>
 hipError_t LaunchFast(dim3 grid, size_t lds, hipStream_t stream, const AT* a, const float* b, float* d,
                       const float* fuse0, const float* fuse1, const MatVecGeometry& g)
 {
-    if (lds > 64 * 1024)
+    const hipError_t status = PrepareLds(&MatVecFast<kLpr, AT>, lds);
+    if (status != hipSuccess)
     {
-        const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(&MatVecFast<kLpr, AT>),
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                      static_cast<int>(lds));
-        if (status != hipSuccess)
-        {
-            return status;
-        }
+        return status;
     }
     hipLaunchKernelGGL((MatVecFast<kLpr, AT>), grid, dim3(kBlock), lds, stream, a, b, d, fuse0, fuse1, g);
     return hipGetLastError();
+}
+
+template <int kLpr, int kCpl>
+hipError_t LaunchFastF16(uint32_t gy, size_t lds, hipStream_t stream, const uint16_t* a, const float* b, float* d,
+                         const float* fuse0, const float* fuse1, const MatVecGeometry& g)
+{
+    const hipError_t status = PrepareLds(&MatVecFastF16<kLpr, kCpl>, lds);
+    if (status != hipSuccess)
+    {
+        return status;
+    }
+    const uint32_t rowsPerBlock = kWavesPerBlock * (kWave / kLpr);
+    const uint32_t blocks = std::max(1u, std::min(CeilDiv(g.rows, rowsPerBlock), 2048u));
+    hipLaunchKernelGGL((MatVecFastF16<kLpr, kCpl>), dim3(blocks, gy, 1), dim3(kBlock), lds, stream, a, b, d, fuse0,
+                       fuse1, g);
+    return hipGetLastError();
+}
+
+hipError_t DispatchFastF16(uint32_t gy, size_t lds, hipStream_t stream, const uint16_t* a, const float* b, float* d,
+                           const float* fuse0, const float* fuse1, const MatVecGeometry& g)
+{
+    const RowShape shape = PickRowShape(g.ncols / 8, 1);
+#define MUYO_GEMV_CASE(L, C)                                                          \
+    if (shape.lpr == L && shape.cpl == C)                                             \
+    {                                                                                 \
+        return LaunchFastF16<L, C>(gy, lds, stream, a, b, d, fuse0, fuse1, g);         \
+    }
+    MUYO_GEMV_CASE(8, 8)
+    MUYO_GEMV_CASE(16, 8)
+    MUYO_GEMV_CASE(32, 8)
+    MUYO_GEMV_CASE(64, 8)
+    MUYO_GEMV_CASE(64, 12)
+    MUYO_GEMV_CASE(64, 16)
+#undef MUYO_GEMV_CASE
+    return hipErrorInvalidValue;
 }
 
 template <typename AT>
@@ -334,11 +440,18 @@ int LaunchMatVec(const char* name, const LlamaMatVecPushConstants* pc, const Muy
     constexpr uint32_t ce = Chunk<AT>::kElems;
     const bool offsetsAligned = (pc->batchStrideA % ce) == 0 || (gy == 1 && pc->baseWorkGroupY == 0);
     const size_t lds = static_cast<size_t>(g.ncols) * sizeof(float);
-    const bool fast = (g.ncols % ce) == 0 && Aligned16(a) && offsetsAligned && lds <= kMaxLdsBytes;
+    // The fp16 kernel stages B with float4 loads: B's batch rows must start 16-byte aligned.
+    const bool bAligned = Aligned16(b) && ((pc->batchStrideB % 4) == 0 || (gy == 1 && pc->baseWorkGroupY == 0));
+    const bool fast = (g.ncols % ce) == 0 && Aligned16(a) && offsetsAligned && lds <= kMaxLdsBytes &&
+                      (sizeof(AT) == 4 || bAligned);
     hipStream_t s = AsStream(stream);
 
     hipError_t status;
-    if (fast)
+    if (fast && sizeof(AT) == 2)
+    {
+        status = DispatchFastF16(gy, lds, s, reinterpret_cast<const uint16_t*>(a), b, d, fuse0, fuse1, g);
+    }
+    else if (fast)
     {
         const uint32_t nchunks = g.ncols / ce;
         const int lpr = PickLanesPerRow(nchunks);

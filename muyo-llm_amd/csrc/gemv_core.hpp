@@ -1,0 +1,239 @@
+// Device building blocks shared by the per-op GEMV (gemv.hip) and the fused decode GEMVs
+// (decode_kernels.hip).
+//
+// A row of fp16 weights is streamed in 16-byte chunks (8 halves); lane `lir` of a kLpr-lane
+// segment owns chunks lir, lir + kLpr, lir + 2*kLpr, ... . A "batch" is kCpl such chunks per
+// lane, all issued as independent loads before any of them is used, so one batch costs one
+// memory latency however long the row is. The activation sits in LDS in the split layout
+// (low and high float4 of chunk c at lo[c] and hi[c]) so the per-lane float4 reads of
+// consecutive chunks are consecutive and bank-conflict free.
+#pragma once
+
+#include "common.hpp"
+
+namespace muyo
+{
+/// LDS slot of element i of an activation whose chunks are split into lo/hi float4 arrays.
+__device__ __forceinline__ uint32_t SplitSlot(uint32_t i, uint32_t nchunks)
+{
+    const uint32_t c = i >> 3;
+    const uint32_t r = i & 7u;
+    return r < 4 ? c * 4 + r : (nchunks + c) * 4 + (r - 4);
+}
+
+/// Issue the loads of one batch: chunks base + lir + i*kLpr (i < kCpl) of `row`. Out-of-range
+/// chunks load the row's last chunk instead (a cache hit) and are dropped in DotBatch, so the
+/// batch is straight-line code: every load issues back to back and each FMA group waits only
+/// for its own load.
+template <int kLpr, int kCpl>
+__device__ __forceinline__ void LoadBatch(const uint16_t* __restrict__ row, uint32_t base, uint32_t nchunks,
+                                          uint32_t lir, half8 (&w)[kCpl])
+{
+    const half8* chunks = reinterpret_cast<const half8*>(row);
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+    {
+        const uint32_t c = min(base + lir + i * kLpr, nchunks - 1);
+        // Weights are streamed once per step: non-temporal, so they do not evict activations.
+        w[i] = __builtin_nontemporal_load(chunks + c);
+    }
+}
+
+/// Dot one loaded chunk (8 halves, widened exactly inside the FMA) with its 8 activations.
+__device__ __forceinline__ float DotChunk(const half8& w, const float4& x0, const float4& x1, float acc)
+{
+    acc = fmaf(static_cast<float>(w[0]), x0.x, acc);
+    acc = fmaf(static_cast<float>(w[1]), x0.y, acc);
+    acc = fmaf(static_cast<float>(w[2]), x0.z, acc);
+    acc = fmaf(static_cast<float>(w[3]), x0.w, acc);
+    acc = fmaf(static_cast<float>(w[4]), x1.x, acc);
+    acc = fmaf(static_cast<float>(w[5]), x1.y, acc);
+    acc = fmaf(static_cast<float>(w[6]), x1.z, acc);
+    acc = fmaf(static_cast<float>(w[7]), x1.w, acc);
+    return acc;
+}
+
+/// Consume one loaded batch against the activation in LDS (chunks past the row add nothing).
+template <int kLpr, int kCpl>
+__device__ __forceinline__ float DotBatch(const half8 (&w)[kCpl], uint32_t base, uint32_t nchunks, uint32_t lir,
+                                          const float4* __restrict__ lo, const float4* __restrict__ hi, float acc)
+{
+    float a[4] = {acc, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+    {
+        const uint32_t c = base + lir + i * kLpr;
+        const uint32_t cc = min(c, nchunks - 1);
+        const float part = DotChunk(w[i], lo[cc], hi[cc], 0.0f);
+        a[i & 3] += c < nchunks ? part : 0.0f;
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
+/// The whole row's dot product for this lane, given its first batch already loaded in `w`.
+/// Rows longer than one batch are double-buffered: batch k+1 is requested before batch k is
+/// consumed, so a long row costs about one memory latency plus its streaming time.
+template <int kLpr, int kCpl>
+__device__ __forceinline__ float RowDot(const uint16_t* __restrict__ row, uint32_t nchunks, uint32_t lir,
+                                        half8 (&w)[kCpl], const float4* __restrict__ lo,
+                                        const float4* __restrict__ hi)
+{
+    constexpr uint32_t kBatch = kLpr * kCpl;
+    if (nchunks <= kBatch)
+    {
+        return DotBatch<kLpr, kCpl>(w, 0, nchunks, lir, lo, hi, 0.0f);
+    }
+    // Ping-pong between `w` and `other` (no register copies): each half-iteration requests the
+    // following batch into one buffer and consumes the other.
+    float acc = 0.0f;
+    half8 other[kCpl];
+    uint32_t base = 0;
+    for (;;)
+    {
+        uint32_t following = base + kBatch;
+        if (following >= nchunks)
+        {
+            return DotBatch<kLpr, kCpl>(w, base, nchunks, lir, lo, hi, acc);
+        }
+        LoadBatch<kLpr, kCpl>(row, following, nchunks, lir, other);
+        acc = DotBatch<kLpr, kCpl>(w, base, nchunks, lir, lo, hi, acc);
+        base = following;
+        following = base + kBatch;
+        if (following >= nchunks)
+        {
+            return DotBatch<kLpr, kCpl>(other, base, nchunks, lir, lo, hi, acc);
+        }
+        LoadBatch<kLpr, kCpl>(row, following, nchunks, lir, w);
+        acc = DotBatch<kLpr, kCpl>(other, base, nchunks, lir, lo, hi, acc);
+        base = following;
+    }
+}
+
+/// Stage an n-float activation (n % 8 == 0) into LDS in the split chunk layout with unrolled,
+/// independent float4 loads (kVec per thread per round), so staging costs one memory latency.
+/// With kNorm the values are scaled by rsqrt(mean(x^2) + eps) * w in the order (scale * x) * w
+/// of rms_norm.comp:122; that path holds x and w in registers and needs n/4 <= kVec * threads.
+/// Ends with the block synchronised.
+template <int kBlockThreads, int kVec, bool kNorm>
+__device__ __forceinline__ void StageSplit(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
+                                           float eps, float4* xs)
+{
+    constexpr int kWaveCount = kBlockThreads / kWave;
+    const uint32_t n4 = n / 4;
+    const uint32_t nchunks = n / 8;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    if constexpr (!kNorm)
+    {
+        for (uint32_t first = 0; first < n4; first += kVec * kBlockThreads)
+        {
+            float4 v[kVec];
+#pragma unroll
+            for (int k = 0; k < kVec; ++k)
+            {
+                v[k] = x4[min(first + threadIdx.x + k * kBlockThreads, n4 - 1)];
+            }
+#pragma unroll
+            for (int k = 0; k < kVec; ++k)
+            {
+                const uint32_t i = first + threadIdx.x + k * kBlockThreads;
+                if (i < n4)
+                {
+                    // float4 i holds elements 4i..4i+3: chunk i/2, the low half when i is even.
+                    xs[(i & 1u) ? nchunks + (i >> 1) : (i >> 1)] = v[k];
+                }
+            }
+        }
+    }
+    else
+    {
+        __shared__ float partial[kWaveCount];
+        const float4* w4 = reinterpret_cast<const float4*>(w);
+        float4 v[kVec];
+        float4 g[kVec];
+#pragma unroll
+        for (int k = 0; k < kVec; ++k)
+        {
+            const uint32_t i = min(threadIdx.x + k * kBlockThreads, n4 - 1);
+            v[k] = x4[i];
+            g[k] = w4[i];
+        }
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kVec; ++k)
+        {
+            if (threadIdx.x + k * kBlockThreads < n4)
+            {
+                ss = fmaf(v[k].x, v[k].x, ss);
+                ss = fmaf(v[k].y, v[k].y, ss);
+                ss = fmaf(v[k].z, v[k].z, ss);
+                ss = fmaf(v[k].w, v[k].w, ss);
+            }
+        }
+        ss = GroupSum<kWave>(ss);
+        if ((threadIdx.x & (kWave - 1)) == 0)
+        {
+            partial[threadIdx.x / kWave] = ss;
+        }
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kWaveCount; ++k)
+        {
+            total += partial[k];
+        }
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
+#pragma unroll
+        for (int k = 0; k < kVec; ++k)
+        {
+            const uint32_t i = threadIdx.x + k * kBlockThreads;
+            if (i < n4)
+            {
+                float4 o;
+                o.x = (scale * v[k].x) * g[k].x;
+                o.y = (scale * v[k].y) * g[k].y;
+                o.z = (scale * v[k].z) * g[k].z;
+                o.w = (scale * v[k].w) * g[k].w;
+                xs[(i & 1u) ? nchunks + (i >> 1) : (i >> 1)] = o;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+/// (lanes per row, chunks per lane per batch) for a row of `nchunks` 16-byte chunks, with at
+/// least kNr rows per wave. One batch covers the row whenever it has at most 1024 chunks.
+struct RowShape
+{
+    int lpr;
+    int cpl;
+};
+
+inline RowShape PickRowShape(uint32_t nchunks, int nr)
+{
+    if (nchunks <= 64)
+    {
+        return {8, 8};
+    }
+    if (nchunks <= 128)
+    {
+        return {16, 8};
+    }
+    if (nchunks <= 256)
+    {
+        return {32, 8};
+    }
+    if (nr == 2)
+    {
+        return {32, 16};  // two rows per wave: at most 32 lanes each
+    }
+    if (nchunks <= 512)
+    {
+        return {64, 8};
+    }
+    if (nchunks <= 768)
+    {
+        return {64, 12};
+    }
+    return {64, 16};
+}
+}  // namespace muyo

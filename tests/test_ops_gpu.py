@@ -524,7 +524,7 @@ def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape):
     vc = torch.empty_like(kc)
     mh.check(mh.load().muyo_fill_normal_f16(kc.data_ptr(), kc.numel(), 31, 0.0, 1.0, stream(torch)))
     mh.check(mh.load().muyo_fill_normal_f16(vc.data_ptr(), vc.numel(), 32, 0.0, 1.0, stream(torch)))
-    for pos in (0, 63, 64, 1000, 2047):
+    for pos in (0, 63, 64, 255, 256, 257, 1000, 2047):
         q = orc.normal_f32(heads * hd, 100 + pos)
         k = orc.normal_f32(kv * hd, 200 + pos)
         v = orc.normal_f32(kv * hd, 300 + pos)
