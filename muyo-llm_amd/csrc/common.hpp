@@ -78,44 +78,100 @@ __device__ __forceinline__ uint16_t FloatToHalfBits(float value)
     return __builtin_bit_cast(uint16_t, static_cast<_Float16>(value));
 }
 
-/// Sum across groups of `kWidth` consecutive lanes; every lane of a group gets the group's sum.
+/// The value held by a lane of the other half of this lane's group of 2*kStep consecutive lanes.
+/// Meant for butterfly reductions in which, before step kStep, every lane of each kStep-lane
+/// half already holds the same value: the partner lane then need not be lane ^ kStep, so the
+/// steps inside a 16-lane row use DPP (quad permutes, then the half-row and row mirrors), the
+/// step across rows a swizzle, and the step across the wave's halves two lane reads.
+template <int kStep>
+__device__ __forceinline__ int PartnerLane(int value)
+{
+    static_assert(kStep == 1 || kStep == 2 || kStep == 4 || kStep == 8 || kStep == 16 || kStep == 32, "step");
+    if constexpr (kStep == 1)
+    {
+        return __builtin_amdgcn_update_dpp(value, value, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    }
+    else if constexpr (kStep == 2)
+    {
+        return __builtin_amdgcn_update_dpp(value, value, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    }
+    else if constexpr (kStep == 4)
+    {
+        return __builtin_amdgcn_update_dpp(value, value, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    }
+    else if constexpr (kStep == 8)
+    {
+        return __builtin_amdgcn_update_dpp(value, value, 0x140, 0xF, 0xF, false);  // row_mirror
+    }
+    else if constexpr (kStep == 16)
+    {
+        return __builtin_amdgcn_ds_swizzle(value, 0x401F);  // bit mode: lane ^ 16 within 32 lanes
+    }
+    else
+    {
+        const int low = __builtin_amdgcn_readlane(value, 0);
+        const int high = __builtin_amdgcn_readlane(value, 32);
+        return (__lane_id() < 32) ? high : low;
+    }
+}
+
+template <int kStep>
+__device__ __forceinline__ float PartnerLane(float value)
+{
+    return __int_as_float(PartnerLane<kStep>(__float_as_int(value)));
+}
+
+/// Sum across groups of `kWidth` consecutive lanes; every lane of a group gets the group's sum,
+/// bit-identical on every lane (each step adds the same two values in either order).
 template <int kWidth>
 __device__ __forceinline__ float GroupSum(float value)
 {
-#pragma unroll
-    for (int offset = kWidth / 2; offset > 0; offset >>= 1)
-    {
-        value += __shfl_xor(value, offset, kWave);
-    }
+    static_assert(kWidth >= 1 && kWidth <= kWave && (kWidth & (kWidth - 1)) == 0, "width");
+    if constexpr (kWidth >= 2) value += PartnerLane<1>(value);
+    if constexpr (kWidth >= 4) value += PartnerLane<2>(value);
+    if constexpr (kWidth >= 8) value += PartnerLane<4>(value);
+    if constexpr (kWidth >= 16) value += PartnerLane<8>(value);
+    if constexpr (kWidth >= 32) value += PartnerLane<16>(value);
+    if constexpr (kWidth >= 64) value += PartnerLane<32>(value);
     return value;
 }
 
 template <int kWidth>
 __device__ __forceinline__ float GroupMax(float value)
 {
-#pragma unroll
-    for (int offset = kWidth / 2; offset > 0; offset >>= 1)
-    {
-        value = fmaxf(value, __shfl_xor(value, offset, kWave));
-    }
+    static_assert(kWidth >= 1 && kWidth <= kWave && (kWidth & (kWidth - 1)) == 0, "width");
+    if constexpr (kWidth >= 2) value = fmaxf(value, PartnerLane<1>(value));
+    if constexpr (kWidth >= 4) value = fmaxf(value, PartnerLane<2>(value));
+    if constexpr (kWidth >= 8) value = fmaxf(value, PartnerLane<4>(value));
+    if constexpr (kWidth >= 16) value = fmaxf(value, PartnerLane<8>(value));
+    if constexpr (kWidth >= 32) value = fmaxf(value, PartnerLane<16>(value));
+    if constexpr (kWidth >= 64) value = fmaxf(value, PartnerLane<32>(value));
     return value;
+}
+
+template <int kStep>
+__device__ __forceinline__ void ArgMaxStep(float& value, int32_t& index)
+{
+    const float other = PartnerLane<kStep>(value);
+    const int32_t otherIndex = PartnerLane<kStep>(index);
+    if (other > value || (other == value && otherIndex < index))
+    {
+        value = other;
+        index = otherIndex;
+    }
 }
 
 /// (value, index) maximum with ties to the lower index, across groups of kWidth lanes.
 template <int kWidth>
 __device__ __forceinline__ void GroupArgMax(float& value, int32_t& index)
 {
-#pragma unroll
-    for (int offset = kWidth / 2; offset > 0; offset >>= 1)
-    {
-        const float other = __shfl_xor(value, offset, kWave);
-        const int32_t otherIndex = __shfl_xor(index, offset, kWave);
-        if (other > value || (other == value && otherIndex < index))
-        {
-            value = other;
-            index = otherIndex;
-        }
-    }
+    static_assert(kWidth >= 1 && kWidth <= kWave && (kWidth & (kWidth - 1)) == 0, "width");
+    if constexpr (kWidth >= 2) ArgMaxStep<1>(value, index);
+    if constexpr (kWidth >= 4) ArgMaxStep<2>(value, index);
+    if constexpr (kWidth >= 8) ArgMaxStep<4>(value, index);
+    if constexpr (kWidth >= 16) ArgMaxStep<8>(value, index);
+    if constexpr (kWidth >= 32) ArgMaxStep<16>(value, index);
+    if constexpr (kWidth >= 64) ArgMaxStep<32>(value, index);
 }
 
 /// 16-byte global load of 8 halves widened to f32 (exact).

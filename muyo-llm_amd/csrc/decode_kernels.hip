@@ -34,25 +34,28 @@ constexpr int kWaves = kBlock / kWave;
 constexpr uint32_t kMaxLds = 160 * 1024;
 constexpr int kStageVec = 8;           // float4 per thread per staging round (rows <= 8192 floats)
 constexpr int kMaxGroup = 8;           // query heads per kv head
-constexpr uint32_t kBlocksPerCu = 4;   // GEMV grid cap: enough waves in flight, no second round
-constexpr uint32_t kMergeChunks = 8;   // chunks the o_proj prologue merges (max_seq <= 2048)
-constexpr uint32_t kMergeItems = 4;    // q channels per thread in that prologue (q dim <= 1024)
+#ifndef MUYO_GEMV_ROUNDS
+#define MUYO_GEMV_ROUNDS 1  // GEMV grid = this many rounds of the workgroups resident on the chip
+#endif
+constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
+constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
+constexpr uint32_t kMergeSlots = 512;  // (head, chunk) weights that prologue holds in LDS
 
-uint32_t GemvBlockCap()
+uint32_t CuCount()
 {
-    static uint32_t cap = 0;
-    if (cap == 0)
+    static uint32_t cus = 0;
+    if (cus == 0)
     {
         int device = 0;
-        int cus = 0;
+        int count = 0;
         if (hipGetDevice(&device) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || cus <= 0)
+            hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || count <= 0)
         {
-            cus = 256;
+            count = 256;
         }
-        cap = static_cast<uint32_t>(cus) * kBlocksPerCu;
+        cus = static_cast<uint32_t>(count);
     }
-    return cap;
+    return cus;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -73,68 +76,70 @@ struct NormStage
 };
 
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
-/// sum_c e^(m_c - M) l_c (flash-decoding's combine).
+/// sum_c e^(m_c - M) l_c (flash-decoding's combine). Every partial is requested at once, before
+/// the per-head weights are known, so the merge costs about one memory latency.
 struct MergeStage
 {
     const int32_t* position;
     const float* attnMax;
     const float* attnSum;
     const float* attnAcc;
-    uint32_t heads, group, headDim, maxChunks;
+    uint32_t heads, group, headDim, gridChunks;
+
+    __device__ uint64_t Slot(uint32_t h, uint32_t c) const
+    {
+        return (static_cast<uint64_t>(h / group) * gridChunks + c) * group + h % group;
+    }
 
     __device__ void Run(float4* xs, uint32_t n) const
     {
-        __shared__ float chunkMax[kBlock];
-        __shared__ float chunkSum[kBlock];
-        __shared__ float weight[kBlock];
+        __shared__ float weight[kMergeSlots];
         // Positions outside the cache are rejected on the host; clamping keeps every read in bounds.
-        const uint32_t pos = static_cast<uint32_t>(max(*position, 0));
-        const uint32_t chunks = min((pos + kAttnChunk) / kAttnChunk, maxChunks);
+        const uint32_t keys = static_cast<uint32_t>(max(*position, 0)) + 1;
+        const uint32_t chunks = min(AttnChunkCount(keys, headDim, kMergeAttnChunks), gridChunks);
         const uint32_t nchunks = n / 8;
-        // Per-(head, chunk) max and sum, and this thread's accumulators, all requested at once.
-        if (threadIdx.x < heads * chunks)
-        {
-            const uint32_t h = threadIdx.x / chunks;
-            const uint32_t c = threadIdx.x % chunks;
-            const uint64_t slot = (static_cast<uint64_t>(h / group) * maxChunks + c) * group + h % group;
-            chunkMax[threadIdx.x] = attnMax[slot];
-            chunkSum[threadIdx.x] = attnSum[slot];
-        }
-        float acc[kMergeItems][kMergeChunks];
+        uint32_t items[kMergeItems];
+        float acc[kMergeItems][kMergeAttnChunks];
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k)
         {
-            const uint32_t item = min(threadIdx.x + k * kBlock, n - 1);
-            const uint32_t h = item / headDim;
-            const uint32_t d = item % headDim;
+            items[k] = min(threadIdx.x + k * kBlock, n - 1);
+            const uint32_t h = items[k] / headDim;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeChunks; ++c)
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                const uint32_t cc = min(c, chunks - 1);
-                const uint64_t slot = (static_cast<uint64_t>(h / group) * maxChunks + cc) * group + h % group;
-                acc[k][c] = attnAcc[slot * headDim + d];
+                acc[k][c] = attnAcc[Slot(h, min(c, chunks - 1)) * headDim + items[k] % headDim];
             }
         }
-        __syncthreads();
         if (threadIdx.x < heads)
         {
             const uint32_t h = threadIdx.x;
-            float m = -INFINITY;
-            for (uint32_t c = 0; c < chunks; ++c)
+            float m[kMergeAttnChunks];
+            float l[kMergeAttnChunks];
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                m = fmaxf(m, chunkMax[h * chunks + c]);
+                m[c] = attnMax[Slot(h, min(c, chunks - 1))];
+                l[c] = attnSum[Slot(h, min(c, chunks - 1))];
+            }
+            float top = -INFINITY;
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            {
+                top = c < chunks ? fmaxf(top, m[c]) : top;
             }
             float den = 0.0f;
-            for (uint32_t c = 0; c < chunks; ++c)
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                const float e = expf(chunkMax[h * chunks + c] - m);
-                weight[h * chunks + c] = e;
-                den = fmaf(e, chunkSum[h * chunks + c], den);
+                m[c] = c < chunks ? expf(m[c] - top) : 0.0f;
+                den = fmaf(m[c], l[c], den);
             }
             const float inv = 1.0f / den;
-            for (uint32_t c = 0; c < chunks; ++c)
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                weight[h * chunks + c] *= inv;
+                weight[h * kMergeAttnChunks + c] = m[c] * inv;  // 0 past the last chunk
             }
         }
         __syncthreads();
@@ -142,19 +147,16 @@ struct MergeStage
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k)
         {
+            const uint32_t h = items[k] / headDim;
+            float out = 0.0f;
+#pragma unroll
+            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            {
+                out = fmaf(weight[h * kMergeAttnChunks + c], acc[k][c], out);
+            }
             const uint32_t item = threadIdx.x + k * kBlock;
             if (item < n)
             {
-                const uint32_t h = item / headDim;
-                float out = 0.0f;
-#pragma unroll
-                for (uint32_t c = 0; c < kMergeChunks; ++c)
-                {
-                    if (c < chunks)
-                    {
-                        out = fmaf(weight[h * chunks + c], acc[k][c], out);
-                    }
-                }
                 flat[SplitSlot(item, nchunks)] = out;
             }
         }
@@ -164,15 +166,19 @@ struct MergeStage
 
 // ------------------------------------------------------------------------------------------------
 // Fused GEMV: units of kNr rows, a staging policy, an epilogue per unit, an optional block tail.
+//
+// kSingle: a row fits one batch. Units are then double-buffered: the next unit's batch is
+// requested before the current one is consumed, so every wave keeps a batch in flight while it
+// computes. Otherwise each row streams through RowDot's ping-pong of batches.
 
-template <int kLpr, int kCpl, int kNr, class Stage, class Epi>
+template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
 __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage, Epi epi)
 {
     extern __shared__ float4 xs[];
     const uint32_t nchunks = cols / 8;
     constexpr int kSegs = kWave / kLpr;
     constexpr int kUnits = kSegs / kNr;
-    static_assert(kUnits >= 1, "a wave must hold at least one unit");
+    static_assert(kUnits >= 1 && (kNr == 1 || kNr == 2), "a wave holds whole units of one or two rows");
     const int lane = threadIdx.x & (kWave - 1);
     const int segment = lane / kLpr;
     const uint32_t lir = lane % kLpr;
@@ -181,46 +187,138 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
     const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
     const uint32_t stride = gridDim.x * kWaves * kUnits;
     const uint32_t units = epi.Units();
+    float bestValue = -INFINITY;
+    int32_t bestIndex = 0x7FFFFFFF;
+
+    // Every lane of a segment holds its row's sum; the unit's second row sits in the partner
+    // segment.
+    auto finish = [&](uint32_t unit, float dot) {
+        dot = GroupSum<kLpr>(dot);
+        float sums[kNr];
+        sums[0] = dot;
+        if constexpr (kNr == 2)
+        {
+            sums[1] = PartnerLane<kLpr>(dot);
+        }
+        if (unit < units && part == 0 && lir == 0)
+        {
+            epi.Finish(unit, sums, bestValue, bestIndex);
+        }
+    };
 
     // Weights do not depend on the activation: start streaming them before it is staged.
     uint32_t first = wave * kUnits;
-    half8 w[kCpl];
+    half8 wa[kCpl];
     if (first + unitInWave < units)
     {
-        LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
+        LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, wa);
     }
     stage.Run(xs, cols);
     const float4* lo = xs;
     const float4* hi = xs + nchunks;
 
+    if constexpr (kSingle)
+    {
+        half8 wb[kCpl];
+        for (; first < units; first += 2 * stride)
+        {
+            const uint32_t ua = first + unitInWave;
+            const uint32_t ub = ua + stride;
+            if (ub < units)
+            {
+                LoadBatch<kLpr, kCpl>(epi.Row(ub, part), 0, nchunks, lir, wb);
+            }
+            finish(ua, ua < units ? DotBatch<kLpr, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f) : 0.0f);
+            if (first + stride >= units)
+            {
+                break;
+            }
+            const uint32_t uc = ub + stride;
+            if (uc < units)
+            {
+                LoadBatch<kLpr, kCpl>(epi.Row(uc, part), 0, nchunks, lir, wa);
+            }
+            finish(ub, ub < units ? DotBatch<kLpr, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f) : 0.0f);
+        }
+    }
+    else
+    {
+        for (; first < units; first += stride)
+        {
+            const uint32_t unit = first + unitInWave;
+            float dot = 0.0f;
+            if (unit < units)
+            {
+                dot = RowDot<kLpr, kCpl>(epi.Row(unit, part), nchunks, lir, wa, lo, hi);
+            }
+            // The next unit's first batch goes out before this unit's reduction and epilogue.
+            const uint32_t next = first + stride + unitInWave;
+            if (next < units)
+            {
+                LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, wa);
+            }
+            finish(unit, dot);
+        }
+    }
+    epi.Tail(bestValue, bestIndex);
+}
+
+/// Long rows (more than 1024 16-byte chunks): the whole workgroup streams one row as a single
+/// batch of kCpl chunks per lane, rows double-buffered, the four wave sums combined in LDS.
+template <int kCpl, class Stage, class Epi>
+__global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Stage stage, Epi epi)
+{
+    extern __shared__ float4 xs[];
+    __shared__ float partial[2][kWaves];
+    const uint32_t nchunks = cols / 8;
+    const uint32_t lir = threadIdx.x;
+    const uint32_t units = epi.Units();
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
-    for (; first < units; first += stride)
-    {
-        const uint32_t unit = first + unitInWave;
-        const bool valid = unit < units;
-        float dot = 0.0f;
-        if (valid)
+    uint32_t parity = 0;
+    auto finish = [&](uint32_t unit, float dot) {
+        dot = GroupSum<kWave>(dot);
+        if ((threadIdx.x & (kWave - 1)) == 0)
         {
-            dot = RowDot<kLpr, kCpl>(epi.Row(unit, part), nchunks, lir, w, lo, hi);
+            partial[parity][threadIdx.x / kWave] = dot;
         }
-        // The next unit's first batch goes out before this unit's reduction and epilogue.
-        const uint32_t next = first + stride + unitInWave;
-        if (next < units)
+        __syncthreads();
+        if (threadIdx.x == 0)
         {
-            LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, w);
-        }
-        dot = GroupSum<kLpr>(dot);
-        float sums[kNr];
-#pragma unroll
-        for (int k = 0; k < kNr; ++k)
-        {
-            sums[k] = __shfl(dot, (unitInWave * kNr + k) * kLpr, kWave);
-        }
-        if (valid && part == 0 && lir == 0)
-        {
+            float sums[1] = {(partial[parity][0] + partial[parity][1]) + (partial[parity][2] + partial[parity][3])};
             epi.Finish(unit, sums, bestValue, bestIndex);
         }
+        parity ^= 1u;
+    };
+
+    uint32_t unit = blockIdx.x;
+    half8 wa[kCpl];
+    half8 wb[kCpl];
+    if (unit < units)
+    {
+        LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
+    }
+    stage.Run(xs, cols);
+    const float4* lo = xs;
+    const float4* hi = xs + nchunks;
+    for (; unit < units; unit += 2 * gridDim.x)
+    {
+        const uint32_t ub = unit + gridDim.x;
+        if (ub < units)
+        {
+            LoadBatch<kBlock, kCpl>(epi.Row(ub, 0), 0, nchunks, lir, wb);
+        }
+        finish(unit, DotBatch<kBlock, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f));
+        if (ub >= units)
+        {
+            break;
+        }
+        const uint32_t uc = ub + gridDim.x;
+        if (uc < units)
+        {
+            LoadBatch<kBlock, kCpl>(epi.Row(uc, 0), 0, nchunks, lir, wa);
+        }
+        finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f));
     }
     epi.Tail(bestValue, bestIndex);
 }
@@ -397,12 +495,35 @@ struct LmHeadEpi
 // ------------------------------------------------------------------------------------------------
 // Launch helpers for the fused GEMV.
 
-template <int kLpr, int kCpl, int kNr, class Stage, class Epi>
-hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
-                        const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+/// Workgroups of `kernel` the chip holds at once with `lds` bytes of dynamic LDS each.
+template <typename Kernel>
+uint32_t ResidentBlocks(Kernel kernel, size_t lds)
 {
-    const uint32_t unitsPerBlock = kWaves * ((kWave / kLpr) / kNr);
-    const uint32_t blocks = std::max(1u, std::min(CeilDiv(units, unitsPerBlock), blockCap));
+    int perCu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, kernel, kBlock, lds) != hipSuccess || perCu < 1)
+    {
+        perCu = 1;
+    }
+    return CuCount() * static_cast<uint32_t>(perCu) * MUYO_GEMV_ROUNDS;
+}
+
+/// Launches `kernel` over `units`, or with blocksOut only reports its workgroup count. The grid
+/// holds at most the workgroups resident at once (each stages the activation once and then
+/// strides over the units), so no workgroup waits for a second round.
+template <auto kKernel, class Stage, class Epi>
+hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBlock, uint32_t blockCap, size_t lds,
+                            uint32_t cols, const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+{
+    const auto kernel = kKernel;
+    // Cached per kernel (the statics belong to this instantiation).
+    static size_t residentLds = 0;
+    static uint32_t resident = 0;
+    if (resident == 0 || residentLds != lds)
+    {
+        resident = ResidentBlocks(kernel, lds);
+        residentLds = lds;
+    }
+    const uint32_t blocks = std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, resident}));
     if (blocksOut != nullptr)
     {
         *blocksOut = blocks;
@@ -412,21 +533,38 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
     static size_t configured = 64 * 1024;
     if (lds > configured)
     {
-        const hipError_t status =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&FusedMatVec<kLpr, kCpl, kNr, Stage, Epi>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+        const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                      static_cast<int>(lds));
         if (status != hipSuccess)
         {
             return status;
         }
         configured = lds;
     }
-    hipLaunchKernelGGL((FusedMatVec<kLpr, kCpl, kNr, Stage, Epi>), dim3(blocks), dim3(kBlock), lds, s, cols, stage,
-                       epi);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), lds, s, cols, stage, epi);
     return hipGetLastError();
 }
 
+template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
+hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
+                        const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+{
+    return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
+        s, units, kWaves * ((kWave / kLpr) / kNr), blockCap, lds, cols, stage, epi, blocksOut);
+}
+
+template <int kCpl, class Stage, class Epi>
+hipError_t LaunchBlockRowT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
+                           const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+{
+    return LaunchGemvKernel<&FusedMatVecBlockRow<kCpl, Stage, Epi>, Stage, Epi>(s, units, 1, blockCap, lds, cols,
+                                                                                 stage, epi, blocksOut);
+}
+
 /// Launches (or, with blocksOut, only sizes) the fused GEMV for a row of `cols` fp16 weights.
+/// Rows of up to 1024 chunks (512 for two-row units) fit one batch of a wave segment; longer
+/// rows use two-row units in RowDot's batch ping-pong, or one workgroup per row.
 template <int kNr, class Stage, class Epi>
 hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_t cols, const Stage& stage,
                        const Epi& epi, uint32_t* blocksOut = nullptr)
@@ -435,12 +573,13 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     {
         return hipErrorInvalidValue;
     }
-    const RowShape shape = PickRowShape(cols / 8, kNr);
+    const uint32_t nchunks = cols / 8;
     const size_t lds = static_cast<size_t>(cols) * sizeof(float);
-#define MUYO_FUSED_CASE(L, C)                                                                                \
-    if (shape.lpr == L && shape.cpl == C)                                                                    \
-    {                                                                                                        \
-        return LaunchFusedT<L, C, kNr, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);    \
+    const RowShape shape = PickRowShape(nchunks, kNr);
+#define MUYO_FUSED_CASE(L, C)                                                                                    \
+    if (shape.lpr == L && shape.cpl == C && nchunks <= L * C)                                                    \
+    {                                                                                                            \
+        return LaunchFusedT<L, C, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
     }
     MUYO_FUSED_CASE(8, 8)
     MUYO_FUSED_CASE(16, 8)
@@ -451,8 +590,24 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
         MUYO_FUSED_CASE(64, 8)
         MUYO_FUSED_CASE(64, 12)
         MUYO_FUSED_CASE(64, 16)
-    }
 #undef MUYO_FUSED_CASE
+        const uint32_t cpl = CeilDiv(nchunks, static_cast<uint32_t>(kBlock));
+#define MUYO_BLOCK_ROW_CASE(C)                                                                       \
+    if (cpl <= C)                                                                                    \
+    {                                                                                                \
+        return LaunchBlockRowT<C, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
+    }
+        MUYO_BLOCK_ROW_CASE(8)
+        MUYO_BLOCK_ROW_CASE(10)
+        MUYO_BLOCK_ROW_CASE(12)
+        MUYO_BLOCK_ROW_CASE(16)
+        MUYO_BLOCK_ROW_CASE(20)
+#undef MUYO_BLOCK_ROW_CASE
+    }
+    else
+    {
+        return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+    }
     return hipErrorInvalidValue;
 }
 
@@ -554,28 +709,30 @@ __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, con
 }
 
 // ------------------------------------------------------------------------------------------------
-// Attention over the fp16 cache: one workgroup per (256-key chunk, kv head).
+// Attention over the fp16 cache: one workgroup per (chunk of keys, kv head).
+//
+// The 256 lanes form kSlices groups of kRC = headDim/8 lanes; a group owns one key at a time and
+// each of its lanes one 16-byte slice of that key's K and V rows, which stay in registers (the
+// next keys' rows are requested before the current ones are used). A group keeps its own online
+// softmax per query head of the GQA group (max, sum, 8 channels of P.V per lane); at the end the
+// groups are combined through LDS and the chunk's partials written for the merge.
 
 template <int kHd>
 __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc,
                                                          const int32_t* __restrict__ position, uint32_t group,
-                                                         uint32_t maxSeq, float scale, DecodeScratch sc)
+                                                         uint32_t maxSeq, uint32_t maxChunks, float scale,
+                                                         DecodeScratch sc)
 {
-    constexpr int kRowChunks = kHd / 8;                  // 16-byte pieces per cache row
-    constexpr int kPieces = kAttnTile * kRowChunks;      // per K (or V) tile
-    constexpr int kPiecesPerThread = kPieces / kBlock;   // 2 (hd 64) or 4 (hd 128)
-    constexpr int kLpk = kRowChunks;                     // lanes per key in the score pass
-    constexpr int kKeysPerWave = kWave / kLpk;
-    constexpr int kItems = kMaxGroup * kHd / kBlock;     // (head, channel) items per thread
-    static_assert(kPieces % kBlock == 0 && (kMaxGroup * kHd) % kBlock == 0, "tile must split over the block");
-    __shared__ half8 kS[kPieces];
-    __shared__ half8 vS[kPieces];
-    __shared__ __align__(16) float qs[kMaxGroup * kHd];
-    __shared__ float probs[kMaxGroup][kAttnTile];
-    __shared__ float runMax[kMaxGroup];
-    __shared__ float runSum[kMaxGroup];
-    __shared__ float rescale[kMaxGroup];
+    constexpr int kRC = kHd / 8;           // lanes per key
+    constexpr int kSlices = kBlock / kRC;  // keys side by side
+    constexpr int kKpt = 2;                // keys per lane per round
+    static_assert(kSlices == 2048 / kHd, "slice count must match AttnSlices");
+    extern __shared__ float combine[];     // [kSlices][group][kHd]
+    __shared__ float sliceMax[kSlices][kMaxGroup];
+    __shared__ float sliceSum[kSlices][kMaxGroup];
+    __shared__ float headMax[kMaxGroup];
+    __shared__ float headSum[kMaxGroup];
 
     const int32_t pos = *position;
     if (pos < 0 || static_cast<uint32_t>(pos) >= maxSeq)
@@ -583,169 +740,194 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         return;
     }
     const uint32_t keys = static_cast<uint32_t>(pos) + 1;
-    const uint32_t chunks = (keys + kAttnChunk - 1) / kAttnChunk;
+    const uint32_t chunkKeys = AttnChunkKeys(keys, kHd, maxChunks);
     const uint32_t chunk = blockIdx.x;
-    if (chunk >= chunks)
+    if (chunk * chunkKeys >= keys)
     {
         return;
     }
     const uint32_t g = blockIdx.y;
-    const uint32_t c0 = chunk * kAttnChunk;
-    const uint32_t cn = min(kAttnChunk, keys - c0);
-    const uint32_t tiles = (cn + kAttnTile - 1) / kAttnTile;
-    const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const half8* kBase = reinterpret_cast<const half8*>(kc + static_cast<uint64_t>(g) * maxSeq * kHd);
-    const half8* vBase = reinterpret_cast<const half8*>(vc + static_cast<uint64_t>(g) * maxSeq * kHd);
+    const uint32_t c0 = chunk * chunkKeys;
+    const uint32_t cn = min(chunkKeys, keys - c0);
+    const uint32_t slice = threadIdx.x / kRC;
+    const uint32_t part = threadIdx.x % kRC;
+    const uint32_t rounds = (cn + kSlices * kKpt - 1) / (kSlices * kKpt);
+    const half8* kBase = reinterpret_cast<const half8*>(kc + static_cast<uint64_t>(g) * maxSeq * kHd) + part;
+    const half8* vBase = reinterpret_cast<const half8*>(vc + static_cast<uint64_t>(g) * maxSeq * kHd) + part;
 
-    // Tile loads: rows past the last key read the last key instead (always in bounds); their
-    // probabilities are zero, so they add nothing.
-    half8 kr[kPiecesPerThread];
-    half8 vr[kPiecesPerThread];
-    auto loadTile = [&](uint32_t t) {
+    // Keys of round r: (r * kKpt + k) * kSlices + slice; keys past the chunk read its last key
+    // (always in bounds) and are masked out of the softmax.
+    auto load = [&](uint32_t r, half8(&kk)[kKpt], half8(&vv)[kKpt]) {
 #pragma unroll
-        for (int i = 0; i < kPiecesPerThread; ++i)
+        for (int k = 0; k < kKpt; ++k)
         {
-            const uint32_t piece = threadIdx.x + i * kBlock;
-            const uint32_t key = min(c0 + t * kAttnTile + piece / kRowChunks, keys - 1);
-            const uint64_t offset = static_cast<uint64_t>(key) * kRowChunks + piece % kRowChunks;
-            kr[i] = kBase[offset];
-            vr[i] = vBase[offset];
+            const uint32_t key = c0 + min((r * kKpt + k) * kSlices + slice, cn - 1);
+            kk[k] = kBase[static_cast<uint64_t>(key) * kRC];
+            vv[k] = vBase[static_cast<uint64_t>(key) * kRC];
         }
     };
-    loadTile(0);
-    for (uint32_t i = threadIdx.x; i < group * kHd; i += kBlock)
-    {
-        qs[i] = q[static_cast<uint64_t>(g) * group * kHd + i];
-    }
-    if (threadIdx.x < kMaxGroup)
-    {
-        runMax[threadIdx.x] = -INFINITY;
-        runSum[threadIdx.x] = 0.0f;
-    }
-    float acc[kItems];
-#pragma unroll
-    for (int k = 0; k < kItems; ++k)
-    {
-        acc[k] = 0.0f;
-    }
-    const uint16_t* vFlat = reinterpret_cast<const uint16_t*>(vS);
-    const int slice = lane % kLpk;
+    half8 ka[kKpt], va[kKpt], kb[kKpt], vb[kKpt];
+    load(0, ka, va);
 
-    for (uint32_t t = 0; t < tiles; ++t)
+    float4 q0[kMaxGroup], q1[kMaxGroup];
+#pragma unroll
+    for (int h = 0; h < kMaxGroup; ++h)
     {
-        const uint32_t tn = min(kAttnTile, cn - t * kAttnTile);
-        __syncthreads();  // the previous tile's LDS reads are done
+        const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + min(h, static_cast<int>(group) - 1)) * kHd) + part * 2;
+        q0[h] = qh[0];
+        q1[h] = qh[1];
+    }
+    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][8];
 #pragma unroll
-        for (int i = 0; i < kPiecesPerThread; ++i)
+    for (int h = 0; h < kMaxGroup; ++h)
+    {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
         {
-            kS[threadIdx.x + i * kBlock] = kr[i];
-            vS[threadIdx.x + i * kBlock] = vr[i];
+            acc[h][c] = 0.0f;
         }
-        __syncthreads();
-        if (t + 1 < tiles)
-        {
-            loadTile(t + 1);  // in flight while this tile is computed
-        }
+    }
 
-        // Scores: kLpk lanes per key, each lane one 16-byte slice against every head of the group.
-        for (uint32_t jb = wave * kKeysPerWave; jb < kAttnTile; jb += kWaves * kKeysPerWave)
-        {
-            const uint32_t j = jb + lane / kLpk;
-            const half8 k8 = kS[j * kRowChunks + slice];
+    auto consume = [&](uint32_t r, const half8(&kk)[kKpt], const half8(&vv)[kKpt]) {
+        bool valid[kKpt];
 #pragma unroll
-            for (int h = 0; h < kMaxGroup; ++h)
+        for (int k = 0; k < kKpt; ++k)
+        {
+            valid[k] = (r * kKpt + k) * kSlices + slice < cn;
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; ++h)
+        {
+            if (h >= static_cast<int>(group))
             {
-                float part = 0.0f;
-                if (h < static_cast<int>(group))
+                break;  // uniform over the workgroup
+            }
+            float s[kKpt];
+            float top = m[h];
+#pragma unroll
+            for (int k = 0; k < kKpt; ++k)
+            {
+                s[k] = GroupSum<kRC>(DotChunk(kk[k], q0[h], q1[h], 0.0f)) * scale;
+                s[k] = valid[k] ? s[k] : -INFINITY;
+                top = fmaxf(top, s[k]);
+            }
+            if (top == -INFINITY)
+            {
+                continue;  // no valid key for this group yet
+            }
+            const float factor = expf(m[h] - top);  // 0 while m is still -inf
+            m[h] = top;
+            float p[kKpt];
+            float psum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kKpt; ++k)
+            {
+                p[k] = expf(s[k] - top);
+                psum += p[k];
+            }
+            l[h] = fmaf(l[h], factor, psum);
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+            {
+                float a = acc[h][c] * factor;
+#pragma unroll
+                for (int k = 0; k < kKpt; ++k)
                 {
-                    const float4 q0 = *reinterpret_cast<const float4*>(qs + h * kHd + slice * 8);
-                    const float4 q1 = *reinterpret_cast<const float4*>(qs + h * kHd + slice * 8 + 4);
-                    part = DotChunk(k8, q0, q1, 0.0f);
+                    a = fmaf(p[k], static_cast<float>(vv[k][c]), a);
                 }
-                part = GroupSum<kLpk>(part);
-                if (slice == 0 && h < static_cast<int>(group))
-                {
-                    probs[h][j] = j < tn ? part * scale : -INFINITY;
-                }
+                acc[h][c] = a;
             }
         }
-        __syncthreads();
+    };
 
-        // Online softmax, one wave per head (a tile is 64 keys: one per lane).
-        for (uint32_t h = wave; h < group; h += kWaves)
+    for (uint32_t r = 0; r < rounds; r += 2)
+    {
+        if (r + 1 < rounds)
         {
-            const float v = probs[h][lane];
-            const float tileMax = GroupMax<kWave>(v);
-            const float oldMax = runMax[h];
-            const float newMax = fmaxf(oldMax, tileMax);
-            const float p = lane < static_cast<int>(tn) ? expf(v - newMax) : 0.0f;
-            const float tileSum = GroupSum<kWave>(p);
-            probs[h][lane] = p;
+            load(r + 1, kb, vb);
+        }
+        consume(r, ka, va);
+        if (r + 1 >= rounds)
+        {
+            break;
+        }
+        if (r + 2 < rounds)
+        {
+            load(r + 2, ka, va);
+        }
+        consume(r + 1, kb, vb);
+    }
+
+    // Combine the slices: per-head chunk max and sum, then the rescaled P.V summed over slices.
+    if (part == 0)
+    {
+#pragma unroll
+        for (int h = 0; h < kMaxGroup; ++h)
+        {
+            sliceMax[slice][h] = m[h];
+            sliceSum[slice][h] = l[h];
+        }
+    }
+    __syncthreads();
+    {
+        // One wave per head; lane i holds slice i.
+        const int lane = threadIdx.x & (kWave - 1);
+        for (uint32_t h = threadIdx.x / kWave; h < group; h += kWaves)
+        {
+            const float mi = lane < kSlices ? sliceMax[lane][h] : -INFINITY;
+            const float top = GroupMax<kSlices>(mi);
+            const float li = (lane < kSlices && mi != -INFINITY) ? sliceSum[lane][h] * expf(mi - top) : 0.0f;
+            const float sum = GroupSum<kSlices>(li);
             if (lane == 0)
             {
-                const float factor = expf(oldMax - newMax);  // 0 for the first tile
-                rescale[h] = factor;
-                runSum[h] = runSum[h] * factor + tileSum;
-                runMax[h] = newMax;
-            }
-        }
-        __syncthreads();
-
-        // P.V: thread item (head, channel), accumulators rescaled to the running max.
-#pragma unroll
-        for (int k = 0; k < kItems; ++k)
-        {
-            const uint32_t item = threadIdx.x + k * kBlock;
-            if (item < group * kHd)
-            {
-                const uint32_t h = item / kHd;
-                const uint32_t d = item % kHd;
-                float a0 = acc[k] * rescale[h];
-                float a1 = 0.0f;
-                uint32_t j = 0;
-                for (; j + 1 < tn; j += 2)
-                {
-                    a0 = fmaf(probs[h][j], HalfBitsToFloat(vFlat[j * kHd + d]), a0);
-                    a1 = fmaf(probs[h][j + 1], HalfBitsToFloat(vFlat[(j + 1) * kHd + d]), a1);
-                }
-                if (j < tn)
-                {
-                    a0 = fmaf(probs[h][j], HalfBitsToFloat(vFlat[j * kHd + d]), a0);
-                }
-                acc[k] = a0 + a1;
+                headMax[h] = top;
+                headSum[h] = sum;
             }
         }
     }
-
-    // Publish this chunk's partials (read after the kernel boundary).
-    const uint64_t slot = static_cast<uint64_t>(g) * gridDim.x + chunk;
+    __syncthreads();
 #pragma unroll
-    for (int k = 0; k < kItems; ++k)
+    for (int h = 0; h < kMaxGroup; ++h)
     {
-        const uint32_t item = threadIdx.x + k * kBlock;
-        if (item < group * kHd)
+        if (h < static_cast<int>(group))
         {
-            sc.attnAcc[(slot * group + item / kHd) * kHd + item % kHd] = acc[k];
+            const float f = m[h] == -INFINITY ? 0.0f : expf(m[h] - headMax[h]);
+            float4* dst = reinterpret_cast<float4*>(combine + (static_cast<uint32_t>(slice) * group + h) * kHd + part * 8);
+            dst[0] = make_float4(acc[h][0] * f, acc[h][1] * f, acc[h][2] * f, acc[h][3] * f);
+            dst[1] = make_float4(acc[h][4] * f, acc[h][5] * f, acc[h][6] * f, acc[h][7] * f);
         }
+    }
+    __syncthreads();
+    const uint64_t slot = static_cast<uint64_t>(g) * gridDim.x + chunk;
+    for (uint32_t item = threadIdx.x; item < group * kHd; item += kBlock)
+    {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < kSlices; ++i)
+        {
+            sum += combine[i * group * kHd + item];
+        }
+        sc.attnAcc[slot * group * kHd + item] = sum;
     }
     if (threadIdx.x < group)
     {
-        sc.attnMax[slot * group + threadIdx.x] = runMax[threadIdx.x];
-        sc.attnSum[slot * group + threadIdx.x] = runSum[threadIdx.x];
+        sc.attnMax[slot * group + threadIdx.x] = headMax[threadIdx.x];
+        sc.attnSum[slot * group + threadIdx.x] = headSum[threadIdx.x];
     }
 }
 
 /// Combine the chunk partials of every query head: one workgroup per head, a thread per channel.
 __global__ __launch_bounds__(128) void AttentionMergeKernel(const int32_t* __restrict__ position, DecodeScratch sc,
                                                             float* __restrict__ out, uint32_t group, uint32_t headDim,
-                                                            uint32_t maxChunks)
+                                                            uint32_t policyChunks, uint32_t maxChunks)
 {
     const uint32_t h = blockIdx.x;
     const uint32_t g = h / group;
     const uint32_t hh = h % group;
-    const uint32_t pos = static_cast<uint32_t>(max(*position, 0));
-    const uint32_t chunks = min((pos + kAttnChunk) / kAttnChunk, maxChunks);
+    const uint32_t keys = static_cast<uint32_t>(max(*position, 0)) + 1;
+    const uint32_t chunks = min(AttnChunkCount(keys, headDim, policyChunks), maxChunks);
     float m[kMaxAttnChunks];
     float l[kMaxAttnChunks];
     float a[kMaxAttnChunks];
@@ -840,7 +1022,7 @@ uint32_t LmHeadBlocks(const DecodeDims& dims)
     uint32_t blocks = 0;
     LmHeadEpi epi{};
     epi.rows = dims.vocab;
-    (void)LaunchFused<1>(nullptr, dims.vocab, std::min(kArgMaxBlocks, GemvBlockCap()), dims.hidden,
+    (void)LaunchFused<1>(nullptr, dims.vocab, kArgMaxBlocks, dims.hidden,
                          NormStage{nullptr, nullptr, 0.0f}, epi, &blocks);
     return blocks;
 }
@@ -848,8 +1030,7 @@ uint32_t LmHeadBlocks(const DecodeDims& dims)
 bool MergeInOProj(const DecodeDims& dims)
 {
     const uint32_t qdim = dims.heads * dims.headDim;
-    return AttnChunks(dims.maxSeq) <= kMergeChunks && qdim <= kMergeItems * kBlock &&
-           dims.heads * AttnChunks(dims.maxSeq) <= static_cast<uint32_t>(kBlock);
+    return qdim <= kMergeItems * kBlock && dims.heads * kMergeAttnChunks <= kMergeSlots;
 }
 
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
@@ -884,40 +1065,58 @@ hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const floa
     QkvEpi epi{wqkv,        bias,       state,         qOut,         kcache, vcache, dims.hidden, dims.heads,
                dims.kvHeads, dims.headDim, dims.maxSeq, dims.thetaScale};
     const uint32_t units = (dims.heads + 2 * dims.kvHeads) * dims.headDim / 2;
-    return LaunchFused<2>(s, units, GemvBlockCap(), dims.hidden, NormStage{x, normW, dims.eps}, epi);
+    return LaunchFused<2>(s, units, kNoLimit, dims.hidden, NormStage{x, normW, dims.eps}, epi);
+}
+
+template <int kHd>
+hipError_t LaunchAttentionT(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
+                            const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch)
+{
+    const uint32_t group = dims.heads / dims.kvHeads;
+    const size_t lds = static_cast<size_t>(AttnSlices(kHd)) * group * kHd * sizeof(float);
+    static size_t configured = 64 * 1024;
+    if (lds > configured)
+    {
+        const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(&AttentionChunk<kHd>),
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                      static_cast<int>(lds));
+        if (status != hipSuccess)
+        {
+            return status;
+        }
+        configured = lds;
+    }
+    const dim3 grid(AttnGridChunks(dims.maxSeq, kHd, dims.attnChunks), dims.kvHeads, 1);
+    hipLaunchKernelGGL(AttentionChunk<kHd>, grid, dim3(kBlock), lds, s, q, kcache, vcache, position, group, dims.maxSeq,
+                       dims.attnChunks, dims.attnScale, scratch);
+    return hipGetLastError();
 }
 
 hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
                            const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch)
 {
-    const uint32_t group = dims.heads / dims.kvHeads;
-    if (group == 0 || group > static_cast<uint32_t>(kMaxGroup) || dims.heads % dims.kvHeads != 0 ||
-        AttnChunks(dims.maxSeq) > kMaxAttnChunks)
+    if (dims.kvHeads == 0 || dims.heads % dims.kvHeads != 0 || dims.heads / dims.kvHeads > kMaxGroup ||
+        dims.maxSeq == 0 || dims.maxSeq > kMaxSeq || dims.attnChunks == 0 || dims.attnChunks > kMaxAttnChunks)
     {
         return hipErrorInvalidValue;
     }
-    const dim3 grid(AttnChunks(dims.maxSeq), dims.kvHeads, 1);
     switch (dims.headDim)
     {
         case 64:
-            hipLaunchKernelGGL(AttentionChunk<64>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group,
-                               dims.maxSeq, dims.attnScale, scratch);
-            break;
+            return LaunchAttentionT<64>(s, dims, q, kcache, vcache, position, scratch);
         case 128:
-            hipLaunchKernelGGL(AttentionChunk<128>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group,
-                               dims.maxSeq, dims.attnScale, scratch);
-            break;
+            return LaunchAttentionT<128>(s, dims, q, kcache, vcache, position, scratch);
         default:
             return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const int32_t* position,
                                 const DecodeScratch& scratch, float* out)
 {
     hipLaunchKernelGGL(AttentionMergeKernel, dim3(dims.heads), dim3(std::min<uint32_t>(dims.headDim, 128)), 0, s,
-                       position, scratch, out, dims.heads / dims.kvHeads, dims.headDim, AttnChunks(dims.maxSeq));
+                       position, scratch, out, dims.heads / dims.kvHeads, dims.headDim, dims.attnChunks,
+                       AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks));
     return hipGetLastError();
 }
 
@@ -926,30 +1125,30 @@ hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16
 {
     const uint32_t qdim = dims.heads * dims.headDim;
     MergeStage stage{position,   scratch.attnMax,           scratch.attnSum, scratch.attnAcc,
-                     dims.heads, dims.heads / dims.kvHeads, dims.headDim,    AttnChunks(dims.maxSeq)};
+                     dims.heads, dims.heads / dims.kvHeads, dims.headDim,    AttnGridChunks(dims.maxSeq, dims.headDim, kMergeAttnChunks)};
     ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
-    return LaunchFused<1>(s, dims.hidden, GemvBlockCap(), qdim, stage, epi);
+    return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
 }
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols)
 {
     ResidualEpi epi{w, residual, out, rows, cols};
-    return LaunchFused<1>(s, rows, GemvBlockCap(), cols, PlainStage{x}, epi);
+    return LaunchFused<1>(s, rows, kNoLimit, cols, PlainStage{x}, epi);
 }
 
 hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                               const uint16_t* wgate, const uint16_t* wup, float* act)
 {
     GateUpEpi epi{wgate, wup, act, dims.ffn, dims.hidden};
-    return LaunchFused<2>(s, dims.ffn, GemvBlockCap(), dims.hidden, NormStage{x, normW, dims.eps}, epi);
+    return LaunchFused<2>(s, dims.ffn, kNoLimit, dims.hidden, NormStage{x, normW, dims.eps}, epi);
 }
 
 hipError_t LaunchLmHeadArgMax(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                               const uint16_t* table, float* logits, const DecodeScratch& scratch)
 {
     LmHeadEpi epi{table, logits, scratch.argValue, scratch.argIndex, dims.vocab, dims.hidden};
-    return LaunchFused<1>(s, dims.vocab, std::min(kArgMaxBlocks, GemvBlockCap()), dims.hidden,
+    return LaunchFused<1>(s, dims.vocab, kArgMaxBlocks, dims.hidden,
                           NormStage{x, normW, dims.eps}, epi);
 }
 
@@ -1021,13 +1220,17 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
         return Fail(MUYO_E_NULL, "%s: q, caches, out and position are required", name);
     }
     if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
-        max_seq == 0 || max_seq > kMaxAttnChunks * kAttnChunk)
+        max_seq == 0 || max_seq > kMaxSeq)
     {
         return Fail(MUYO_E_UNSUPPORTED,
                     "%s: needs heads %% kv_heads == 0, group <= 8, head_dim 64 or 128, max_seq <= %u", name,
-                    kMaxAttnChunks * kAttnChunk);
+                    kMaxSeq);
     }
-    const int status = EnsureAttentionScratch(kv_heads, AttnChunks(max_seq), heads / kv_heads, head_dim);
+    if (!Aligned16(q) || !Aligned16(kcache) || !Aligned16(vcache))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: q and the caches must be 16-byte aligned", name);
+    }
+    const int status = EnsureAttentionScratch(kv_heads, AttnGridChunks(max_seq, head_dim, kMaxAttnChunks), heads / kv_heads, head_dim);
     if (status != MUYO_OK)
     {
         return status;
@@ -1038,6 +1241,7 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
     dims.headDim = head_dim;
     dims.maxSeq = max_seq;
     dims.attnScale = scale;
+    dims.attnChunks = kMaxAttnChunks;
     hipError_t launched = LaunchAttention(AsStream(stream), dims, q, static_cast<const uint16_t*>(kcache),
                                           static_cast<const uint16_t*>(vcache), position, g_attentionScratch.scratch);
     if (launched == hipSuccess)

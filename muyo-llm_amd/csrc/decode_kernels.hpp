@@ -26,6 +26,7 @@ struct DecodeDims
     float eps;
     float thetaScale;  // ropeBase^(-2/headDim), computed in f32 on the host
     float attnScale;   // 1/sqrt(headDim)
+    uint32_t attnChunks;  // most attention chunks per kv head (kMaxAttnChunks or kMergeAttnChunks)
 };
 
 /// Device-resident state of a generation run. `token` and `position` are those of the step
@@ -41,24 +42,51 @@ struct DecodeState
 /// Scratch shared by the kernels of one decoder (sized for its model).
 struct DecodeScratch
 {
-    float* attnMax;     // [kvHeads][chunks][group]        chunk-local softmax max
-    float* attnSum;     // [kvHeads][chunks][group]        chunk-local softmax sum
-    float* attnAcc;     // [kvHeads][chunks][group][hd]    chunk-local P.V
+    float* attnMax;     // [kvHeads][gridChunks][group]        chunk-local softmax max
+    float* attnSum;     // [kvHeads][gridChunks][group]        chunk-local softmax sum
+    float* attnAcc;     // [kvHeads][gridChunks][group][hd]    chunk-local P.V (relative to the max)
     float* argValue;    // [kArgMaxBlocks]                 per-workgroup LM-head max
     int32_t* argIndex;  // [kArgMaxBlocks]                 and its (lowest) index
 };
 
-constexpr uint32_t kAttnTile = 64;    // keys per LDS tile
-constexpr uint32_t kAttnChunk = 256;  // keys per attention workgroup (4 tiles)
 constexpr uint32_t kArgMaxBlocks = 1024;
-constexpr uint32_t kMaxAttnChunks = 32;  // max_seq up to 8192
+constexpr uint32_t kMaxAttnChunks = 32;    // attention workgroups per kv head, at most
+constexpr uint32_t kMergeAttnChunks = 16;  // the same when o_proj's prologue merges the partials
+constexpr uint32_t kMaxSeq = 32768;
 
-inline uint32_t AttnChunks(uint32_t maxSeq) { return (maxSeq + kAttnChunk - 1) / kAttnChunk; }
+/// Keys one attention workgroup processes side by side: its 256 lanes hold one 16-byte slice of
+/// a cache row each (headDim 64 -> 32 keys, 128 -> 16 keys).
+__host__ __device__ inline uint32_t AttnSlices(uint32_t headDim) { return 2048u / headDim; }
+
+/// Keys per attention chunk for a cache of `keys` rows: a multiple of the slices, large enough
+/// that at most maxChunks chunks cover the rows.
+__host__ __device__ inline uint32_t AttnChunkKeys(uint32_t keys, uint32_t headDim, uint32_t maxChunks)
+{
+    const uint32_t slices = AttnSlices(headDim);
+    const uint32_t per = (keys + maxChunks - 1) / maxChunks;
+    const uint32_t rounded = (per + slices - 1) / slices * slices;
+    return rounded > slices ? rounded : slices;
+}
+
+__host__ __device__ inline uint32_t AttnChunkCount(uint32_t keys, uint32_t headDim, uint32_t maxChunks)
+{
+    const uint32_t chunkKeys = AttnChunkKeys(keys, headDim, maxChunks);
+    return (keys + chunkKeys - 1) / chunkKeys;
+}
+
+/// Chunk slots per kv head (the attention grid's x): the most chunks any position up to maxSeq
+/// needs, min(maxChunks, ceil(maxSeq / slices)).
+inline uint32_t AttnGridChunks(uint32_t maxSeq, uint32_t headDim, uint32_t maxChunks)
+{
+    const uint32_t bySlices = (maxSeq + AttnSlices(headDim) - 1) / AttnSlices(headDim);
+    return bySlices < maxChunks ? bySlices : maxChunks;
+}
 
 /// Workgroups of the LM-head kernel (each leaves one argmax partial).
 uint32_t LmHeadBlocks(const DecodeDims& dims);
 
-/// True when o_proj merges the attention partials in its prologue (small models).
+/// True when o_proj can merge the attention partials in its prologue (small models); such a
+/// decoder runs attention with at most kMergeAttnChunks chunks per kv head.
 bool MergeInOProj(const DecodeDims& dims);
 
 // Launchers. All return hipGetLastError() after the launch.

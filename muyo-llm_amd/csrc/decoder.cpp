@@ -143,10 +143,9 @@ int Validate(const MuyoQwen2Config& c)
     {
         return Fail(MUYO_E_UNSUPPORTED, "decoder: a GEMV input longer than 40960 floats does not fit LDS");
     }
-    if (c.maxSeq > kMaxAttnChunks * kAttnChunk)
+    if (c.maxSeq > kMaxSeq)
     {
-        return Fail(MUYO_E_UNSUPPORTED, "decoder: maxSeq %u exceeds %u (%u attention chunks of %u keys)", c.maxSeq,
-                    kMaxAttnChunks * kAttnChunk, kMaxAttnChunks, kAttnChunk);
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: maxSeq %u exceeds %u", c.maxSeq, kMaxSeq);
     }
     return MUYO_OK;
 }
@@ -355,6 +354,8 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     // The same f32 host computations as src/FullModel.cpp:184 and :201.
     d->dims.thetaScale = std::pow(c.ropeBase, -2.0F / static_cast<float>(c.headDim));
     d->dims.attnScale = 1.0F / std::sqrt(static_cast<float>(c.headDim));
+    d->mergeInOProj = MergeInOProj(d->dims);
+    d->dims.attnChunks = d->mergeInOProj ? kMergeAttnChunks : kMaxAttnChunks;
 
     // Arena layout: embedding, output norm, logits, then each layer's tensors, then activations
     // and scratch. Every tensor starts on a 256-byte boundary.
@@ -379,7 +380,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     }
     const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
     const size_t group = c.heads / c.kvHeads;
-    const size_t chunks = AttnChunks(c.maxSeq);
+    const size_t chunks = AttnGridChunks(c.maxSeq, c.headDim, d->dims.attnChunks);
     const TensorSlot xA = place(c.hidden * 4);
     const TensorSlot xB = place(c.hidden * 4);
     const TensorSlot xMid = place(c.hidden * 4);
@@ -440,7 +441,6 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->scratch.argValue = d->At<float>(argValue);
     d->scratch.argIndex = d->At<int32_t>(argIndex);
     d->argBlocks = LmHeadBlocks(d->dims);
-    d->mergeInOProj = MergeInOProj(d->dims);
     *out = d;
     return MUYO_OK;
 }

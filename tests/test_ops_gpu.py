@@ -513,18 +513,25 @@ def test_cpy_kv_cache_fill_and_shader_index_math(mh, gpu):
 # fp16 KV cache: rope + append, attention
 
 
-@pytest.mark.parametrize("shape", ["0.5b", "7b"])
-def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape):
+# Positions cover one key, chunk-size steps of the adaptive chunking (32/64 keys per chunk for
+# head_dim 64 around rows 1024..1025), several rounds per lane (long caches) and the last row.
+ATTN_CASES = [("0.5b", 2048, (0, 1, 31, 32, 63, 64, 255, 256, 257, 1000, 1023, 1024, 1025, 2047)),
+              ("7b", 2048, (0, 15, 16, 17, 511, 512, 513, 2040, 2047)),
+              ("0.5b", 8192, (4095, 8191)),
+              ("7b", 8192, (5000, 8191))]
+
+
+@pytest.mark.parametrize("shape,max_seq,positions", ATTN_CASES)
+def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape, max_seq, positions):
     torch = gpu
     heads, kv, hd = (14, 2, 64) if shape == "0.5b" else (28, 4, 128)
-    max_seq = 2048
     ts = mh.theta_scale(1e6, hd)
     scale = 1.0 / math.sqrt(hd)
     kc = torch.empty(kv * max_seq * hd, dtype=torch.float16, device="cuda")
     vc = torch.empty_like(kc)
     mh.check(mh.load().muyo_fill_normal_f16(kc.data_ptr(), kc.numel(), 31, 0.0, 1.0, stream(torch)))
     mh.check(mh.load().muyo_fill_normal_f16(vc.data_ptr(), vc.numel(), 32, 0.0, 1.0, stream(torch)))
-    for pos in (0, 63, 64, 255, 256, 257, 1000, 2047):
+    for pos in positions:
         q = orc.normal_f32(heads * hd, 100 + pos)
         k = orc.normal_f32(kv * hd, 200 + pos)
         v = orc.normal_f32(kv * hd, 300 + pos)
