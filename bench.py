@@ -32,6 +32,11 @@ sys.path.insert(0, str(ROOT / "muyo-llm_amd"))
 
 METRIC = "F16 GEMV+norm HBM GB/s (% of MI355X peak); Qwen2.5-0.5B-shape decode tok/s"
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per LM-head launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what the
+# counter reads for a 256 MiB device copy (profiles/lm_head_0.5b_pmc.md), and the L2 hit rate
+# (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)) of the same runs.
+LM_HEAD_TRAFFIC_BYTES = 273_149_422
+LM_HEAD_L2_HIT_RATE = 0.105
 
 
 def step_bytes(c: dict, position: int) -> int:
@@ -149,6 +154,52 @@ def cpu_baseline(shape, position, seconds, seed):
     }
 
 
+def kernel_only(mh, torch, which: str, launches: int) -> dict:
+    """Launch one kernel `launches` times back to back (for rocprofv3 kernel traces and counters).
+
+    lm_head: the 0.5B-shape LM-head kernel (272,884,224 algorithmic bytes per launch).
+    copy:    torch's device copy of 256 MiB f32 (268,435,456 bytes read + the same written), the
+             calibration for FETCH_SIZE / WRITE_SIZE.
+    """
+    stream = torch.cuda.current_stream()
+    b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if which == "lm_head":
+        shape = dict(mh.QWEN25_05B)
+        dec = mh.Decoder(mh.qwen2_config(**shape))
+        try:
+            dec.fill_random(20261201)
+            dec.set_state(1, 1, stream.cuda_stream)
+            for _ in range(3):
+                dec.enqueue_kernel("LM_HEAD", 0, stream.cuda_stream)
+            torch.cuda.synchronize()
+            b.record(stream)
+            for _ in range(launches):
+                dec.enqueue_kernel("LM_HEAD", 0, stream.cuda_stream)
+            e.record(stream)
+            torch.cuda.synchronize()
+        finally:
+            dec.close()
+        nbytes = lm_head_bytes(shape)
+    elif which == "copy":
+        n = 64 * 1024 * 1024
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        b.record(stream)
+        for _ in range(launches):
+            dst.copy_(src)
+        e.record(stream)
+        torch.cuda.synchronize()
+        nbytes = 2 * 4 * n
+    else:
+        raise ValueError(which)
+    ms = b.elapsed_time(e) / launches
+    return {"kernel": which, "launches": launches, "avg_ms": round(ms, 5), "bytes_per_launch": nbytes,
+            "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -158,6 +209,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape secondary figure")
+    ap.add_argument("--kernel-only", choices=["lm_head", "copy"],
+                    help="only launch one kernel back to back (for rocprofv3 traces and counters)")
+    ap.add_argument("--launches", type=int, default=20, help="launches for --kernel-only")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -172,6 +226,9 @@ def main() -> int:
 
     torch.cuda.set_device(0)
     mh.load()
+    if args.kernel_only:
+        print(json.dumps(kernel_only(mh, torch, args.kernel_only, args.launches)), flush=True)
+        return 0
     shape = dict(mh.QWEN25_05B)
     seed = 20261201
 
@@ -220,13 +277,14 @@ def main() -> int:
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "bytes_per_step": total_bytes // args.steps,
         "roofline": {
-            "kernel": "FusedMatVec<16,8,1,NormStage,LmHeadEpi> (final norm + tied LM head 151936x896 + argmax)",
+            "kernel": "FusedMatVec<16,8,1,true,NormStage,LmHeadEpi> (final norm + tied LM head 151936x896 + argmax)",
             "bound": "hbm",
             "achieved": round(lm_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": LM_HEAD_TRAFFIC_BYTES,
+            "l2_hit_rate": LM_HEAD_L2_HIT_RATE,
             "launch_ms": round(kern["lm_head_ms"], 5),
             "bytes_per_launch": lm_head_bytes(shape),
         },
