@@ -64,8 +64,8 @@ typedef struct MuyoMatVecSpec
 } MuyoMatVecSpec;
 
 /* mul_mat_vec_f16_f32_f32 (CMakeLists.txt:168-172; shaders/llama/mul_mat_vec.comp:248-264).
- * Replaces the GEMV node of src/MatVec.cpp:112-172 and the projection nodes of
- * src/FullModel.cpp:133-175,237-253,347-418,474-485.
+ * Replaces the GEMV node of src/MatVec.cpp:112-159 and the projection nodes (QKV, o, gate, up,
+ * down, LM head) that src/FullModel.cpp builds with MatVecSpec/MatVecExecute (:133-175).
  *   d[batch][row] = sum_k f32(A[batchA][row*ncols + k]) * B[batch][k]
  *                   (+ FUSE0[...] if BIAS0) (+ FUSE1[...] if BIAS1)
  * Rows computed: [0, min(numRows*x*z, strideD)); batches: y. As in the shader, the A row stride
@@ -76,14 +76,14 @@ int muyo_mul_mat_vec_f16_f32_f32(const LlamaMatVecPushConstants* pc, const MuyoM
                                  uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* mul_mat_vec_f32_f32_f32 (CMakeLists.txt:174-178): same contract with F32 A. This is the
- * GQA-batched attention GEMV of src/FullModel.cpp:294-345 (scores over the key cache with
- * dispatch x = position + 1, and values over the transposed value cache). */
+ * GQA-batched attention GEMV of src/FullModel.cpp:793-812 (scores over the key cache with
+ * dispatch x = position + 1) and :825-844 (values over the transposed value cache). */
 int muyo_mul_mat_vec_f32_f32_f32(const LlamaMatVecPushConstants* pc, const MuyoMatVecSpec* spec, const float* a,
                                  const float* b, float* d, const float* fuse0, const float* fuse1, uint32_t dispatch_x,
                                  uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* rms_norm_f32 (CMakeLists.txt:117-121; shaders/llama/rms_norm.comp:53-151). Replaces
- * src/RmsNorm.cpp:112-160 and src/FullModel.cpp:215-247. One output row per dispatched
+ * src/RmsNorm.cpp:91-154 and src/FullModel.cpp:215-247. One output row per dispatched
  * workgroup (x = rows, y = channels, z = samples):
  *   d = x * rsqrt(mean(x^2) + param1) [* w]   (w when do_multiply != 0)
  * `partial_sums` is the shader's declared-but-unread binding 3 and may be NULL. */
@@ -98,42 +98,42 @@ int muyo_rms_norm_f32_f16w(const LlamaAddPushConstants* pc, uint32_t do_multiply
                            uint32_t dispatch_z, void* stream);
 
 /* add_f32 (CMakeLists.txt:110-115; shaders/llama/add.comp:23-46). Replaces
- * src/ElementwiseAdd.cpp:100-190 and src/FullModel.cpp:250-284. d = a + b over the dispatched
+ * src/ElementwiseAdd.cpp:123-162 and src/FullModel.cpp:250-284. d = a + b over the dispatched
  * element range, B broadcast by modulo unless norepeat != 0. ADD_RMS is off (as compiled by the
  * reference), so partial_sums is not written and may be NULL. Canonical dispatch: (1, ceil(ne/512), z). */
 int muyo_add_f32(const LlamaAddPushConstants* pc, uint32_t norepeat, const float* a, const float* b, float* d,
                  float* partial_sums, uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* swiglu_f32 (CMakeLists.txt:130-134; shaders/llama/swiglu.comp + glu_main.glsl). Replaces
- * src/Swiglu.cpp:100-160 and src/FullModel.cpp:287-327. d = silu(a) * b in the mode of
+ * src/Swiglu.cpp:94-145 and src/FullModel.cpp:287-327. d = silu(a) * b in the mode of
  * `pc->mode`. Index quotients use the divisors the ne2_* fastdiv words encode (as the shader
  * does); a word pair that is init_fastdiv_values of no divisor (e.g. zeroed) is MUYO_E_CONTRACT. */
 int muyo_swiglu_f32(const LlamaGluPushConstants* pc, const float* a, const float* b, float* d, uint32_t dispatch_x,
                     uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* rope_neox_f32 (CMakeLists.txt:123-128; shaders/llama/rope_neox.comp, rope_funcs.glsl:76-114).
- * Replaces src/Rope.cpp:95-160 and src/FullModel.cpp:179-212 (q rope and the k rope that writes
- * into the key cache through nb11/dOffset). Positions are int32 per i2; `ff` is read only when
+ * Replaces src/Rope.cpp:96-153 and src/FullModel.cpp:179-212 (q rope, and the k rope of
+ * :771-784 that writes into the key cache through nb11/dOffset). Positions are int32 per i2; `ff` is read only when
  * hasFf != 0 and `set_rows` (uint32 pairs) only when setRowsStride != 0. */
 int muyo_rope_neox_f32(const LlamaRopePushConstants* pc, const float* x, const int32_t* positions, const float* ff,
                        float* d, const uint32_t* set_rows, uint32_t dispatch_x, uint32_t dispatch_y,
                        uint32_t dispatch_z, void* stream);
 
 /* soft_max_f32 (CMakeLists.txt:161-163; shaders/llama/soft_max.comp:41-172). Replaces
- * src/SoftMax.cpp:75-140 and src/FullModel.cpp:331-349. Row r = z*262144 + y*512 + x of the
+ * src/SoftMax.cpp:85-128 and src/FullModel.cpp:331-349. Row r = z*262144 + y*512 + x of the
  * dispatch, bounded by nrowsX: d = softmax(x*scale + slope*mask [, sink]). */
 int muyo_soft_max_f32(const LlamaSoftMaxPushConstants* pc, const float* x, const float* mask, const float* sinks,
                       float* d, uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* argmax_f32 (CMakeLists.txt:148-150; shaders/llama/argmax.comp:20-60). Replaces
- * src/Argmax.cpp:75-120 and src/FullModel.cpp:461-484. d[row] = index of the largest of the KX
+ * src/Argmax.cpp:74-106 and src/FullModel.cpp:461-484. d[row] = index of the largest of the KX
  * values of row `row` (< KY). Ties resolve to the LOWEST index, which is the rule of the host
  * greedy scan the reference actually samples with (src/Sampler.cpp:32-43). */
 int muyo_argmax_f32(const LlamaGenericHeadPushConstants* pc, const float* a, int32_t* d, uint32_t dispatch_x,
                     uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* get_rows_f16_f32 / get_rows_f32 (CMakeLists.txt:136-146; shaders/llama/get_rows.comp:8-42).
- * Replace src/GetRows.cpp:95-150 and src/FullModel.cpp:424-458: d[i10][:] = f32(A[idx[i10]][:]).
+ * Replace src/GetRows.cpp:84-139 and src/FullModel.cpp:424-458: d[i10][:] = f32(A[idx[i10]][:]).
  * A row index outside [0, ne01) gives a zero row instead of an out-of-bounds read. */
 int muyo_get_rows_f16_f32(const LlamaAddPushConstants* pc, const void* a, const int32_t* b, float* d,
                           uint32_t dispatch_x, uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
@@ -141,7 +141,7 @@ int muyo_get_rows_f32(const LlamaAddPushConstants* pc, const float* a, const int
                       uint32_t dispatch_y, uint32_t dispatch_z, void* stream);
 
 /* cpy_f32_f32 (CMakeLists.txt:156-159; shaders/llama/copy.comp + generic_unary_head.glsl).
- * Replaces the value-column append of src/FullModel.cpp:353-420 and src/KvCache.cpp:181-226:
+ * Replaces the value-column append of src/FullModel.cpp:353-420 and src/KvCache.cpp:184-225:
  * d[doff + dst_idx(i)] = a[aoff + src0_idx(i)], i < ne. As in the shader, the quotients of
  * src0_idx/dst_idx use the divisors the fastdiv words encode (shifts packed outermost divisor
  * first) and the offsets use the shapes; a pair that encodes no divisor is MUYO_E_CONTRACT and
@@ -151,13 +151,14 @@ int muyo_cpy_f32_f32(const LlamaCopyPushConstants* pc, const float* a, float* d,
 
 /* ---------------------------------------------------------------------------------------------
  * Decode-step attention over an fp16 KV cache (no single reference node: it replaces the
- * k_rope -> kcache, v_copy -> vcache, attn_scores, attn_weights and attn_output nodes of
- * src/FullModel.cpp:258-345 for one layer).
+ * attn_scores, attn_softmax and attn_values nodes of src/FullModel.cpp:793-844 for one layer;
+ * the reference computes the same with f32 caches, src/Attention.cpp:253-294).
  * Layout: kcache/vcache are [kv_heads][max_seq][head_dim] fp16; q is [heads][head_dim] f32.
  * For every query head h (kv head h / (heads/kv_heads)):
  *   out[h] = sum_{j<=pos} softmax_j(scale * q[h].k[j]) * v[j]
- * `positions` is a device int32 (the cache row of the current token; keys 0..pos are read).
- * The caller appends k/v of the current token before this call (muyo_kv_append_f16).
+ * `position` is a device int32 (the cache row of the current token; keys 0..pos are read).
+ * The caller appends k/v of the current token before this call (muyo_rope_append_f16kv).
+ * max_seq <= 32768; q and the caches 16-byte aligned.
  * ------------------------------------------------------------------------------------------- */
 int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* vcache, float* out,
                                 const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
@@ -165,14 +166,14 @@ int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* 
 
 /* Rope k (NeoX, theta = pos * theta_scale^j) and append k and v of the current token, as fp16,
  * at row `*position` of the [kv_heads][max_seq][head_dim] caches; q is roped into q_out. This
- * is the q_rope + k_rope + v_copy node trio of src/FullModel.cpp:258-292 for an fp16 cache. */
+ * is the q rope + k rope + v copy node trio of src/FullModel.cpp:756-795 for an fp16 cache. */
 int muyo_rope_append_f16kv(const float* q, const float* k, const float* v, float* q_out, void* kcache, void* vcache,
                            const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
                            uint32_t max_seq, float theta_scale, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
- * Decoder: the composed decode step (src/FullModel.cpp:487-1292 RunFullModel's graph plus its
- * feedToken/sampleNext loop, minus GGUF loading and tokenisation). Device memory is owned by the
+ * Decoder: the composed decode step (RunFullModel's graph, src/FullModel.cpp:685-998, plus its
+ * feedToken/sampleNext loop, :1096-1117, minus GGUF loading and tokenisation). Device memory is owned by the
  * decoder; the step is captured once into a hipGraph and replayed per token with the token and
  * position held in device memory.
  * ------------------------------------------------------------------------------------------- */

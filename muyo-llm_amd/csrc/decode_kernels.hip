@@ -1,6 +1,6 @@
 // Fused decode-step kernels for gfx950.
 //
-// One step (the reference records 18 nodes per layer, src/FullModel.cpp:227-498):
+// One step (the reference records 18 nodes per layer, src/FullModel.cpp:726-993):
 //   BeginStep      : greedy id of the previous step from the LM head's per-workgroup partials,
 //                    step bookkeeping (position, generated-id ring), embedding row -> f32 x
 //   per layer:

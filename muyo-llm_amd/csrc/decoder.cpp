@@ -1,6 +1,6 @@
 // The decode-step executor behind the muyo_decoder_* C ABI.
 //
-// It plays the role of RunFullModel's render graph (src/FullModel.cpp:487-1010) plus its
+// It plays the role of RunFullModel's render graph (src/FullModel.cpp:685-998) plus its
 // feedToken/sampleNext loop (:1096-1117): one arena of device memory holds every weight, the
 // fp16 KV cache and the activations; one step is 2 + 5 * layers launches on one stream
 // (6 per layer when the attention partials need their own merge kernel; decode_kernels.hip).

@@ -446,7 +446,7 @@ void oracle_attention_f16kv(const float* q, const uint16_t* kcache, const uint16
 }
 
 /* ------------------------------------------------------------------------------------------ */
-/* Decode step: tools/reference_qwen2.py:107-166 in the node order of src/FullModel.cpp:186-498. */
+/* Decode step: tools/reference_qwen2.py:107-166 in the node order of src/FullModel.cpp:726-993. */
 
 void oracle_decode_layer(const OracleQwen2* m, uint32_t l, const float* x, int32_t pos, float* out)
 {

@@ -7,7 +7,7 @@
  *
  * Every op restates the reference's own CPU reference loop (muyo-llm, src/ *.cpp), cited per
  * function. The decode step restates tools/reference_qwen2.py:100-166 in the node order of
- * src/FullModel.cpp:186-498, with double accumulation for the GEMV/attention sums so that
+ * src/FullModel.cpp:726-993, with double accumulation for the GEMV/attention sums so that
  * greedy ids are robust to summation order.
  *
  * Pins (how each function is checked independently of its own formula) are listed in the

@@ -102,7 +102,7 @@ def test_matvec_generic_path_and_row_bounds(mh, gpu, orc):
 
 
 def test_matvec_f32_gqa_score_and_value_gemvs(mh, gpu, orc):
-    """The attention GEMVs of src/FullModel.cpp:294-345 on an f32 cache, via batch/broadcast."""
+    """The attention GEMVs of src/FullModel.cpp:793-812 (scores) and :825-844 (values) on an f32 cache, via batch/broadcast."""
     torch = gpu
     heads, kv, hd, max_seq, pos = 14, 2, 64, 2048, 300
     gqa = heads // kv
@@ -380,7 +380,7 @@ def test_rope_batched_decode_shape(mh, gpu, orc):
 
 
 def test_rope_into_key_cache_row(mh, gpu, orc):
-    """k_rope of src/FullModel.cpp:272-285: rows strided by hd*max_seq, dOffset = pos*hd; bit-exact slots."""
+    """k_rope of src/FullModel.cpp:771-784: rows strided by hd*max_seq, dOffset = pos*hd; bit-exact slots."""
     torch = gpu
     kv, hd, max_seq, pos = 2, 64, 2048, 1234
     k = orc.normal_f32(kv * hd, 21)
