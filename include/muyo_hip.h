@@ -284,6 +284,14 @@ int muyo_decoder_set_state(MuyoDecoder* decoder, int32_t token, int32_t position
  * `stream`, with the decoder's buffers and current device state. */
 int muyo_decoder_enqueue_kernel(MuyoDecoder* decoder, uint32_t kernel, uint32_t layer, void* stream);
 
+/* The reference's node self-tests (`int RunX()` of src/{MatVec,RmsNorm,Rope,SoftMax,Argmax,
+ * ElementwiseAdd,Swiglu,GetRows,KvCache,Attention}.cpp, C++ declarations in include/muyo/) by
+ * the reference CLI's mode names (src/main.cpp:246-248): "--add", "--matvec", "--rmsnorm", "--rope",
+ * "--swiglu", "--getrows", "--argmax", "--softmax", "--attention", "--kvcache", or "--smoke" for
+ * all. Runs on the current device, synchronously. Returns 0 when every selected test matches its
+ * CPU reference, 1 when one does not, MUYO_E_RANGE for an unknown mode. */
+int muyo_self_test(const char* mode);
+
 /* ---------------------------------------------------------------------------------------------
  * Synthetic-input helpers (portable seeded generator; bit-identical on host and device).
  *   word(seed, i)   = mix64(mix64(seed) + i)            mix64 = SplitMix64's finaliser

@@ -150,6 +150,7 @@ _SIGNATURES = {
     "muyo_decoder_launches_per_step": (u32, [vp]),
     "muyo_decoder_set_state": (ctypes.c_int, [vp, i32, i32, vp]),
     "muyo_decoder_enqueue_kernel": (ctypes.c_int, [vp, u32, u32, vp]),
+    "muyo_self_test": (ctypes.c_int, [ctypes.c_char_p]),
     "muyo_fill_normal_f16": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_normal_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_uniform_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, vp]),

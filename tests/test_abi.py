@@ -103,3 +103,50 @@ def test_step_bytes_match_the_published_derivation():
     s7 = dict(mh.QWEN25_7B)
     w7 = s7["layers"] * 2 * (4608 * 3584 + 3584 * 3584 + 3 * 18944 * 3584) + 2 * 152064 * 3584
     assert w7 == 14_140_571_648
+
+
+def test_node_factories_fill_like_the_reference(tmp_path, mh):
+    """include/muyo/Nodes.h compiles as C++ and its Make* fills equal the Python mirror's word for
+    word (the fills the GPU parity tests use, each citing the reference factory it restates)."""
+    probe = tmp_path / "nodes.cpp"
+    probe.write_text(r'''
+#include <cstdio>
+#include "muyo/Nodes.h"
+using namespace muyo_llm::hip;
+template <typename T> void Dump(const char* name, const T& pc) {
+    const unsigned char* p = reinterpret_cast<const unsigned char*>(&pc);
+    std::printf("%s ", name);
+    for (size_t i = 0; i < sizeof(T); ++i) std::printf("%02x", p[i]);
+    std::printf("\n");
+}
+int main() {
+    Dump("matvec", MakeMatVec(896, 1152, LLAMA_MAT_VEC_FUSION_BIAS0));
+    Dump("rows", MakeRows(896, 4, 1e-6F));
+    Dump("add", MakeAdd(1000));
+    Dump("swiglu", MakeSwiglu(600));
+    Dump("rope", MakeRopeNeox(2, 64, 1e6F, 64 * 2048, 1234 * 64));
+    Dump("softmax", MakeSoftMax(14, 2048, 0.125F));
+    Dump("argmax", MakeArgmax(151936));
+    Dump("getrows", MakeGetRows(896, 151936));
+    Dump("valuecol", MakeValueColumn(128, 64, 2048, 5));
+    return 0;
+}
+''')
+    exe = tmp_path / "nodes"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(probe), "-o", str(exe)],
+                   check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                       check=True).stdout.splitlines())
+    want = {
+        "matvec": mh.mat_vec_push_constants(896, 1152, fusion_flags=mh.FUSION_BIAS0),
+        "rows": mh.rows_push_constants(896, 4, 1e-6),
+        "add": mh.add_push_constants(1000),
+        "swiglu": mh.glu_push_constants(600),
+        "rope": mh.rope_push_constants(2, 64, 1e6, output_row_stride=64 * 2048, destination_offset=1234 * 64),
+        "softmax": mh.soft_max_push_constants(14, 2048, 0.125),
+        "argmax": mh.argmax_push_constants(151936),
+        "getrows": mh.get_rows_push_constants(896, 151936),
+        "valuecol": mh.value_column_push_constants(128, 64, 2048, 5),
+    }
+    for name, pc in want.items():
+        assert got[name] == mh.contract_bytes(pc).hex(), name

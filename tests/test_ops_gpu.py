@@ -575,3 +575,24 @@ def test_generator_matches_oracle_bits(mh, gpu, orc):
     assert np.array_equal(host(f), orc.normal_f32(n, 6, 1.0, 0.1))
     assert np.array_equal(host(u), orc.uniform_f32(n, 7))
     assert mh.tensor_seed(1, "FFN_UP", 3) == orc.tensor_seed(1, "FFN_UP", 3)
+
+
+# ------------------------------------------------------------------------------------------------
+# the reference's node self-tests (RunX), through the C ABI and the muyo_llm CLI
+
+
+@pytest.mark.parametrize("mode", ["--add", "--matvec", "--rmsnorm", "--rope", "--swiglu", "--getrows", "--argmax",
+                                  "--softmax", "--attention", "--kvcache"])
+def test_reference_self_tests(mh, gpu, mode):
+    assert mh.load().muyo_self_test(mode.encode()) == 0
+
+
+def test_self_test_cli_smoke(mh, gpu):
+    import pathlib
+    import subprocess
+
+    cli = pathlib.Path(mh.__file__).resolve().parent / "muyo_llm"
+    done = subprocess.run([str(cli), "--smoke"], capture_output=True, text=True, timeout=120)
+    assert done.returncode == 0, done.stdout + done.stderr
+    assert done.stdout.count("OK:") == 10
+    assert mh.load().muyo_self_test(b"--nope") == mh.MUYO_E_RANGE
