@@ -575,20 +575,33 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     }
     const uint32_t nchunks = cols / 8;
     const size_t lds = static_cast<size_t>(cols) * sizeof(float);
-    const RowShape shape = PickRowShape(nchunks, kNr);
+    const RowShape shape = PickFusedShape(nchunks, kNr);
 #define MUYO_FUSED_CASE(L, C)                                                                                    \
     if (shape.lpr == L && shape.cpl == C && nchunks <= L * C)                                                    \
     {                                                                                                            \
         return LaunchFusedT<L, C, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
     }
+    MUYO_FUSED_CASE(8, 7)
     MUYO_FUSED_CASE(8, 8)
+    MUYO_FUSED_CASE(16, 7)
     MUYO_FUSED_CASE(16, 8)
+    MUYO_FUSED_CASE(32, 7)
     MUYO_FUSED_CASE(32, 8)
-    MUYO_FUSED_CASE(32, 16)
-    if constexpr (kNr == 1)
+    if constexpr (kNr == 2)
     {
+        MUYO_FUSED_CASE(32, 10)
+        MUYO_FUSED_CASE(32, 12)
+        MUYO_FUSED_CASE(32, 14)
+        MUYO_FUSED_CASE(32, 16)
+        return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+    }
+    else
+    {
+        MUYO_FUSED_CASE(64, 7)
         MUYO_FUSED_CASE(64, 8)
+        MUYO_FUSED_CASE(64, 10)
         MUYO_FUSED_CASE(64, 12)
+        MUYO_FUSED_CASE(64, 14)
         MUYO_FUSED_CASE(64, 16)
 #undef MUYO_FUSED_CASE
         const uint32_t cpl = CeilDiv(nchunks, static_cast<uint32_t>(kBlock));
@@ -603,10 +616,6 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
         MUYO_BLOCK_ROW_CASE(16)
         MUYO_BLOCK_ROW_CASE(20)
 #undef MUYO_BLOCK_ROW_CASE
-    }
-    else
-    {
-        return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
     }
     return hipErrorInvalidValue;
 }
@@ -709,13 +718,15 @@ __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, con
 }
 
 // ------------------------------------------------------------------------------------------------
-// Attention over the fp16 cache: one workgroup per (chunk of keys, kv head).
+// Attention over the fp16 cache: one workgroup per (chunk of keys, kv head, query head of its
+// GQA group).
 //
 // The 256 lanes form kSlices groups of kRC = headDim/8 lanes; a group owns one key at a time and
 // each of its lanes one 16-byte slice of that key's K and V rows, which stay in registers (the
 // next keys' rows are requested before the current ones are used). A group keeps its own online
-// softmax per query head of the GQA group (max, sum, 8 channels of P.V per lane); at the end the
-// groups are combined through LDS and the chunk's partials written for the merge.
+// softmax (max, sum, 8 channels of P.V per lane); at the end the groups are combined through LDS
+// and the chunk's partials written for the merge. The query heads of a group read the same K/V
+// chunk (from L2 after the first), which buys parallelism: the work per lane is one head's.
 
 template <int kHd>
 __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict__ q, const uint16_t* __restrict__ kc,
@@ -727,12 +738,13 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     constexpr int kRC = kHd / 8;           // lanes per key
     constexpr int kSlices = kBlock / kRC;  // keys side by side
     constexpr int kKpt = 2;                // keys per lane per round
+    constexpr int kPad = kHd + 4;          // LDS row stride: slices of one lane position differ in bank
     static_assert(kSlices == 2048 / kHd, "slice count must match AttnSlices");
-    extern __shared__ float combine[];     // [kSlices][group][kHd]
-    __shared__ float sliceMax[kSlices][kMaxGroup];
-    __shared__ float sliceSum[kSlices][kMaxGroup];
-    __shared__ float headMax[kMaxGroup];
-    __shared__ float headSum[kMaxGroup];
+    __shared__ float combine[kSlices * kPad];
+    __shared__ float sliceMax[kSlices];
+    __shared__ float sliceSum[kSlices];
+    __shared__ float headMax;
+    __shared__ float headSum;
 
     const int32_t pos = *position;
     if (pos < 0 || static_cast<uint32_t>(pos) >= maxSeq)
@@ -747,6 +759,7 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         return;
     }
     const uint32_t g = blockIdx.y;
+    const uint32_t h = blockIdx.z;
     const uint32_t c0 = chunk * chunkKeys;
     const uint32_t cn = min(chunkKeys, keys - c0);
     const uint32_t slice = threadIdx.x / kRC;
@@ -768,77 +781,53 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     };
     half8 ka[kKpt], va[kKpt], kb[kKpt], vb[kKpt];
     load(0, ka, va);
+    const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + h) * kHd) + part * 2;
+    const float4 q0 = qh[0];
+    const float4 q1 = qh[1];
 
-    float4 q0[kMaxGroup], q1[kMaxGroup];
+    float m = -INFINITY;
+    float l = 0.0f;
+    float acc[8];
 #pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
+    for (int c = 0; c < 8; ++c)
     {
-        const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + min(h, static_cast<int>(group) - 1)) * kHd) + part * 2;
-        q0[h] = qh[0];
-        q1[h] = qh[1];
+        acc[c] = 0.0f;
     }
-    float m[kMaxGroup], l[kMaxGroup], acc[kMaxGroup][8];
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-    {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-        {
-            acc[h][c] = 0.0f;
-        }
-    }
-
     auto consume = [&](uint32_t r, const half8(&kk)[kKpt], const half8(&vv)[kKpt]) {
-        bool valid[kKpt];
+        float s[kKpt];
+        float top = m;
 #pragma unroll
         for (int k = 0; k < kKpt; ++k)
         {
-            valid[k] = (r * kKpt + k) * kSlices + slice < cn;
+            s[k] = GroupSum<kRC>(DotChunk(kk[k], q0, q1, 0.0f)) * scale;
+            s[k] = (r * kKpt + k) * kSlices + slice < cn ? s[k] : -INFINITY;
+            top = fmaxf(top, s[k]);
         }
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
+        if (top == -INFINITY)
         {
-            if (h >= static_cast<int>(group))
-            {
-                break;  // uniform over the workgroup
-            }
-            float s[kKpt];
-            float top = m[h];
+            return;  // no valid key for this group yet
+        }
+        const float factor = expf(m - top);  // 0 while m is still -inf
+        m = top;
+        float p[kKpt];
+        float psum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kKpt; ++k)
+        {
+            p[k] = expf(s[k] - top);
+            psum += p[k];
+        }
+        l = fmaf(l, factor, psum);
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+        {
+            float a = acc[c] * factor;
 #pragma unroll
             for (int k = 0; k < kKpt; ++k)
             {
-                s[k] = GroupSum<kRC>(DotChunk(kk[k], q0[h], q1[h], 0.0f)) * scale;
-                s[k] = valid[k] ? s[k] : -INFINITY;
-                top = fmaxf(top, s[k]);
+                a = fmaf(p[k], static_cast<float>(vv[k][c]), a);
             }
-            if (top == -INFINITY)
-            {
-                continue;  // no valid key for this group yet
-            }
-            const float factor = expf(m[h] - top);  // 0 while m is still -inf
-            m[h] = top;
-            float p[kKpt];
-            float psum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < kKpt; ++k)
-            {
-                p[k] = expf(s[k] - top);
-                psum += p[k];
-            }
-            l[h] = fmaf(l[h], factor, psum);
-#pragma unroll
-            for (int c = 0; c < 8; ++c)
-            {
-                float a = acc[h][c] * factor;
-#pragma unroll
-                for (int k = 0; k < kKpt; ++k)
-                {
-                    a = fmaf(p[k], static_cast<float>(vv[k][c]), a);
-                }
-                acc[h][c] = a;
-            }
+            acc[c] = a;
         }
     };
 
@@ -860,61 +849,48 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         consume(r + 1, kb, vb);
     }
 
-    // Combine the slices: per-head chunk max and sum, then the rescaled P.V summed over slices.
+    // Combine the slices: the chunk's max and sum (wave 0), then the rescaled P.V summed over
+    // slices.
     if (part == 0)
     {
-#pragma unroll
-        for (int h = 0; h < kMaxGroup; ++h)
-        {
-            sliceMax[slice][h] = m[h];
-            sliceSum[slice][h] = l[h];
-        }
+        sliceMax[slice] = m;
+        sliceSum[slice] = l;
     }
     __syncthreads();
+    if (threadIdx.x < kWave)
     {
-        // One wave per head; lane i holds slice i.
-        const int lane = threadIdx.x & (kWave - 1);
-        for (uint32_t h = threadIdx.x / kWave; h < group; h += kWaves)
+        const int lane = threadIdx.x;
+        const float mi = lane < kSlices ? sliceMax[lane] : -INFINITY;
+        const float top = GroupMax<kSlices>(mi);
+        const float li = (lane < kSlices && mi != -INFINITY) ? sliceSum[lane] * expf(mi - top) : 0.0f;
+        const float sum = GroupSum<kSlices>(li);
+        if (lane == 0)
         {
-            const float mi = lane < kSlices ? sliceMax[lane][h] : -INFINITY;
-            const float top = GroupMax<kSlices>(mi);
-            const float li = (lane < kSlices && mi != -INFINITY) ? sliceSum[lane][h] * expf(mi - top) : 0.0f;
-            const float sum = GroupSum<kSlices>(li);
-            if (lane == 0)
-            {
-                headMax[h] = top;
-                headSum[h] = sum;
-            }
+            headMax = top;
+            headSum = sum;
         }
     }
     __syncthreads();
-#pragma unroll
-    for (int h = 0; h < kMaxGroup; ++h)
-    {
-        if (h < static_cast<int>(group))
-        {
-            const float f = m[h] == -INFINITY ? 0.0f : expf(m[h] - headMax[h]);
-            float4* dst = reinterpret_cast<float4*>(combine + (static_cast<uint32_t>(slice) * group + h) * kHd + part * 8);
-            dst[0] = make_float4(acc[h][0] * f, acc[h][1] * f, acc[h][2] * f, acc[h][3] * f);
-            dst[1] = make_float4(acc[h][4] * f, acc[h][5] * f, acc[h][6] * f, acc[h][7] * f);
-        }
-    }
+    const float f = m == -INFINITY ? 0.0f : expf(m - headMax);
+    float4* dst = reinterpret_cast<float4*>(combine + slice * kPad + part * 8);
+    dst[0] = make_float4(acc[0] * f, acc[1] * f, acc[2] * f, acc[3] * f);
+    dst[1] = make_float4(acc[4] * f, acc[5] * f, acc[6] * f, acc[7] * f);
     __syncthreads();
-    const uint64_t slot = static_cast<uint64_t>(g) * gridDim.x + chunk;
-    for (uint32_t item = threadIdx.x; item < group * kHd; item += kBlock)
+    const uint64_t slot = (static_cast<uint64_t>(g) * gridDim.x + chunk) * group + h;
+    for (uint32_t d = threadIdx.x; d < kHd; d += kBlock)
     {
         float sum = 0.0f;
 #pragma unroll 8
         for (int i = 0; i < kSlices; ++i)
         {
-            sum += combine[i * group * kHd + item];
+            sum += combine[i * kPad + d];
         }
-        sc.attnAcc[slot * group * kHd + item] = sum;
+        sc.attnAcc[slot * kHd + d] = sum;
     }
-    if (threadIdx.x < group)
+    if (threadIdx.x == 0)
     {
-        sc.attnMax[slot * group + threadIdx.x] = headMax[threadIdx.x];
-        sc.attnSum[slot * group + threadIdx.x] = headSum[threadIdx.x];
+        sc.attnMax[slot] = headMax;
+        sc.attnSum[slot] = headSum;
     }
 }
 
@@ -1073,21 +1049,8 @@ hipError_t LaunchAttentionT(hipStream_t s, const DecodeDims& dims, const float* 
                             const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch)
 {
     const uint32_t group = dims.heads / dims.kvHeads;
-    const size_t lds = static_cast<size_t>(AttnSlices(kHd)) * group * kHd * sizeof(float);
-    static size_t configured = 64 * 1024;
-    if (lds > configured)
-    {
-        const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(&AttentionChunk<kHd>),
-                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                      static_cast<int>(lds));
-        if (status != hipSuccess)
-        {
-            return status;
-        }
-        configured = lds;
-    }
-    const dim3 grid(AttnGridChunks(dims.maxSeq, kHd, dims.attnChunks), dims.kvHeads, 1);
-    hipLaunchKernelGGL(AttentionChunk<kHd>, grid, dim3(kBlock), lds, s, q, kcache, vcache, position, group, dims.maxSeq,
+    const dim3 grid(AttnGridChunks(dims.maxSeq, kHd, dims.attnChunks), dims.kvHeads, group);
+    hipLaunchKernelGGL(AttentionChunk<kHd>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group, dims.maxSeq,
                        dims.attnChunks, dims.attnScale, scratch);
     return hipGetLastError();
 }

@@ -50,7 +50,7 @@ struct DecodeScratch
 };
 
 constexpr uint32_t kArgMaxBlocks = 1024;
-constexpr uint32_t kMaxAttnChunks = 32;    // attention workgroups per kv head, at most
+constexpr uint32_t kMaxAttnChunks = 16;    // attention chunks per kv head, at most
 constexpr uint32_t kMergeAttnChunks = 16;  // the same when o_proj's prologue merges the partials
 constexpr uint32_t kMaxSeq = 32768;
 

@@ -236,4 +236,27 @@ inline RowShape PickRowShape(uint32_t nchunks, int nr)
     }
     return {64, 16};
 }
+
+/// The fused decode GEMVs' shape: the fewest chunks per lane that cover the row in one batch at
+/// the lane count PickRowShape would use, so short rows waste no loads (e.g. 896 columns = 112
+/// chunks -> 16 lanes x 7; 3584 columns = 448 chunks -> 32 x 14 for two-row units, 64 x 7
+/// otherwise). Rows past one batch keep PickRowShape's shape.
+inline RowShape PickFusedShape(uint32_t nchunks, int nr)
+{
+    static constexpr int kCpls[] = {7, 8, 10, 12, 14, 16};
+    RowShape shape = PickRowShape(nchunks, nr);
+    if (nr == 1 && nchunks > 256 && nchunks <= 1024)
+    {
+        shape.lpr = 64;
+    }
+    for (int cpl : kCpls)
+    {
+        if (static_cast<uint32_t>(shape.lpr * cpl) >= nchunks)
+        {
+            shape.cpl = cpl;
+            return shape;
+        }
+    }
+    return shape;
+}
 }  // namespace muyo
