@@ -167,68 +167,79 @@ struct MergeStage
 // ------------------------------------------------------------------------------------------------
 // Fused GEMV: units of kNr rows, a staging policy, an epilogue per unit, an optional block tail.
 //
-// kSingle: a row fits one batch. Units are then double-buffered: the next unit's batch is
-// requested before the current one is consumed, so every wave keeps a batch in flight while it
-// computes. Otherwise each row streams through RowDot's ping-pong of batches.
+// kSingle (a row fits one batch): one segment of kLpr lanes streams all kNr rows of a unit. Each
+// lane keeps its activation chunks in registers (read from LDS once), and units are double-
+// buffered: the next unit's rows are requested before the current ones are consumed, so every
+// wave keeps a batch in flight while it computes. Otherwise the kNr rows of a unit sit in kNr
+// adjacent segments and each row streams through RowDot's ping-pong of batches.
+
+template <int kLpr, int kNr, bool kSingle>
+constexpr uint32_t UnitsPerWave()
+{
+    return kSingle ? kWave / kLpr : (kWave / kLpr) / kNr;
+}
 
 template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
 __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage, Epi epi)
 {
     extern __shared__ float4 xs[];
     const uint32_t nchunks = cols / 8;
-    constexpr int kSegs = kWave / kLpr;
-    constexpr int kUnits = kSegs / kNr;
+    constexpr int kUnits = UnitsPerWave<kLpr, kNr, kSingle>();
     static_assert(kUnits >= 1 && (kNr == 1 || kNr == 2), "a wave holds whole units of one or two rows");
     const int lane = threadIdx.x & (kWave - 1);
     const int segment = lane / kLpr;
     const uint32_t lir = lane % kLpr;
-    const int unitInWave = segment / kNr;
-    const int part = segment % kNr;
+    const int unitInWave = kSingle ? segment : segment / kNr;
+    const int part = kSingle ? 0 : segment % kNr;
     const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
     const uint32_t stride = gridDim.x * kWaves * kUnits;
     const uint32_t units = epi.Units();
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
-
-    // Every lane of a segment holds its row's sum; the unit's second row sits in the partner
-    // segment.
-    auto finish = [&](uint32_t unit, float dot) {
-        dot = GroupSum<kLpr>(dot);
-        float sums[kNr];
-        sums[0] = dot;
-        if constexpr (kNr == 2)
-        {
-            sums[1] = PartnerLane<kLpr>(dot);
-        }
-        if (unit < units && part == 0 && lir == 0)
-        {
-            epi.Finish(unit, sums, bestValue, bestIndex);
-        }
-    };
-
-    // Weights do not depend on the activation: start streaming them before it is staged.
     uint32_t first = wave * kUnits;
-    half8 wa[kCpl];
-    if (first + unitInWave < units)
-    {
-        LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, wa);
-    }
-    stage.Run(xs, cols);
-    const float4* lo = xs;
-    const float4* hi = xs + nchunks;
 
     if constexpr (kSingle)
     {
-        half8 wb[kCpl];
+        // Weights do not depend on the activation: start streaming them before it is staged.
+        half8 wa[kNr][kCpl];
+        half8 wb[kNr][kCpl];
+        auto load = [&](uint32_t unit, half8(&w)[kNr][kCpl]) {
+#pragma unroll
+            for (int r = 0; r < kNr; ++r)
+            {
+                LoadBatch<kLpr, kCpl>(epi.Row(unit, r), 0, nchunks, lir, w[r]);
+            }
+        };
+        if (first + unitInWave < units)
+        {
+            load(first + unitInWave, wa);
+        }
+        stage.Run(xs, cols);
+        float4 xlo[kCpl];
+        float4 xhi[kCpl];
+        LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
+        // Every lane of the segment ends with the unit's row sums.
+        auto finish = [&](uint32_t unit, const half8(&w)[kNr][kCpl]) {
+            float sums[kNr];
+#pragma unroll
+            for (int r = 0; r < kNr; ++r)
+            {
+                sums[r] = GroupSum<kLpr>(unit < units ? DotRegisters<kLpr, kCpl>(w[r], xlo, xhi, nchunks, lir) : 0.0f);
+            }
+            if (unit < units && lir == 0)
+            {
+                epi.Finish(unit, sums, bestValue, bestIndex);
+            }
+        };
         for (; first < units; first += 2 * stride)
         {
             const uint32_t ua = first + unitInWave;
             const uint32_t ub = ua + stride;
             if (ub < units)
             {
-                LoadBatch<kLpr, kCpl>(epi.Row(ub, part), 0, nchunks, lir, wb);
+                load(ub, wb);
             }
-            finish(ua, ua < units ? DotBatch<kLpr, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f) : 0.0f);
+            finish(ua, wa);
             if (first + stride >= units)
             {
                 break;
@@ -236,28 +247,48 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             const uint32_t uc = ub + stride;
             if (uc < units)
             {
-                LoadBatch<kLpr, kCpl>(epi.Row(uc, part), 0, nchunks, lir, wa);
+                load(uc, wa);
             }
-            finish(ub, ub < units ? DotBatch<kLpr, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f) : 0.0f);
+            finish(ub, wb);
         }
     }
     else
     {
+        half8 w[kCpl];
+        if (first + unitInWave < units)
+        {
+            LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
+        }
+        stage.Run(xs, cols);
+        const float4* lo = xs;
+        const float4* hi = xs + nchunks;
         for (; first < units; first += stride)
         {
             const uint32_t unit = first + unitInWave;
             float dot = 0.0f;
             if (unit < units)
             {
-                dot = RowDot<kLpr, kCpl>(epi.Row(unit, part), nchunks, lir, wa, lo, hi);
+                dot = RowDot<kLpr, kCpl>(epi.Row(unit, part), nchunks, lir, w, lo, hi);
             }
             // The next unit's first batch goes out before this unit's reduction and epilogue.
             const uint32_t next = first + stride + unitInWave;
             if (next < units)
             {
-                LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, wa);
+                LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, w);
             }
-            finish(unit, dot);
+            // Every lane of a segment holds its row's sum; the unit's second row sits in the
+            // partner segment.
+            dot = GroupSum<kLpr>(dot);
+            float sums[kNr];
+            sums[0] = dot;
+            if constexpr (kNr == 2)
+            {
+                sums[1] = PartnerLane<kLpr>(dot);
+            }
+            if (unit < units && part == 0 && lir == 0)
+            {
+                epi.Finish(unit, sums, bestValue, bestIndex);
+            }
         }
     }
     epi.Tail(bestValue, bestIndex);
@@ -551,7 +582,7 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
                         const Stage& stage, const Epi& epi, uint32_t* blocksOut)
 {
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
-        s, units, kWaves * ((kWave / kLpr) / kNr), blockCap, lds, cols, stage, epi, blocksOut);
+        s, units, kWaves * UnitsPerWave<kLpr, kNr, kSingle>(), blockCap, lds, cols, stage, epi, blocksOut);
 }
 
 template <int kCpl, class Stage, class Epi>
@@ -577,7 +608,7 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     const size_t lds = static_cast<size_t>(cols) * sizeof(float);
     const RowShape shape = PickFusedShape(nchunks, kNr);
 #define MUYO_FUSED_CASE(L, C)                                                                                    \
-    if (shape.lpr == L && shape.cpl == C && nchunks <= L * C)                                                    \
+    if (shape.lpr == L && shape.cpl == C)                                                                        \
     {                                                                                                            \
         return LaunchFusedT<L, C, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
     }
@@ -587,19 +618,16 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     MUYO_FUSED_CASE(16, 8)
     MUYO_FUSED_CASE(32, 7)
     MUYO_FUSED_CASE(32, 8)
+    MUYO_FUSED_CASE(64, 7)
+    MUYO_FUSED_CASE(64, 8)
+    MUYO_FUSED_CASE(64, 10)
     if constexpr (kNr == 2)
     {
-        MUYO_FUSED_CASE(32, 10)
-        MUYO_FUSED_CASE(32, 12)
-        MUYO_FUSED_CASE(32, 14)
-        MUYO_FUSED_CASE(32, 16)
+        // Rows past 640 chunks: the two rows of a unit in adjacent 32-lane segments.
         return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
     }
     else
     {
-        MUYO_FUSED_CASE(64, 7)
-        MUYO_FUSED_CASE(64, 8)
-        MUYO_FUSED_CASE(64, 10)
         MUYO_FUSED_CASE(64, 12)
         MUYO_FUSED_CASE(64, 14)
         MUYO_FUSED_CASE(64, 16)

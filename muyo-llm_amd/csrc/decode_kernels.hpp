@@ -51,7 +51,7 @@ struct DecodeScratch
 
 constexpr uint32_t kArgMaxBlocks = 1024;
 constexpr uint32_t kMaxAttnChunks = 16;    // attention chunks per kv head, at most
-constexpr uint32_t kMergeAttnChunks = 16;  // the same when o_proj's prologue merges the partials
+constexpr uint32_t kMergeAttnChunks = 8;   // the same when o_proj's prologue merges the partials
 constexpr uint32_t kMaxSeq = 32768;
 
 /// Keys one attention workgroup processes side by side: its 256 lanes hold one 16-byte slice of

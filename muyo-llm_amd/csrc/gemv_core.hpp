@@ -70,6 +70,38 @@ __device__ __forceinline__ float DotBatch(const half8 (&w)[kCpl], uint32_t base,
     return (a[0] + a[1]) + (a[2] + a[3]);
 }
 
+/// This lane's activation chunks (chunk lir + i*kLpr, clamped), read from LDS once and kept in
+/// registers: a lane meets the same columns in every row it processes.
+template <int kLpr, int kCpl>
+__device__ __forceinline__ void LoadActivation(const float4* __restrict__ lo, const float4* __restrict__ hi,
+                                               uint32_t nchunks, uint32_t lir, float4 (&xlo)[kCpl],
+                                               float4 (&xhi)[kCpl])
+{
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+    {
+        const uint32_t c = min(lir + i * kLpr, nchunks - 1);
+        xlo[i] = lo[c];
+        xhi[i] = hi[c];
+    }
+}
+
+/// One loaded single-batch row against the activation in registers (chunks past the row add
+/// nothing). The summation order is DotBatch's.
+template <int kLpr, int kCpl>
+__device__ __forceinline__ float DotRegisters(const half8 (&w)[kCpl], const float4 (&xlo)[kCpl],
+                                              const float4 (&xhi)[kCpl], uint32_t nchunks, uint32_t lir)
+{
+    float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+    {
+        const float part = DotChunk(w[i], xlo[i], xhi[i], 0.0f);
+        a[i & 3] += lir + i * kLpr < nchunks ? part : 0.0f;
+    }
+    return (a[0] + a[1]) + (a[2] + a[3]);
+}
+
 /// The whole row's dot product for this lane, given its first batch already loaded in `w`.
 /// Rows longer than one batch are double-buffered: batch k+1 is requested before batch k is
 /// consumed, so a long row costs about one memory latency plus its streaming time.
@@ -237,26 +269,25 @@ inline RowShape PickRowShape(uint32_t nchunks, int nr)
     return {64, 16};
 }
 
-/// The fused decode GEMVs' shape: the fewest chunks per lane that cover the row in one batch at
-/// the lane count PickRowShape would use, so short rows waste no loads (e.g. 896 columns = 112
-/// chunks -> 16 lanes x 7; 3584 columns = 448 chunks -> 32 x 14 for two-row units, 64 x 7
-/// otherwise). Rows past one batch keep PickRowShape's shape.
+/// The fused decode GEMVs' single-batch shape: one segment of `lpr` lanes streams every row of a
+/// unit, each lane `cpl` chunks per row with the fewest chunks that cover the row (e.g. 896
+/// columns = 112 chunks -> 16 lanes x 7; 3584 columns = 448 chunks -> 64 x 7; 4864 columns =
+/// 608 chunks -> 64 x 10). cpl 0 means the row does not fit one batch within the register budget
+/// of `nr` rows per unit.
 inline RowShape PickFusedShape(uint32_t nchunks, int nr)
 {
     static constexpr int kCpls[] = {7, 8, 10, 12, 14, 16};
-    RowShape shape = PickRowShape(nchunks, nr);
-    if (nr == 1 && nchunks > 256 && nchunks <= 1024)
-    {
-        shape.lpr = 64;
-    }
+    RowShape shape = PickRowShape(nchunks, 1);
+    const int maxCpl = nr == 1 ? 16 : 10;
     for (int cpl : kCpls)
     {
-        if (static_cast<uint32_t>(shape.lpr * cpl) >= nchunks)
+        if (cpl <= maxCpl && static_cast<uint32_t>(shape.lpr * cpl) >= nchunks)
         {
             shape.cpl = cpl;
             return shape;
         }
     }
+    shape.cpl = 0;
     return shape;
 }
 }  // namespace muyo
