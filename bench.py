@@ -16,7 +16,12 @@ roofline: the LM-head kernel (rms_norm prologue + 151936 x 896 fp16 GEMV + argma
 single launch, 272 MB, bigger than the 256 MB MALL), timed alone with HIP events on its stream.
 
 cpu_baseline: the CPU oracle's decode step (oracle/, a C restatement of the reference's CPU
-path) on one host core, over a bounded sample of steps of the same workload.
+path) on one host core, over a bounded sample of steps of the same workload; the same on all
+the process's cores (OpenMP over GEMV rows, at most 16) is reported beside it.
+
+kernels: per-launch figures of the per-op launchers at the batched element-wise/reduction shapes
+and the decode GEMV suite (inputs under 256 MB rotated over >= 512 MB of copies), and torch's
+device copy for reference.
 """
 from __future__ import annotations
 
@@ -123,34 +128,173 @@ def time_kernels(mh, torch, shape, seed, rounds):
     return out
 
 
+def time_ops(mh, torch, reps: int = 10) -> dict:
+    """Per-launch time of each per-op launcher at the batched shapes of the element-wise and
+    reduction set (4096 rows at Qwen2.5-0.5B widths) and of the decode GEMV suite, through the C
+    ABI with the reference's push-constant fills. Inputs smaller than 256 MB rotate over enough
+    copies to total >= 512 MB per timed loop, so they stream from HBM rather than the MALL."""
+    lib = mh.load()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    floor = 512 * 1024 * 1024
+
+    def normal(n, seed, mean=0.0, std=1.0):
+        t = torch.empty(n, dtype=torch.float32, device="cuda")
+        mh.check(lib.muyo_fill_normal_f32(t.data_ptr(), n, seed, mean, std, sp))
+        return t
+
+    def normal16(n, seed, mean=0.0, std=1.0):
+        t = torch.empty(n, dtype=torch.float16, device="cuda")
+        mh.check(lib.muyo_fill_normal_f16(t.data_ptr(), n, seed, mean, std, sp))
+        return t
+
+    def copies_for(nbytes):
+        return max(1, -(-floor // nbytes)) if nbytes < 256 * 1024 * 1024 else 1
+
+    def timed(launches):
+        for launch in launches:
+            mh.check(launch())
+        torch.cuda.synchronize()
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b.record(stream)
+        for _ in range(reps):
+            for launch in launches:
+                mh.check(launch())
+        e.record(stream)
+        torch.cuda.synchronize()
+        return b.elapsed_time(e) / (reps * len(launches))
+
+    out = {}
+
+    def record(name, nbytes, ms, copies):
+        out[name] = {"launch_ms": round(ms, 5), "bytes_per_launch": nbytes, "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "pct_of_peak": round(100 * nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1), "rotated_copies": copies}
+
+    rows = 4096
+    # rms_norm 4096 x 896, fp16 weight N(1, 0.1)
+    nbytes = rows * (3584 + 3584) + 1792
+    k = copies_for(nbytes)
+    xs = [normal(rows * 896, 10 + i) for i in range(k)]
+    ys = [torch.empty_like(x) for x in xs]
+    w16 = normal16(896, 9, 1.0, 0.1)
+    pc = mh.rows_push_constants(896, rows, 1e-6)
+    record("rms_norm_4096x896", nbytes, timed([
+        (lambda x=x, y=y: lib.muyo_rms_norm_f32_f16w(mh.ref(pc), 1, x.data_ptr(), w16.data_ptr(), y.data_ptr(), None,
+                                                     rows, 1, 1, sp)) for x, y in zip(xs, ys)]), k)
+    # add 4096 x 896
+    nbytes = rows * 10752
+    k = copies_for(nbytes)
+    bs = [normal(rows * 896, 40 + i) for i in range(k)]
+    pc = mh.add_push_constants(rows * 896, row=896)
+    record("add_4096x896", nbytes, timed([
+        (lambda a=a, b=b, y=y: lib.muyo_add_f32(mh.ref(pc), 1, a.data_ptr(), b.data_ptr(), y.data_ptr(), None,
+                                               *mh.add_dispatch(rows * 896), sp)) for a, b, y in zip(xs, bs, ys)]), k)
+    del xs, ys, bs
+    # swiglu 4096 x (2 x 4864)
+    n = rows * 4864
+    nbytes = rows * 58368
+    k = copies_for(nbytes)
+    gs = [normal(n, 60 + i) for i in range(k)]
+    us = [normal(n, 70 + i) for i in range(k)]
+    ds = [torch.empty_like(g) for g in gs]
+    pc = mh.glu_push_constants(n, 4864)
+    record("swiglu_4096x4864", nbytes, timed([
+        (lambda g=g, u=u, d=d: lib.muyo_swiglu_f32(mh.ref(pc), g.data_ptr(), u.data_ptr(), d.data_ptr(),
+                                                  *mh.add_dispatch(n), sp)) for g, u, d in zip(gs, us, ds)]), k)
+    del gs, us, ds
+    # rope_neox 4096 tokens x 16 heads x 64, theta 1e6, positions in [0, 2047]
+    heads = 16
+    nbytes = rows * (4096 + 4096 + 4)
+    k = copies_for(nbytes)
+    xs = [normal(rows * heads * 64, 80 + i) for i in range(k)]
+    ys = [torch.empty_like(x) for x in xs]
+    gen = torch.Generator(device="cuda").manual_seed(81)
+    pos = torch.randint(0, 2048, (rows,), dtype=torch.int32, device="cuda", generator=gen)
+    pc = mh.rope_push_constants(heads, 64, 1e6, tokens=rows)
+    record("rope_neox_4096x16x64", nbytes, timed([
+        (lambda x=x, y=y: lib.muyo_rope_neox_f32(mh.ref(pc), x.data_ptr(), pos.data_ptr(), None, y.data_ptr(), None,
+                                                 heads * rows, 1, 1, sp)) for x, y in zip(xs, ys)]), k)
+    del xs, ys
+    # softmax 4096 x 14 heads x 2048, N(0, 3)
+    srows = rows * 14
+    x = normal(srows * 2048, 90, 0.0, 3.0)
+    y = torch.empty_like(x)
+    pc = mh.soft_max_push_constants(srows, 2048, 1.0)
+    record("soft_max_4096x14x2048", srows * 2048 * 8, timed([
+        lambda: lib.muyo_soft_max_f32(mh.ref(pc), x.data_ptr(), None, None, y.data_ptr(), *mh.row_dispatch(srows), sp)]),
+        1)
+    del x, y
+    # argmax 4096 x 151936, N(0, 2)
+    x = normal(rows * 151936, 91, 0.0, 2.0)
+    idx = torch.empty(rows, dtype=torch.int32, device="cuda")
+    pc = mh.argmax_push_constants(151936, rows)
+    record("argmax_4096x151936", rows * 151936 * 4 + rows * 4, timed([
+        lambda: lib.muyo_argmax_f32(mh.ref(pc), x.data_ptr(), idx.data_ptr(), *mh.row_dispatch(rows), sp)]), 1)
+    del x, idx
+    # decode GEMV suite (Qwen2.5-0.5B): fp16 W N(0, 0.02), f32 x, f32 y (+ f32 bias for QKV)
+    spec = mh.MuyoMatVecSpec(32, 1, 1)
+    for name, r, c, bias in [("gemv_qkv_1152x896", 1152, 896, True), ("gemv_o_896x896", 896, 896, False),
+                             ("gemv_gate_up_9728x896", 9728, 896, False), ("gemv_down_896x4864", 896, 4864, False),
+                             ("gemv_lm_head_151936x896", 151936, 896, False)]:
+        nbytes = 2 * r * c + 4 * c + 4 * r + (4 * r if bias else 0)
+        k = copies_for(nbytes)
+        ws = [normal16(r * c, 100 + i, 0.0, 0.02) for i in range(k)]
+        xv = normal(c, 99, 0.0, 1.0)
+        ys = [torch.empty(r, dtype=torch.float32, device="cuda") for _ in range(k)]
+        bv = normal(r, 98, 0.0, 0.02) if bias else None
+        pc = mh.mat_vec_push_constants(c, r, fusion_flags=mh.FUSION_BIAS0 if bias else 0)
+        record(name, nbytes, timed([
+            (lambda w=w, y=y: lib.muyo_mul_mat_vec_f16_f32_f32(mh.ref(pc), mh.ref(spec), w.data_ptr(), xv.data_ptr(),
+                                                               y.data_ptr(), bv.data_ptr() if bias else None, None, r,
+                                                               1, 1, sp)) for w, y in zip(ws, ys)]), k)
+        del ws, ys
+    # device copy reference: torch's copy of 256 MiB (read + write)
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    record("device_copy_256MiB", 2 * src.numel() * 4, timed([lambda: (dst.copy_(src), 0)[1]]), 1)
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(shape, position, seconds, seed):
     """The CPU oracle's decode step on one core over a bounded sample (TEST INFRASTRUCTURE path)."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    oracle.set_threads(min(16, os.cpu_count() or 1))
+    cores = min(16, len(os.sched_getaffinity(0)))
+    oracle.set_threads(cores)
     model = oracle.Model(**shape)
     model.fill_random(seed)
     model.fill_kv_random(position, seed + 1)
-    oracle.set_threads(1)
-    token, done, t0 = 9707, 0, time.perf_counter()
-    positions = []
-    while True:
-        token, _, _ = model.step(token, position + done)
-        positions.append(position + done)
-        done += 1
-        if time.perf_counter() - t0 >= seconds or position + done >= shape["max_seq"]:
-            break
-    elapsed = time.perf_counter() - t0
-    total = sum(step_bytes(shape, p) for p in positions)
+
+    def sample(threads):
+        oracle.set_threads(threads)
+        token, done, t0 = 9707, 0, time.perf_counter()
+        positions = []
+        while True:
+            token, _, _ = model.step(token, position + done)
+            positions.append(position + done)
+            done += 1
+            if time.perf_counter() - t0 >= seconds or position + done >= shape["max_seq"]:
+                break
+        elapsed = time.perf_counter() - t0
+        total = sum(step_bytes(shape, p) for p in positions)
+        return total / elapsed / 1e9, done, elapsed, positions
+
+    gbs, done, elapsed, positions = sample(1)
+    omp_gbs, omp_done, omp_elapsed, _ = sample(cores)
     return {
-        "value": round(total / elapsed / 1e9, 3),
+        "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
         "sample": f"{done} decode steps of the same 0.5B-shape workload at cache rows {positions[0]}..{positions[-1]} "
                   f"({elapsed:.1f} s, {done / elapsed:.3f} tok/s, double-accumulating C oracle, -O2, 1 thread)",
         "tok_per_s": round(done / elapsed, 4),
+        "openmp": {"value": round(omp_gbs, 3), "unit": "GB/s", "cores": cores,
+                   "tok_per_s": round(omp_done / omp_elapsed, 4),
+                   "sample": f"{omp_done} steps from the same rows, GEMV rows split over {cores} OpenMP threads"},
     }
 
 
@@ -206,7 +350,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--position", type=int, default=1024)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-ops", action="store_true", help="skip the per-op launcher suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape secondary figure")
     ap.add_argument("--kernel-only", choices=["lm_head", "copy"],
@@ -237,6 +382,7 @@ def main() -> int:
     value = total_bytes / (ms * 1e-3 * args.steps) / 1e9
 
     kern = time_kernels(mh, torch, shape, seed, rounds=64)
+    ops = {} if args.no_ops else time_ops(mh, torch)
     lm_gbs = lm_head_bytes(shape) / (kern["lm_head_ms"] * 1e-3) / 1e9
     gu_gbs = gate_up_bytes(shape) / (kern["gate_up_ms"] * 1e-3) / 1e9
 
@@ -292,6 +438,7 @@ def main() -> int:
             "gate_up_swiglu": {"GB/s": round(gu_gbs, 1), "launch_ms": round(kern["gate_up_ms"], 5),
                                "bytes_per_launch": gate_up_bytes(shape),
                                "note": "rotated over the 24 layers' weights (420 MB > MALL)"},
+            **ops,
         },
         "secondary": secondary,
         "greedy_ids_head": ids[:8],

@@ -141,6 +141,13 @@ int LaunchRmsNorm(const char* name, const LlamaAddPushConstants* pc, uint32_t do
     {
         return Fail(MUYO_E_CONTRACT, "%s: ne10 (weight length) must be >= 1", name);
     }
+    // The dispatch is the tensor's (rows, channels, samples), as in ggml's {ne01, ne02, ne03}: a
+    // larger one would index past A.
+    if (gx > pc->ne01 || gy > pc->ne02 || gz > pc->ne03)
+    {
+        return Fail(MUYO_E_DISPATCH, "%s: dispatch (%u, %u, %u) exceeds the tensor's (ne01, ne02, ne03) = (%u, %u, %u)",
+                    name, gx, gy, gz, pc->ne01, pc->ne02, pc->ne03);
+    }
     const uint64_t total = static_cast<uint64_t>(gx) * gy * gz;
     if (total > 0xFFFFFFFFull / kWave)
     {

@@ -71,6 +71,11 @@ def test_argument_errors_without_a_gpu(mh):
     assert lib.muyo_mul_mat_vec_f16_f32_f32(mh.ref(pc), None, None, None, None, None, None, 8, 1, 1, 0) == mh.MUYO_E_NULL
     assert b"required" in lib.muyo_last_error()
     assert lib.muyo_rms_norm_f32(None, 1, None, None, None, None, 1, 1, 1, 0) == mh.MUYO_E_NULL
+    # rms_norm's dispatch is (rows, channels, samples): past the tensor it is refused, not read.
+    rows = mh.rows_push_constants(896, 4096, 1e-6)
+    fake = ctypes.c_void_p(16)
+    assert lib.muyo_rms_norm_f32(mh.ref(rows), 1, fake, fake, fake, None, 512, 8, 1, 0) == mh.MUYO_E_DISPATCH
+    assert lib.muyo_rms_norm_f32(mh.ref(rows), 1, fake, fake, fake, None, 4097, 1, 1, 0) == mh.MUYO_E_DISPATCH
     glu = mh.glu_push_constants(600)
     glu.ne2_012mp ^= 1
     fake = ctypes.c_void_p(16)
