@@ -32,7 +32,7 @@ namespace
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
 constexpr uint32_t kMaxLds = 160 * 1024;
-constexpr int kStageVec = 8;           // float4 per thread per staging round (rows <= 8192 floats)
+constexpr int kStageVec = 8;           // float4 per thread per staging round at most (rows <= 8192 floats)
 constexpr int kMaxGroup = 8;           // query heads per kv head
 #ifndef MUYO_GEMV_ROUNDS
 #define MUYO_GEMV_ROUNDS 1  // GEMV grid = this many rounds of the workgroups resident on the chip
@@ -64,7 +64,11 @@ uint32_t CuCount()
 struct PlainStage
 {
     const float* x;
-    __device__ void Run(float4* xs, uint32_t n) const { StageSplit<kBlock, kStageVec, false>(x, nullptr, n, 0.0f, xs); }
+    template <int kVec>
+    __device__ void Run(float4* xs, uint32_t n) const
+    {
+        StageSplit<kBlock, kVec, false>(x, nullptr, n, 0.0f, xs);
+    }
 };
 
 struct NormStage
@@ -72,7 +76,11 @@ struct NormStage
     const float* x;
     const float* w;
     float eps;
-    __device__ void Run(float4* xs, uint32_t n) const { StageSplit<kBlock, kStageVec, true>(x, w, n, eps, xs); }
+    template <int kVec>
+    __device__ void Run(float4* xs, uint32_t n) const
+    {
+        StageSplit<kBlock, kVec, true>(x, w, n, eps, xs);
+    }
 };
 
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
@@ -91,6 +99,7 @@ struct MergeStage
         return (static_cast<uint64_t>(h / group) * gridChunks + c) * group + h % group;
     }
 
+    template <int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
         __shared__ float weight[kMergeSlots];
@@ -168,10 +177,20 @@ struct MergeStage
 // Fused GEMV: units of kNr rows, a staging policy, an epilogue per unit, an optional block tail.
 //
 // kSingle (a row fits one batch): one segment of kLpr lanes streams all kNr rows of a unit. Each
-// lane keeps its activation chunks in registers (read from LDS once), and units are double-
-// buffered: the next unit's rows are requested before the current ones are consumed, so every
-// wave keeps a batch in flight while it computes. Otherwise the kNr rows of a unit sit in kNr
-// adjacent segments and each row streams through RowDot's ping-pong of batches.
+// lane keeps its activation chunks in registers (read from LDS once) and requests the next
+// unit's rows as soon as the current ones are consumed. One buffer per wave keeps the register
+// count low enough for two or three resident waves per SIMD, which hide each other's latency
+// (measured faster than double-buffering at one or two). Otherwise the kNr rows of a unit sit in
+// kNr adjacent segments and each row streams through RowDot's ping-pong of batches.
+
+/// float4 loads per thread that stage a row of at most kLpr * kCpl chunks in one round (the
+/// norm prologue needs one round): fewer registers for short rows.
+template <int kLpr, int kCpl>
+constexpr int StageVecFor()
+{
+    constexpr int n = (kLpr * kCpl * 2 + kBlock - 1) / kBlock;
+    return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : kStageVec;
+}
 
 template <int kLpr, int kNr, bool kSingle>
 constexpr uint32_t UnitsPerWave()
@@ -201,9 +220,8 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
     if constexpr (kSingle)
     {
         // Weights do not depend on the activation: start streaming them before it is staged.
-        half8 wa[kNr][kCpl];
-        half8 wb[kNr][kCpl];
-        auto load = [&](uint32_t unit, half8(&w)[kNr][kCpl]) {
+        half8 w[kNr][kCpl];
+        auto load = [&](uint32_t unit) {
 #pragma unroll
             for (int r = 0; r < kNr; ++r)
             {
@@ -212,44 +230,37 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
         };
         if (first + unitInWave < units)
         {
-            load(first + unitInWave, wa);
+            load(first + unitInWave);
         }
-        stage.Run(xs, cols);
+        stage.template Run<StageVecFor<kLpr, kCpl>()>(xs, cols);
         float4 xlo[kCpl];
         float4 xhi[kCpl];
         LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
-        // Every lane of the segment ends with the unit's row sums.
-        auto finish = [&](uint32_t unit, const half8(&w)[kNr][kCpl]) {
+        for (; first < units; first += stride)
+        {
+            const uint32_t unit = first + unitInWave;
             float sums[kNr];
 #pragma unroll
             for (int r = 0; r < kNr; ++r)
             {
-                sums[r] = GroupSum<kLpr>(unit < units ? DotRegisters<kLpr, kCpl>(w[r], xlo, xhi, nchunks, lir) : 0.0f);
+                sums[r] = unit < units ? DotRegisters<kLpr, kCpl>(w[r], xlo, xhi, nchunks, lir) : 0.0f;
+            }
+            // The next unit's rows go out before this unit's reduction and epilogue; with a single
+            // buffer per wave the other resident waves keep the memory busy meanwhile.
+            if (unit + stride < units)
+            {
+                load(unit + stride);
+            }
+            // Every lane of the segment ends with the unit's row sums.
+#pragma unroll
+            for (int r = 0; r < kNr; ++r)
+            {
+                sums[r] = GroupSum<kLpr>(sums[r]);
             }
             if (unit < units && lir == 0)
             {
                 epi.Finish(unit, sums, bestValue, bestIndex);
             }
-        };
-        for (; first < units; first += 2 * stride)
-        {
-            const uint32_t ua = first + unitInWave;
-            const uint32_t ub = ua + stride;
-            if (ub < units)
-            {
-                load(ub, wb);
-            }
-            finish(ua, wa);
-            if (first + stride >= units)
-            {
-                break;
-            }
-            const uint32_t uc = ub + stride;
-            if (uc < units)
-            {
-                load(uc, wa);
-            }
-            finish(ub, wb);
         }
     }
     else
@@ -259,7 +270,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
         {
             LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
         }
-        stage.Run(xs, cols);
+        stage.template Run<kStageVec>(xs, cols);
         const float4* lo = xs;
         const float4* hi = xs + nchunks;
         for (; first < units; first += stride)
@@ -329,7 +340,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
     {
         LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
     }
-    stage.Run(xs, cols);
+    stage.template Run<kStageVec>(xs, cols);
     const float4* lo = xs;
     const float4* hi = xs + nchunks;
     for (; unit < units; unit += 2 * gridDim.x)

@@ -143,6 +143,11 @@ int Validate(const MuyoQwen2Config& c)
     {
         return Fail(MUYO_E_UNSUPPORTED, "decoder: a GEMV input longer than 40960 floats does not fit LDS");
     }
+    if (c.hidden > 8192)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: hidden %u exceeds 8192 (the fused rms_norm prologue's one round)",
+                    c.hidden);
+    }
     if (c.maxSeq > kMaxSeq)
     {
         return Fail(MUYO_E_UNSUPPORTED, "decoder: maxSeq %u exceeds %u", c.maxSeq, kMaxSeq);
