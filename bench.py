@@ -20,8 +20,8 @@ path) on one host core, over a bounded sample of steps of the same workload; the
 the process's cores (OpenMP over GEMV rows, at most 16) is reported beside it.
 
 kernels: per-launch figures of the per-op launchers at the batched element-wise/reduction shapes
-and the decode GEMV suite (inputs under 256 MB rotated over >= 512 MB of copies), and torch's
-device copy for reference.
+and the decode GEMV suite (inputs under 256 MB rotated over >= 512 MB of copies; the launches
+replayed from a hipGraph), and torch's device copy for reference.
 """
 from __future__ import annotations
 
@@ -151,15 +151,31 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     def copies_for(nbytes):
         return max(1, -(-floor // nbytes)) if nbytes < 256 * 1024 * 1024 else 1
 
-    def timed(launches):
+    def timed(launches, graph=True):
+        """ms per launch. With `graph` and several launches, they are captured once into a hipGraph
+        and replayed, so the figure is the kernels' own time plus the GPU's inter-kernel gaps,
+        without the host's launch cost; each launch takes the stream as `st`."""
+        graph = graph and len(launches) > 1
         for launch in launches:
-            mh.check(launch())
+            mh.check(launch(st=sp))
+        torch.cuda.synchronize()
+        if graph:
+            captured = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(captured):
+                capture = torch.cuda.current_stream().cuda_stream
+                for launch in launches:
+                    mh.check(launch(st=capture))
+            run = captured.replay
+            run()
+        else:
+            def run():
+                for launch in launches:
+                    mh.check(launch(st=sp))
         torch.cuda.synchronize()
         b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         b.record(stream)
         for _ in range(reps):
-            for launch in launches:
-                mh.check(launch())
+            run()
         e.record(stream)
         torch.cuda.synchronize()
         return b.elapsed_time(e) / (reps * len(launches))
@@ -179,16 +195,16 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     w16 = normal16(896, 9, 1.0, 0.1)
     pc = mh.rows_push_constants(896, rows, 1e-6)
     record("rms_norm_4096x896", nbytes, timed([
-        (lambda x=x, y=y: lib.muyo_rms_norm_f32_f16w(mh.ref(pc), 1, x.data_ptr(), w16.data_ptr(), y.data_ptr(), None,
-                                                     rows, 1, 1, sp)) for x, y in zip(xs, ys)]), k)
+        (lambda x=x, y=y, st=None: lib.muyo_rms_norm_f32_f16w(mh.ref(pc), 1, x.data_ptr(), w16.data_ptr(), y.data_ptr(), None,
+                                                     rows, 1, 1, st)) for x, y in zip(xs, ys)]), k)
     # add 4096 x 896
     nbytes = rows * 10752
     k = copies_for(nbytes)
     bs = [normal(rows * 896, 40 + i) for i in range(k)]
     pc = mh.add_push_constants(rows * 896, row=896)
     record("add_4096x896", nbytes, timed([
-        (lambda a=a, b=b, y=y: lib.muyo_add_f32(mh.ref(pc), 1, a.data_ptr(), b.data_ptr(), y.data_ptr(), None,
-                                               *mh.add_dispatch(rows * 896), sp)) for a, b, y in zip(xs, bs, ys)]), k)
+        (lambda a=a, b=b, y=y, st=None: lib.muyo_add_f32(mh.ref(pc), 1, a.data_ptr(), b.data_ptr(), y.data_ptr(), None,
+                                               *mh.add_dispatch(rows * 896), st)) for a, b, y in zip(xs, bs, ys)]), k)
     del xs, ys, bs
     # swiglu 4096 x (2 x 4864)
     n = rows * 4864
@@ -199,8 +215,8 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     ds = [torch.empty_like(g) for g in gs]
     pc = mh.glu_push_constants(n, 4864)
     record("swiglu_4096x4864", nbytes, timed([
-        (lambda g=g, u=u, d=d: lib.muyo_swiglu_f32(mh.ref(pc), g.data_ptr(), u.data_ptr(), d.data_ptr(),
-                                                  *mh.add_dispatch(n), sp)) for g, u, d in zip(gs, us, ds)]), k)
+        (lambda g=g, u=u, d=d, st=None: lib.muyo_swiglu_f32(mh.ref(pc), g.data_ptr(), u.data_ptr(), d.data_ptr(),
+                                                  *mh.add_dispatch(n), st)) for g, u, d in zip(gs, us, ds)]), k)
     del gs, us, ds
     # rope_neox 4096 tokens x 16 heads x 64, theta 1e6, positions in [0, 2047]
     heads = 16
@@ -212,8 +228,8 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     pos = torch.randint(0, 2048, (rows,), dtype=torch.int32, device="cuda", generator=gen)
     pc = mh.rope_push_constants(heads, 64, 1e6, tokens=rows)
     record("rope_neox_4096x16x64", nbytes, timed([
-        (lambda x=x, y=y: lib.muyo_rope_neox_f32(mh.ref(pc), x.data_ptr(), pos.data_ptr(), None, y.data_ptr(), None,
-                                                 heads * rows, 1, 1, sp)) for x, y in zip(xs, ys)]), k)
+        (lambda x=x, y=y, st=None: lib.muyo_rope_neox_f32(mh.ref(pc), x.data_ptr(), pos.data_ptr(), None, y.data_ptr(), None,
+                                                 heads * rows, 1, 1, st)) for x, y in zip(xs, ys)]), k)
     del xs, ys
     # softmax 4096 x 14 heads x 2048, N(0, 3)
     srows = rows * 14
@@ -221,7 +237,7 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     y = torch.empty_like(x)
     pc = mh.soft_max_push_constants(srows, 2048, 1.0)
     record("soft_max_4096x14x2048", srows * 2048 * 8, timed([
-        lambda: lib.muyo_soft_max_f32(mh.ref(pc), x.data_ptr(), None, None, y.data_ptr(), *mh.row_dispatch(srows), sp)]),
+        lambda st=None: lib.muyo_soft_max_f32(mh.ref(pc), x.data_ptr(), None, None, y.data_ptr(), *mh.row_dispatch(srows), st)]),
         1)
     del x, y
     # argmax 4096 x 151936, N(0, 2)
@@ -229,7 +245,7 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     idx = torch.empty(rows, dtype=torch.int32, device="cuda")
     pc = mh.argmax_push_constants(151936, rows)
     record("argmax_4096x151936", rows * 151936 * 4 + rows * 4, timed([
-        lambda: lib.muyo_argmax_f32(mh.ref(pc), x.data_ptr(), idx.data_ptr(), *mh.row_dispatch(rows), sp)]), 1)
+        lambda st=None: lib.muyo_argmax_f32(mh.ref(pc), x.data_ptr(), idx.data_ptr(), *mh.row_dispatch(rows), st)]), 1)
     del x, idx
     # decode GEMV suite (Qwen2.5-0.5B): fp16 W N(0, 0.02), f32 x, f32 y (+ f32 bias for QKV)
     spec = mh.MuyoMatVecSpec(32, 1, 1)
@@ -244,14 +260,14 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
         bv = normal(r, 98, 0.0, 0.02) if bias else None
         pc = mh.mat_vec_push_constants(c, r, fusion_flags=mh.FUSION_BIAS0 if bias else 0)
         record(name, nbytes, timed([
-            (lambda w=w, y=y: lib.muyo_mul_mat_vec_f16_f32_f32(mh.ref(pc), mh.ref(spec), w.data_ptr(), xv.data_ptr(),
+            (lambda w=w, y=y, st=None: lib.muyo_mul_mat_vec_f16_f32_f32(mh.ref(pc), mh.ref(spec), w.data_ptr(), xv.data_ptr(),
                                                                y.data_ptr(), bv.data_ptr() if bias else None, None, r,
-                                                               1, 1, sp)) for w, y in zip(ws, ys)]), k)
+                                                               1, 1, st)) for w, y in zip(ws, ys)]), k)
         del ws, ys
     # device copy reference: torch's copy of 256 MiB (read + write)
     src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
-    record("device_copy_256MiB", 2 * src.numel() * 4, timed([lambda: (dst.copy_(src), 0)[1]]), 1)
+    record("device_copy_256MiB", 2 * src.numel() * 4, timed([lambda st=None: (dst.copy_(src), 0)[1]], graph=False), 1)
     del src, dst
     torch.cuda.empty_cache()
     return out

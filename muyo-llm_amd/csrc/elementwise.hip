@@ -95,12 +95,15 @@ __global__ __launch_bounds__(kBlock) void AddGeneral(const float* __restrict__ a
     }
 }
 
-bool Contiguous(uint32_t ne0, uint32_t ne1, uint32_t ne2, uint32_t nb0, uint32_t nb1, uint32_t nb2, uint32_t nb3)
+/// True when element (i0, i1, i2, i3) of a tensor with these extents and strides sits at
+/// i0 + ne0 * (i1 + ne1 * (i2 + ne2 * i3)); a dimension of extent 1 has no say in that.
+bool Contiguous(uint32_t ne0, uint32_t ne1, uint32_t ne2, uint32_t ne3, uint32_t nb0, uint32_t nb1, uint32_t nb2,
+                uint32_t nb3)
 {
     const uint64_t s1 = ne0;
     const uint64_t s2 = s1 * ne1;
     const uint64_t s3 = s2 * ne2;
-    return nb0 == 1 && nb1 == s1 && nb2 == s2 && nb3 == s3;
+    return (ne0 <= 1 || nb0 == 1) && (ne1 <= 1 || nb1 == s1) && (ne2 <= 1 || nb2 == s2) && (ne3 <= 1 || nb3 == s3);
 }
 
 uint32_t GridFor(uint64_t items)
@@ -193,6 +196,8 @@ __global__ __launch_bounds__(kBlock) void SwiGluGeneral(const float* __restrict_
 // ------------------------------------------------------------------------------------------------
 // rope_neox (shaders/llama/rope_neox.comp:6-17, rope_funcs.glsl:17-35,76-114)
 
+constexpr uint32_t kRopeTablePairs = 256;
+
 struct RopeArgs
 {
     LlamaRopePushConstants pc;
@@ -211,14 +216,23 @@ __global__ __launch_bounds__(kBlock) void RopeNeox(const float* __restrict__ x, 
                                                    const uint32_t* __restrict__ setRows, RopeArgs args)
 {
     const LlamaRopePushConstants& p = args.pc;
-    const uint64_t item = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x;
-    const uint64_t total = static_cast<uint64_t>(p.nrows) * args.pairs;
-    if (item >= total)
+    // thetaScale^j depends only on the pair index within the rotated span: computed once per
+    // workgroup (the shader's pow(theta_scale, i0 / 2) at each j).
+    __shared__ float thetaPow[kRopeTablePairs];
+    const uint32_t tablePairs = min(p.nDims / 2, kRopeTablePairs);
+    for (uint32_t j = threadIdx.x; j < tablePairs; j += kBlock)
+    {
+        thetaPow[j] = powf(p.thetaScale, static_cast<float>(j));
+    }
+    __syncthreads();
+    // The host keeps nrows * pairs below 2^32.
+    const uint32_t item = blockIdx.x * kBlock + threadIdx.x;
+    if (item >= p.nrows * args.pairs)
     {
         return;
     }
-    const uint32_t row = static_cast<uint32_t>(item / args.pairs);
-    const uint32_t i0 = 2u * static_cast<uint32_t>(item % args.pairs);
+    const uint32_t row = item / args.pairs;
+    const uint32_t i0 = 2u * (item - row * args.pairs);
     // row = x + 32768 * z over the dispatched workgroups.
     const bool rowCovered = args.gz == 1 ? row < args.gx : ((row % 32768u) < args.gx && row / 32768u < args.gz);
     if (!rowCovered || i0 >= p.ne00)
@@ -247,7 +261,9 @@ __global__ __launch_bounds__(kBlock) void RopeNeox(const float* __restrict__ x, 
         return;
     }
     const uint32_t iw = i0 - p.nOffs;
-    const float thetaBase = static_cast<float>(positions[i2]) * powf(p.thetaScale, static_cast<float>(iw) / 2.0f);
+    const float power = (iw & 1u) == 0 && iw / 2 < tablePairs ? thetaPow[iw / 2]
+                                                               : powf(p.thetaScale, static_cast<float>(iw) / 2.0f);
+    const float thetaBase = static_cast<float>(positions[i2]) * power;
     const float freqFactor = p.hasFf != 0 ? ff[iw / 2] : 1.0f;
     // rope_yarn
     const float thetaExtrap = thetaBase / freqFactor;
@@ -493,9 +509,10 @@ extern "C" int muyo_add_f32(const LlamaAddPushConstants* pc, uint32_t norepeat, 
     const bool flat =
         limit == pc->ne && pc->misalignOffsets == 0 && (pc->ne & 3u) == 0 &&
         static_cast<uint64_t>(pc->ne00) * pc->ne01 * pc->ne02 * pc->ne03 == pc->ne &&
-        Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->nb00, pc->nb01, pc->nb02, pc->nb03) &&
-        Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->nb20, pc->nb21, pc->nb22, pc->nb23) &&
-        (norepeat || sameShape) && Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->nb10, pc->nb11, pc->nb12, pc->nb13) &&
+        Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->ne03, pc->nb00, pc->nb01, pc->nb02, pc->nb03) &&
+        Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->ne03, pc->nb20, pc->nb21, pc->nb22, pc->nb23) &&
+        (norepeat || sameShape) &&
+        Contiguous(pc->ne00, pc->ne01, pc->ne02, pc->ne03, pc->nb10, pc->nb11, pc->nb12, pc->nb13) &&
         Aligned16(a) && Aligned16(b) && Aligned16(d);
     const hipStream_t s = AsStream(stream);
     if (flat)
@@ -571,10 +588,10 @@ extern "C" int muyo_swiglu_f32(const LlamaGluPushConstants* pc, const float* a, 
         div[0] == d012 && div[1] == static_cast<uint64_t>(pc->ne21) * pc->ne20 && div[2] == pc->ne20;
     const uint64_t limit = CoveredLimit(pc->N, dispatch_y, dispatch_z);
     const bool flat = limit == pc->N && canonicalDivisors && pc->mode == LLAMA_GLU_MODE_SPLIT && pc->misalignOffsets == 0 &&
-                      (pc->N & 3u) == 0 && d012 >= pc->N &&
-                      Contiguous(pc->ne20, pc->ne21, pc->ne22, pc->nb00, pc->nb01, pc->nb02, pc->nb03) &&
-                      Contiguous(pc->ne20, pc->ne21, pc->ne22, pc->nb10, pc->nb11, pc->nb12, pc->nb13) &&
-                      Contiguous(pc->ne20, pc->ne21, pc->ne22, pc->nb20, pc->nb21, pc->nb22, pc->nb23) &&
+                      (pc->N & 3u) == 0 && d012 >= pc->N &&  // so every element has i23 = 0
+                      Contiguous(pc->ne20, pc->ne21, pc->ne22, 1, pc->nb00, pc->nb01, pc->nb02, pc->nb03) &&
+                      Contiguous(pc->ne20, pc->ne21, pc->ne22, 1, pc->nb10, pc->nb11, pc->nb12, pc->nb13) &&
+                      Contiguous(pc->ne20, pc->ne21, pc->ne22, 1, pc->nb20, pc->nb21, pc->nb22, pc->nb23) &&
                       Aligned16(a) && Aligned16(b) && Aligned16(d);
     const hipStream_t s = AsStream(stream);
     if (flat)
@@ -647,6 +664,11 @@ extern "C" int muyo_rope_neox_f32(const LlamaRopePushConstants* pc, const float*
     args.gz = dispatch_z;
     args.pairs = static_cast<uint32_t>(std::min<uint64_t>(256ull * dispatch_y, (pc->ne00 + 1) / 2));
     const uint64_t total = static_cast<uint64_t>(pc->nrows) * args.pairs;
+    if (total >= 0xFFFFFFFFull - kBlock)
+    {
+        return Fail(MUYO_E_RANGE, "%s: %llu (row, pair) items exceed the 32-bit index space", name,
+                    static_cast<unsigned long long>(total));
+    }
     hipLaunchKernelGGL(RopeNeox, dim3(CeilDiv(total, kBlock)), dim3(kBlock), 0, AsStream(stream), x, positions, ff, d,
                        set_rows, args);
     return LaunchStatus(name);

@@ -31,7 +31,11 @@ struct RmsArgs
     uint32_t aoff, boff, doff;
     float eps;
     uint32_t multiply;
+    uint32_t aligned;   // A and D 16-byte aligned
+    uint32_t wAligned;  // the weight row 16-byte aligned
 };
+
+constexpr int kRmsCachedFloat4 = 8;  // rows of up to 2048 floats stay in registers
 
 template <typename WT>
 __device__ __forceinline__ float WeightAt(const WT* w, uint64_t i);
@@ -46,6 +50,24 @@ template <>
 __device__ __forceinline__ float WeightAt<uint16_t>(const uint16_t* w, uint64_t i)
 {
     return HalfBitsToFloat(w[i]);
+}
+
+/// Four consecutive weights from element i (i % 4 == 0, the row 16-byte aligned).
+template <typename WT>
+__device__ __forceinline__ float4 LoadWeight4(const WT* w, uint64_t i);
+
+template <>
+__device__ __forceinline__ float4 LoadWeight4<float>(const float* w, uint64_t i)
+{
+    return *reinterpret_cast<const float4*>(w + i);
+}
+
+template <>
+__device__ __forceinline__ float4 LoadWeight4<uint16_t>(const uint16_t* w, uint64_t i)
+{
+    const uint2 h = *reinterpret_cast<const uint2*>(w + i);
+    return make_float4(HalfBitsToFloat(static_cast<uint16_t>(h.x & 0xFFFFu)), HalfBitsToFloat(static_cast<uint16_t>(h.x >> 16)),
+                       HalfBitsToFloat(static_cast<uint16_t>(h.y & 0xFFFFu)), HalfBitsToFloat(static_cast<uint16_t>(h.y >> 16)));
 }
 
 __device__ __forceinline__ uint32_t ModIfNeeded(uint32_t a, uint32_t b) { return b == 0 ? 0 : a % b; }
@@ -72,7 +94,58 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
     const float* x = a + aOff;
     float* y = d + dOff;
 
-    const bool vec = ((aOff | dOff | p.ncols) & 3u) == 0;
+    const bool vec = p.aligned && ((aOff | dOff | p.ncols) & 3u) == 0;
+    const bool wrap = p.ncols > p.ne10;
+    if (vec && p.ncols <= kRmsCachedFloat4 * 4 * kWave)
+    {
+        // The whole row in registers: one batch of loads, the sum, then the scaled row.
+        const uint32_t n4 = p.ncols / 4;
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        float4 v[kRmsCachedFloat4];
+#pragma unroll
+        for (int k = 0; k < kRmsCachedFloat4; ++k)
+        {
+            v[k] = x4[min(static_cast<uint32_t>(lane + k * kWave), n4 - 1)];
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kRmsCachedFloat4; ++k)
+        {
+            if (lane + k * kWave < n4)
+            {
+                sum = fmaf(v[k].x, v[k].x, sum);
+                sum = fmaf(v[k].y, v[k].y, sum);
+                sum = fmaf(v[k].z, v[k].z, sum);
+                sum = fmaf(v[k].w, v[k].w, sum);
+            }
+        }
+        sum = GroupSum<kWave>(sum);
+        const float scale = 1.0f / sqrtf(sum / static_cast<float>(p.ncols) + p.eps);
+        const bool weights4 = p.multiply && p.wAligned && !wrap && (bOff & 3u) == 0;
+#pragma unroll
+        for (int k = 0; k < kRmsCachedFloat4; ++k)
+        {
+            const uint32_t i = lane + k * kWave;
+            if (i < n4)
+            {
+                float4 o = make_float4(scale * v[k].x, scale * v[k].y, scale * v[k].z, scale * v[k].w);
+                if (weights4)
+                {
+                    const float4 g = LoadWeight4<WT>(w, bOff + 4ull * i);
+                    o = make_float4(o.x * g.x, o.y * g.y, o.z * g.z, o.w * g.w);
+                }
+                else if (p.multiply)
+                {
+                    o.x *= WeightAt<WT>(w, bOff + (4 * i + 0) % p.ne10);
+                    o.y *= WeightAt<WT>(w, bOff + (4 * i + 1) % p.ne10);
+                    o.z *= WeightAt<WT>(w, bOff + (4 * i + 2) % p.ne10);
+                    o.w *= WeightAt<WT>(w, bOff + (4 * i + 3) % p.ne10);
+                }
+                reinterpret_cast<float4*>(y)[i] = o;
+            }
+        }
+        return;
+    }
     float sum = 0.0f;
     if (vec)
     {
@@ -96,8 +169,7 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
     sum = GroupSum<kWave>(sum);
     const float scale = 1.0f / sqrtf(sum / static_cast<float>(p.ncols) + p.eps);
 
-    const bool wrap = p.ncols > p.ne10;
-    if (vec && !wrap && p.multiply && (bOff & 3u) == 0 && sizeof(WT) == 4)
+    if (vec && !wrap && p.multiply && p.wAligned && (bOff & 3u) == 0 && sizeof(WT) == 4)
     {
         const uint32_t n4 = p.ncols / 4;
         const float4* w4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(w) + bOff);
@@ -173,6 +245,8 @@ int LaunchRmsNorm(const char* name, const LlamaAddPushConstants* pc, uint32_t do
     p.doff = pc->misalignOffsets & 0xFFu;
     p.eps = pc->param1;
     p.multiply = doMultiply ? 1u : 0u;
+    p.aligned = Aligned16(a) && Aligned16(d) ? 1u : 0u;
+    p.wAligned = b != nullptr && Aligned16(b) ? 1u : 0u;
     hipLaunchKernelGGL((RmsNormRows<WT>), dim3(CeilDiv(total, kWaves)), dim3(kBlock), 0, AsStream(stream), a, b, d,
                        p);
     return LaunchStatus(name);
