@@ -80,17 +80,19 @@ def test_decoder_graph_replay_matches_eager_steps(mh, gpu, orc):
     assert ids == again == stepped
 
 
-def test_decoder_05b_greedy_32_steps(mh, gpu, orc, capsys):
-    """Qwen2.5-0.5B shape, KV pre-filled to p = 128, 32 greedy tokens from a seeded random id."""
+@pytest.mark.parametrize("position", [128, 1024, 2016])
+def test_decoder_05b_greedy_32_steps(mh, gpu, orc, capsys, position):
+    """Qwen2.5-0.5B shape, KV pre-filled to p, 32 greedy tokens from a seeded random id (p = 2016
+    ends at cache row 2047, the last of a 2048-row cache)."""
     orc.set_threads(16)
     shape = mh.QWEN25_05B
-    dec, model = make_pair(mh, orc, shape, seed=2026, kv_positions=128, kv_seed=2027)
+    dec, model = make_pair(mh, orc, shape, seed=2026, kv_positions=position, kv_seed=2027)
     start = int(orc.uniform_f32(1, 99)[0] * 0.5 * shape["vocab"] + 0.5 * shape["vocab"])
     with dec:
-        ids = dec.generate(start, 128, 32)
-    want, margins = model.greedy(start, 128, 32)
+        ids = dec.generate(start, position, 32)
+    want, margins = model.greedy(start, position, 32)
     with capsys.disabled():
-        print(f"\n[0.5b greedy] start {start} ids {ids[:8]}... min top1-top2 margin {min(margins):.3g}")
+        print(f"\n[0.5b greedy p={position}] start {start} ids {ids[:8]}... min top1-top2 margin {min(margins):.3g}")
     assert ids == want
 
 
