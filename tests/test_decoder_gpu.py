@@ -63,6 +63,34 @@ def test_decoder_small_steps_match_oracle(mh, gpu, orc):
                 assert diff.max() <= 2e-3 * (1 + np.abs(orc.half_to_float(ref[:, 30:42])).max())
 
 
+# Shapes off the two Qwen sizes: a full GQA group of 8 with head_dim 128 (q dim 1024, merged in
+# o_proj), a q dim past 1024 with head_dim 64 (separate merge kernel), odd cache lengths and rows
+# at the end of the cache.
+ODD_SHAPES = {
+    "group8_hd128": (dict(layers=1, hidden=512, ffn=1024, heads=8, kv_heads=1, head_dim=128, vocab=500,
+                          max_seq=300), 296),
+    "qdim1280_hd64": (dict(layers=2, hidden=640, ffn=1792, heads=20, kv_heads=4, head_dim=64, vocab=700,
+                           max_seq=333), 329),
+    "hidden_1536_short_cache": (dict(layers=1, hidden=1536, ffn=8960, heads=12, kv_heads=2, head_dim=128,
+                                     vocab=300, max_seq=40), 36),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ODD_SHAPES))
+def test_decoder_odd_shapes_match_oracle(mh, gpu, orc, name):
+    shape, start = ODD_SHAPES[name]
+    dec, model = make_pair(mh, orc, shape, seed=31, kv_positions=start, kv_seed=32)
+    with dec:
+        token = 3
+        for i in range(4):
+            got = dec.step(token, start + i)
+            want, logits, _ = model.step(token, start + i)
+            gpu_logits = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+            assert close(gpu_logits, logits, 1e-3) == 0, f"{name} step {i}"
+            assert got == want
+            token = got
+
+
 def test_decoder_graph_replay_matches_eager_steps(mh, gpu, orc):
     """generate() (one hipGraph launch per token, ids fed back on the device) == step-by-step."""
     cfg = mh.qwen2_config(**SMALL)
