@@ -376,8 +376,8 @@ struct QkvEpi
     float* qOut;
     uint16_t* kcache;
     uint16_t* vcache;
+    const float* ropePow;  // thetaScale^j for j < headDim / 2, powf on the host as the CPU path does
     uint32_t cols, heads, kvHeads, headDim, maxSeq;
-    float thetaScale;
 
     __device__ uint32_t Units() const { return (heads + 2 * kvHeads) * headDim / 2; }
 
@@ -410,7 +410,7 @@ struct QkvEpi
             // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
             const uint32_t head = unit / half;
             const uint32_t j = unit % half;
-            const float theta = static_cast<float>(pos) * powf(thetaScale, static_cast<float>(j));
+            const float theta = static_cast<float>(pos) * ropePow[j];
             const float c = cosf(theta);
             const float sn = sinf(theta);
             const float o0 = s0 * c - s1 * sn;
@@ -1077,8 +1077,9 @@ hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const floa
                                const uint16_t* wqkv, const float* bias, const DecodeState* state, float* qOut,
                                uint16_t* kcache, uint16_t* vcache)
 {
-    QkvEpi epi{wqkv,        bias,       state,         qOut,         kcache, vcache, dims.hidden, dims.heads,
-               dims.kvHeads, dims.headDim, dims.maxSeq, dims.thetaScale};
+    QkvEpi epi{wqkv,       bias,         state,        qOut,         kcache,
+               vcache,     dims.ropePow, dims.hidden,  dims.heads,   dims.kvHeads,
+               dims.headDim, dims.maxSeq};
     const uint32_t units = (dims.heads + 2 * dims.kvHeads) * dims.headDim / 2;
     return LaunchFused<2>(s, units, kNoLimit, dims.hidden, NormStage{x, normW, dims.eps}, epi);
 }

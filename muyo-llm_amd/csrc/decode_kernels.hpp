@@ -25,6 +25,7 @@ struct DecodeDims
     uint32_t maxSeq;
     float eps;
     float thetaScale;  // ropeBase^(-2/headDim), computed in f32 on the host
+    const float* ropePow;  // device table of thetaScale^j, j < headDim / 2 (powf on the host)
     float attnScale;   // 1/sqrt(headDim)
     uint32_t attnChunks;  // most attention chunks per kv head (kMaxAttnChunks or kMergeAttnChunks)
 };

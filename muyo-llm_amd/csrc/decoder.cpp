@@ -400,6 +400,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot attnAcc = place(small * c.headDim * 4);
     const TensorSlot argValue = place(kArgMaxBlocks * 4);
     const TensorSlot argIndex = place(kArgMaxBlocks * 4);
+    const TensorSlot ropePow = place(static_cast<size_t>(c.headDim / 2) * 4);
     d->arenaBytes = cursor;
 
     hipError_t status = hipGetDevice(&d->device);
@@ -422,6 +423,17 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     {
         status = hipMemsetAsync(d->arena, 0, d->arenaBytes, d->stream);
     }
+    // The rope angles' powers, as the CPU path computes them (std::pow in f32, src/Rope.cpp:48-51).
+    std::vector<float> powers(c.headDim / 2);
+    for (uint32_t j = 0; j < c.headDim / 2; ++j)
+    {
+        powers[j] = std::pow(d->dims.thetaScale, static_cast<float>(j));
+    }
+    if (status == hipSuccess)
+    {
+        status = hipMemcpyAsync(d->arena + ropePow.offset, powers.data(), powers.size() * sizeof(float),
+                                hipMemcpyHostToDevice, d->stream);
+    }
     if (status == hipSuccess)
     {
         status = hipStreamSynchronize(d->stream);
@@ -443,6 +455,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->scratch.attnMax = d->At<float>(attnMax);
     d->scratch.attnSum = d->At<float>(attnSum);
     d->scratch.attnAcc = d->At<float>(attnAcc);
+    d->dims.ropePow = d->At<float>(ropePow);
     d->scratch.argValue = d->At<float>(argValue);
     d->scratch.argIndex = d->At<int32_t>(argIndex);
     d->argBlocks = LmHeadBlocks(d->dims);
