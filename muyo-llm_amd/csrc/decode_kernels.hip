@@ -64,6 +64,13 @@ uint32_t CuCount()
 struct PlainStage
 {
     const float* x;
+    static constexpr bool kCanDirect = true;  // see DirectStage
+    static constexpr bool kDirect = false;
+    template <int kLpr, int kCpl>
+    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
+    {
+        LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, 0.0f, lir, xlo, xhi);
+    }
     template <int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
@@ -76,11 +83,29 @@ struct NormStage
     const float* x;
     const float* w;
     float eps;
+    static constexpr bool kCanDirect = true;
+    static constexpr bool kDirect = false;
+    template <int kLpr, int kCpl>
+    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
+    {
+        LoadActivationDirect<kLpr, kCpl, true>(x, w, n, eps, lir, xlo, xhi);
+    }
     template <int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
         StageSplit<kBlock, kVec, true>(x, w, n, eps, xs);
     }
+};
+
+/// A staging policy applied by every lane to its own activation chunks, straight from global
+/// memory into registers (single-batch rows, where one segment covers the row): no LDS and no
+/// barrier, so the activation costs one latency that overlaps the weights'. Every segment reads
+/// the whole activation, which costs L1 bandwidth; launches with more workgroups than CUs stage
+/// through LDS instead.
+template <class Base>
+struct DirectStage : Base
+{
+    static constexpr bool kDirect = true;
 };
 
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
@@ -93,6 +118,8 @@ struct MergeStage
     const float* attnSum;
     const float* attnAcc;
     uint32_t heads, group, headDim, gridChunks;
+    static constexpr bool kCanDirect = false;  // the per-head weights are shared through LDS
+    static constexpr bool kDirect = false;
 
     __device__ uint64_t Slot(uint32_t h, uint32_t c) const
     {
@@ -221,6 +248,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
     {
         // Weights do not depend on the activation: start streaming them before it is staged.
         half8 w[kNr][kCpl];
+        typename Epi::Pre pre{};
         auto load = [&](uint32_t unit) {
 #pragma unroll
             for (int r = 0; r < kNr; ++r)
@@ -230,12 +258,20 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
         };
         if (first + unitInWave < units)
         {
+            pre = epi.Prefetch(first + unitInWave);
             load(first + unitInWave);
         }
-        stage.template Run<StageVecFor<kLpr, kCpl>()>(xs, cols);
         float4 xlo[kCpl];
         float4 xhi[kCpl];
-        LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
+        if constexpr (Stage::kDirect)
+        {
+            stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi);
+        }
+        else
+        {
+            stage.template Run<StageVecFor<kLpr, kCpl>()>(xs, cols);
+            LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
+        }
         for (; first < units; first += stride)
         {
             const uint32_t unit = first + unitInWave;
@@ -247,8 +283,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             }
             // The next unit's rows go out before this unit's reduction and epilogue; with a single
             // buffer per wave the other resident waves keep the memory busy meanwhile.
+            typename Epi::Pre next{};
             if (unit + stride < units)
             {
+                next = epi.Prefetch(unit + stride);
                 load(unit + stride);
             }
             // Every lane of the segment ends with the unit's row sums.
@@ -259,15 +297,18 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             }
             if (unit < units && lir == 0)
             {
-                epi.Finish(unit, sums, bestValue, bestIndex);
+                epi.Finish(unit, sums, pre, bestValue, bestIndex);
             }
+            pre = next;
         }
     }
     else
     {
         half8 w[kCpl];
+        typename Epi::Pre pre{};
         if (first + unitInWave < units)
         {
+            pre = epi.Prefetch(first + unitInWave);
             LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
         }
         stage.template Run<kStageVec>(xs, cols);
@@ -283,8 +324,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             }
             // The next unit's first batch goes out before this unit's reduction and epilogue.
             const uint32_t next = first + stride + unitInWave;
+            typename Epi::Pre nextPre{};
             if (next < units)
             {
+                nextPre = epi.Prefetch(next);
                 LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, w);
             }
             // Every lane of a segment holds its row's sum; the unit's second row sits in the
@@ -298,8 +341,9 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             }
             if (unit < units && part == 0 && lir == 0)
             {
-                epi.Finish(unit, sums, bestValue, bestIndex);
+                epi.Finish(unit, sums, pre, bestValue, bestIndex);
             }
+            pre = nextPre;
         }
     }
     epi.Tail(bestValue, bestIndex);
@@ -318,7 +362,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
     uint32_t parity = 0;
-    auto finish = [&](uint32_t unit, float dot) {
+    auto finish = [&](uint32_t unit, float dot, const typename Epi::Pre& pre) {
         dot = GroupSum<kWave>(dot);
         if ((threadIdx.x & (kWave - 1)) == 0)
         {
@@ -328,7 +372,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         if (threadIdx.x == 0)
         {
             float sums[1] = {(partial[parity][0] + partial[parity][1]) + (partial[parity][2] + partial[parity][3])};
-            epi.Finish(unit, sums, bestValue, bestIndex);
+            epi.Finish(unit, sums, pre, bestValue, bestIndex);
         }
         parity ^= 1u;
     };
@@ -336,8 +380,11 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
     uint32_t unit = blockIdx.x;
     half8 wa[kCpl];
     half8 wb[kCpl];
+    typename Epi::Pre pa{};
+    typename Epi::Pre pb{};
     if (unit < units)
     {
+        pa = epi.Prefetch(unit);
         LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
     }
     stage.template Run<kStageVec>(xs, cols);
@@ -348,9 +395,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         const uint32_t ub = unit + gridDim.x;
         if (ub < units)
         {
+            pb = epi.Prefetch(ub);
             LoadBatch<kBlock, kCpl>(epi.Row(ub, 0), 0, nchunks, lir, wb);
         }
-        finish(unit, DotBatch<kBlock, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f));
+        finish(unit, DotBatch<kBlock, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f), pa);
         if (ub >= units)
         {
             break;
@@ -358,9 +406,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         const uint32_t uc = ub + gridDim.x;
         if (uc < units)
         {
+            pa = epi.Prefetch(uc);
             LoadBatch<kBlock, kCpl>(epi.Row(uc, 0), 0, nchunks, lir, wa);
         }
-        finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f));
+        finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f), pb);
     }
     epi.Tail(bestValue, bestIndex);
 }
@@ -382,15 +431,14 @@ struct QkvEpi
     __device__ uint32_t Units() const { return (heads + 2 * kvHeads) * headDim / 2; }
 
     /// Rope units pair rows (j, j + hd/2) of one q or k head; value units pair adjacent rows.
+    /// Branch-free, so the epilogue's operand loads issue with the weights.
     __device__ uint32_t RowOf(uint32_t unit, int part) const
     {
         const uint32_t half = headDim / 2;
         const uint32_t ropeUnits = (heads + kvHeads) * half;
-        if (unit < ropeUnits)
-        {
-            return (unit / half) * headDim + unit % half + part * half;
-        }
-        return (heads + kvHeads) * headDim + 2 * (unit - ropeUnits) + part;
+        const uint32_t rope = (unit / half) * headDim + unit % half + part * half;
+        const uint32_t value = (heads + kvHeads) * headDim + 2 * (unit - ropeUnits) + part;
+        return unit < ropeUnits ? rope : value;
     }
 
     __device__ const uint16_t* Row(uint32_t unit, int part) const
@@ -398,19 +446,31 @@ struct QkvEpi
         return w + static_cast<uint64_t>(RowOf(unit, part)) * cols;
     }
 
-    __device__ void Finish(uint32_t unit, const float* s, float&, int32_t&) const
+    /// The epilogue's operands, requested with the unit's weights so their latency overlaps them.
+    struct Pre
+    {
+        float bias0, bias1, pow;
+        int32_t pos;
+    };
+
+    __device__ Pre Prefetch(uint32_t unit) const
+    {
+        return Pre{bias[RowOf(unit, 0)], bias[RowOf(unit, 1)], ropePow[unit % (headDim / 2)], state->position};
+    }
+
+    __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
     {
         const uint32_t half = headDim / 2;
         const uint32_t ropeUnits = (heads + kvHeads) * half;
-        const int32_t pos = state->position;
-        const float s0 = s[0] + bias[RowOf(unit, 0)];
-        const float s1 = s[1] + bias[RowOf(unit, 1)];
+        const int32_t pos = pre.pos;
+        const float s0 = s[0] + pre.bias0;
+        const float s1 = s[1] + pre.bias1;
         if (unit < ropeUnits)
         {
             // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
             const uint32_t head = unit / half;
             const uint32_t j = unit % half;
-            const float theta = static_cast<float>(pos) * ropePow[j];
+            const float theta = static_cast<float>(pos) * pre.pow;
             const float c = cosf(theta);
             const float sn = sinf(theta);
             const float o0 = s0 * c - s1 * sn;
@@ -449,7 +509,15 @@ struct ResidualEpi
 
     __device__ uint32_t Units() const { return rows; }
     __device__ const uint16_t* Row(uint32_t unit, int) const { return w + static_cast<uint64_t>(unit) * cols; }
-    __device__ void Finish(uint32_t unit, const float* s, float&, int32_t&) const { out[unit] = residual[unit] + s[0]; }
+    struct Pre
+    {
+        float residual;
+    };
+    __device__ Pre Prefetch(uint32_t unit) const { return Pre{residual[unit]}; }
+    __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
+    {
+        out[unit] = pre.residual + s[0];
+    }
     __device__ void Tail(float, int32_t) const {}
 };
 
@@ -465,7 +533,11 @@ struct GateUpEpi
     {
         return (part == 0 ? gate : up) + static_cast<uint64_t>(unit) * cols;
     }
-    __device__ void Finish(uint32_t unit, const float* s, float&, int32_t&) const
+    struct Pre
+    {
+    };
+    __device__ Pre Prefetch(uint32_t) const { return Pre{}; }
+    __device__ void Finish(uint32_t unit, const float* s, const Pre&, float&, int32_t&) const
     {
         act[unit] = s[0] / (1.0f + expf(-s[0])) * s[1];  // swiglu.comp's op
     }
@@ -513,7 +585,11 @@ struct LmHeadEpi
 
     __device__ uint32_t Units() const { return rows; }
     __device__ const uint16_t* Row(uint32_t unit, int) const { return table + static_cast<uint64_t>(unit) * cols; }
-    __device__ void Finish(uint32_t unit, const float* s, float& bestValue, int32_t& bestIndex) const
+    struct Pre
+    {
+    };
+    __device__ Pre Prefetch(uint32_t) const { return Pre{}; }
+    __device__ void Finish(uint32_t unit, const float* s, const Pre&, float& bestValue, int32_t& bestIndex) const
     {
         logits[unit] = s[0];
         // Units reach a lane in increasing order, so '>' keeps the lowest index on ties.
@@ -592,8 +668,23 @@ template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
 hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
                         const Stage& stage, const Epi& epi, uint32_t* blocksOut)
 {
+    constexpr uint32_t kUnitsPerBlock = kWaves * UnitsPerWave<kLpr, kNr, kSingle>();
+    if constexpr (kSingle && Stage::kCanDirect)
+    {
+        // At most one workgroup per CU: latency-bound, so each lane stages its own chunks.
+        uint32_t blocks = 0;
+        LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
+            s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, &blocks);
+        if (blocks <= CuCount())
+        {
+            const DirectStage<Stage> direct{stage};
+            return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, DirectStage<Stage>, Epi>,
+                                    DirectStage<Stage>, Epi>(s, units, kUnitsPerBlock, blockCap, 0, cols, direct, epi,
+                                                             blocksOut);
+        }
+    }
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
-        s, units, kWaves * UnitsPerWave<kLpr, kNr, kSingle>(), blockCap, lds, cols, stage, epi, blocksOut);
+        s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, blocksOut);
 }
 
 template <int kCpl, class Stage, class Epi>

@@ -86,6 +86,67 @@ __device__ __forceinline__ void LoadActivation(const float4* __restrict__ lo, co
     }
 }
 
+/// This lane's activation chunks (chunk lir + i*kLpr, clamped) read straight from global memory
+/// into registers, for rows that one kLpr-lane segment covers (kLpr * kCpl >= n/8): no LDS and
+/// no workgroup barrier. With kNorm the chunks are scaled in place by rsqrt(mean(x^2) + eps) * w
+/// in rms_norm.comp:122's order (scale * x) * w; the sum of squares is the segment's, which
+/// holds every element of the row once.
+template <int kLpr, int kCpl, bool kNorm>
+__device__ __forceinline__ void LoadActivationDirect(const float* __restrict__ x, const float* __restrict__ w,
+                                                     uint32_t n, float eps, uint32_t lir, float4 (&xlo)[kCpl],
+                                                     float4 (&xhi)[kCpl])
+{
+    const uint32_t nchunks = n / 8;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 glo[kCpl];
+    float4 ghi[kCpl];
+#pragma unroll
+    for (int i = 0; i < kCpl; ++i)
+    {
+        const uint32_t c = min(lir + i * kLpr, nchunks - 1);
+        xlo[i] = x4[2 * c];
+        xhi[i] = x4[2 * c + 1];
+        if constexpr (kNorm)
+        {
+            glo[i] = w4[2 * c];
+            ghi[i] = w4[2 * c + 1];
+        }
+    }
+    if constexpr (kNorm)
+    {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCpl; ++i)
+        {
+            float part = 0.0f;
+            part = fmaf(xlo[i].x, xlo[i].x, part);
+            part = fmaf(xlo[i].y, xlo[i].y, part);
+            part = fmaf(xlo[i].z, xlo[i].z, part);
+            part = fmaf(xlo[i].w, xlo[i].w, part);
+            part = fmaf(xhi[i].x, xhi[i].x, part);
+            part = fmaf(xhi[i].y, xhi[i].y, part);
+            part = fmaf(xhi[i].z, xhi[i].z, part);
+            part = fmaf(xhi[i].w, xhi[i].w, part);
+            ss += lir + i * kLpr < nchunks ? part : 0.0f;
+        }
+        ss = GroupSum<kLpr>(ss);
+        const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+#pragma unroll
+        for (int i = 0; i < kCpl; ++i)
+        {
+            xlo[i].x = (scale * xlo[i].x) * glo[i].x;
+            xlo[i].y = (scale * xlo[i].y) * glo[i].y;
+            xlo[i].z = (scale * xlo[i].z) * glo[i].z;
+            xlo[i].w = (scale * xlo[i].w) * glo[i].w;
+            xhi[i].x = (scale * xhi[i].x) * ghi[i].x;
+            xhi[i].y = (scale * xhi[i].y) * ghi[i].y;
+            xhi[i].z = (scale * xhi[i].z) * ghi[i].z;
+            xhi[i].w = (scale * xhi[i].w) * ghi[i].w;
+        }
+    }
+}
+
 /// One loaded single-batch row against the activation in registers (chunks past the row add
 /// nothing). The summation order is DotBatch's.
 template <int kLpr, int kCpl>
