@@ -37,6 +37,10 @@ constexpr int kMaxGroup = 8;           // query heads per kv head
 #ifndef MUYO_GEMV_ROUNDS
 #define MUYO_GEMV_ROUNDS 1  // GEMV grid = this many rounds of the workgroups resident on the chip
 #endif
+#ifndef MUYO_DIRECT_THREADS
+#define MUYO_DIRECT_THREADS 64  // workgroup size of the register-direct GEMVs
+#endif
+constexpr int kDirectThreads = MUYO_DIRECT_THREADS;
 constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
 constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
 constexpr uint32_t kMergeSlots = 512;  // (head, chunk) weights that prologue holds in LDS
@@ -66,15 +70,16 @@ struct PlainStage
     const float* x;
     static constexpr bool kCanDirect = true;  // see DirectStage
     static constexpr bool kDirect = false;
+    static constexpr bool kElementwise = true;  // any column range stages on its own
     template <int kLpr, int kCpl>
     __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
     {
         LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, 0.0f, lir, xlo, xhi);
     }
-    template <int kVec>
+    template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
-        StageSplit<kBlock, kVec, false>(x, nullptr, n, 0.0f, xs);
+        StageSplit<kThreads, kVec, false>(x, nullptr, n, 0.0f, xs);
     }
 };
 
@@ -85,15 +90,16 @@ struct NormStage
     float eps;
     static constexpr bool kCanDirect = true;
     static constexpr bool kDirect = false;
+    static constexpr bool kElementwise = false;  // the norm needs the whole row
     template <int kLpr, int kCpl>
     __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
     {
         LoadActivationDirect<kLpr, kCpl, true>(x, w, n, eps, lir, xlo, xhi);
     }
-    template <int kVec>
+    template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
-        StageSplit<kBlock, kVec, true>(x, w, n, eps, xs);
+        StageSplit<kThreads, kVec, true>(x, w, n, eps, xs);
     }
 };
 
@@ -120,15 +126,17 @@ struct MergeStage
     uint32_t heads, group, headDim, gridChunks;
     static constexpr bool kCanDirect = false;  // the per-head weights are shared through LDS
     static constexpr bool kDirect = false;
+    static constexpr bool kElementwise = false;
 
     __device__ uint64_t Slot(uint32_t h, uint32_t c) const
     {
         return (static_cast<uint64_t>(h / group) * gridChunks + c) * group + h % group;
     }
 
-    template <int kVec>
+    template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
+        static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
         __shared__ float weight[kMergeSlots];
         // Positions outside the cache are rejected on the host; clamping keeps every read in bounds.
         const uint32_t keys = static_cast<uint32_t>(max(*position, 0)) + 1;
@@ -212,10 +220,10 @@ struct MergeStage
 
 /// float4 loads per thread that stage a row of at most kLpr * kCpl chunks in one round (the
 /// norm prologue needs one round): fewer registers for short rows.
-template <int kLpr, int kCpl>
+template <int kLpr, int kCpl, int kThreads>
 constexpr int StageVecFor()
 {
-    constexpr int n = (kLpr * kCpl * 2 + kBlock - 1) / kBlock;
+    constexpr int n = (kLpr * kCpl * 2 + kThreads - 1) / kThreads;
     return n <= 1 ? 1 : n <= 2 ? 2 : n <= 4 ? 4 : kStageVec;
 }
 
@@ -225,9 +233,11 @@ constexpr uint32_t UnitsPerWave()
     return kSingle ? kWave / kLpr : (kWave / kLpr) / kNr;
 }
 
-template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
-__global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage, Epi epi)
+template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi, int kThreads = kBlock>
+__global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage stage, Epi epi)
 {
+    static_assert(kThreads == kBlock || kSingle, "multi-batch rows stage with kBlock threads");
+    constexpr int kWavesPerBlock = kThreads / kWave;
     extern __shared__ float4 xs[];
     const uint32_t nchunks = cols / 8;
     constexpr int kUnits = UnitsPerWave<kLpr, kNr, kSingle>();
@@ -237,8 +247,8 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
     const uint32_t lir = lane % kLpr;
     const int unitInWave = kSingle ? segment : segment / kNr;
     const int part = kSingle ? 0 : segment % kNr;
-    const uint32_t wave = blockIdx.x * kWaves + threadIdx.x / kWave;
-    const uint32_t stride = gridDim.x * kWaves * kUnits;
+    const uint32_t wave = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    const uint32_t stride = gridDim.x * kWavesPerBlock * kUnits;
     const uint32_t units = epi.Units();
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
         }
         else
         {
-            stage.template Run<StageVecFor<kLpr, kCpl>()>(xs, cols);
+            stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols);
             LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
         }
         for (; first < units; first += stride)
@@ -311,7 +321,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             pre = epi.Prefetch(first + unitInWave);
             LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
         }
-        stage.template Run<kStageVec>(xs, cols);
+        stage.template Run<kBlock, kStageVec>(xs, cols);
         const float4* lo = xs;
         const float4* hi = xs + nchunks;
         for (; first < units; first += stride)
@@ -346,7 +356,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVec(uint32_t cols, Stage stage
             pre = nextPre;
         }
     }
-    epi.Tail(bestValue, bestIndex);
+    epi.template Tail<kThreads>(bestValue, bestIndex);
 }
 
 /// Long rows (more than 1024 16-byte chunks): the whole workgroup streams one row as a single
@@ -387,7 +397,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         pa = epi.Prefetch(unit);
         LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
     }
-    stage.template Run<kStageVec>(xs, cols);
+    stage.template Run<kBlock, kStageVec>(xs, cols);
     const float4* lo = xs;
     const float4* hi = xs + nchunks;
     for (; unit < units; unit += 2 * gridDim.x)
@@ -411,7 +421,90 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         }
         finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f), pb);
     }
-    epi.Tail(bestValue, bestIndex);
+    epi.template Tail<kBlock>(bestValue, bestIndex);
+}
+
+/// Long rows, split by columns: workgroup b owns a run of at most kMaxSplitRows consecutive rows
+/// and wave w the w-th quarter of every row's chunks, its activation quarter read from LDS into
+/// registers once. Each wave streams its quarter of the block's rows double-buffered with no
+/// barrier between rows; the quarter sums meet in LDS once, after the last row.
+constexpr uint32_t kMaxSplitRows = 32;
+
+template <int kCpl, class Stage, class Epi>
+__global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, Stage stage, Epi epi)
+{
+    extern __shared__ float4 xs[];
+    __shared__ float partial[kMaxSplitRows][kWaves];
+    const uint32_t nchunks = cols / 8;
+    const uint32_t quarter = (nchunks + kWaves - 1) / kWaves;
+    const uint32_t waveId = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t begin = min(waveId * quarter, nchunks - 1);
+    const uint32_t span = min(begin + quarter, nchunks) - begin;  // this wave's chunks, >= 1
+    const uint32_t units = epi.Units();
+    const uint32_t perBlock = (units + gridDim.x - 1) / gridDim.x;  // <= kMaxSplitRows (host check)
+    const uint32_t r0 = blockIdx.x * perBlock;
+    const uint32_t count = r0 < units ? min(perBlock, units - r0) : 0;
+    typename Epi::Pre pre{};
+    if (threadIdx.x < count)
+    {
+        pre = epi.Prefetch(r0 + threadIdx.x);
+    }
+    half8 wa[kCpl];
+    half8 wb[kCpl];
+    auto load = [&](uint32_t k, half8(&w)[kCpl]) {
+        LoadBatch<kWave, kCpl>(epi.Row(r0 + k, 0) + 8 * begin, 0, span, lane, w);
+    };
+    auto dot = [&](uint32_t k, const half8(&w)[kCpl], const float4(&xlo)[kCpl], const float4(&xhi)[kCpl]) {
+        const float d = GroupSum<kWave>(DotRegisters<kWave, kCpl>(w, xlo, xhi, span, lane));
+        if (lane == 0)
+        {
+            partial[k][waveId] = d;
+        }
+    };
+    if (count > 0)
+    {
+        load(0, wa);
+    }
+    float4 xlo[kCpl];
+    float4 xhi[kCpl];
+    if constexpr (Stage::kElementwise)
+    {
+        // Each wave reads its own quarter of x straight into registers: one latency, no LDS.
+        LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, 0.0f, lane, xlo, xhi);
+    }
+    else
+    {
+        stage.template Run<kBlock, kStageVec>(xs, cols);
+        LoadActivation<kWave, kCpl>(xs + begin, xs + nchunks + begin, span, lane, xlo, xhi);
+    }
+    for (uint32_t k = 0; k < count; k += 2)
+    {
+        if (k + 1 < count)
+        {
+            load(k + 1, wb);
+        }
+        dot(k, wa, xlo, xhi);
+        if (k + 1 >= count)
+        {
+            break;
+        }
+        if (k + 2 < count)
+        {
+            load(k + 2, wa);
+        }
+        dot(k + 1, wb, xlo, xhi);
+    }
+    __syncthreads();
+    float bestValue = -INFINITY;
+    int32_t bestIndex = 0x7FFFFFFF;
+    if (threadIdx.x < count)
+    {
+        const uint32_t k = threadIdx.x;
+        float sums[1] = {(partial[k][0] + partial[k][1]) + (partial[k][2] + partial[k][3])};
+        epi.Finish(r0 + k, sums, pre, bestValue, bestIndex);
+    }
+    epi.template Tail<kBlock>(bestValue, bestIndex);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -497,7 +590,10 @@ struct QkvEpi
         }
     }
 
-    __device__ void Tail(float, int32_t) const {}
+    template <int kThreads>
+    __device__ void Tail(float, int32_t) const
+    {
+    }
 };
 
 struct ResidualEpi
@@ -518,7 +614,10 @@ struct ResidualEpi
     {
         out[unit] = pre.residual + s[0];
     }
-    __device__ void Tail(float, int32_t) const {}
+    template <int kThreads>
+    __device__ void Tail(float, int32_t) const
+    {
+    }
 };
 
 struct GateUpEpi
@@ -541,7 +640,10 @@ struct GateUpEpi
     {
         act[unit] = s[0] / (1.0f + expf(-s[0])) * s[1];  // swiglu.comp's op
     }
-    __device__ void Tail(float, int32_t) const {}
+    template <int kThreads>
+    __device__ void Tail(float, int32_t) const
+    {
+    }
 };
 
 /// Better (value, index) under "larger value, then lower index" (the host greedy scan's rule).
@@ -550,12 +652,18 @@ __device__ __forceinline__ bool Better(float v, int32_t i, float bestV, int32_t 
     return v > bestV || (v == bestV && i < bestI);
 }
 
-/// Reduce (value, index) over a 256-thread block; the result lands in thread 0.
+/// Reduce (value, index) over a block of kThreads; the result lands in thread 0.
+template <int kThreads = kBlock>
 __device__ __forceinline__ void BlockArgMax(float& value, int32_t& index)
 {
-    __shared__ float waveValue[kWaves];
-    __shared__ int32_t waveIndex[kWaves];
+    constexpr int kWaveCount = kThreads / kWave;
     GroupArgMax<kWave>(value, index);
+    if constexpr (kWaveCount == 1)
+    {
+        return;
+    }
+    __shared__ float waveValue[kWaveCount];
+    __shared__ int32_t waveIndex[kWaveCount];
     if ((threadIdx.x & (kWave - 1)) == 0)
     {
         waveValue[threadIdx.x / kWave] = value;
@@ -564,7 +672,7 @@ __device__ __forceinline__ void BlockArgMax(float& value, int32_t& index)
     __syncthreads();
     if (threadIdx.x == 0)
     {
-        for (int k = 1; k < kWaves; ++k)
+        for (int k = 1; k < kWaveCount; ++k)
         {
             if (Better(waveValue[k], waveIndex[k], value, index))
             {
@@ -599,9 +707,10 @@ struct LmHeadEpi
             bestIndex = static_cast<int32_t>(unit);
         }
     }
+    template <int kThreads>
     __device__ void Tail(float value, int32_t index) const
     {
-        BlockArgMax(value, index);
+        BlockArgMax<kThreads>(value, index);
         if (threadIdx.x == 0)
         {
             argValue[blockIdx.x] = value;
@@ -615,10 +724,10 @@ struct LmHeadEpi
 
 /// Workgroups of `kernel` the chip holds at once with `lds` bytes of dynamic LDS each.
 template <typename Kernel>
-uint32_t ResidentBlocks(Kernel kernel, size_t lds)
+uint32_t ResidentBlocks(Kernel kernel, int threads, size_t lds)
 {
     int perCu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, kernel, kBlock, lds) != hipSuccess || perCu < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&perCu, kernel, threads, lds) != hipSuccess || perCu < 1)
     {
         perCu = 1;
     }
@@ -628,7 +737,7 @@ uint32_t ResidentBlocks(Kernel kernel, size_t lds)
 /// Launches `kernel` over `units`, or with blocksOut only reports its workgroup count. The grid
 /// holds at most the workgroups resident at once (each stages the activation once and then
 /// strides over the units), so no workgroup waits for a second round.
-template <auto kKernel, class Stage, class Epi>
+template <auto kKernel, class Stage, class Epi, int kThreads = kBlock>
 hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBlock, uint32_t blockCap, size_t lds,
                             uint32_t cols, const Stage& stage, const Epi& epi, uint32_t* blocksOut)
 {
@@ -638,7 +747,7 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
     static uint32_t resident = 0;
     if (resident == 0 || residentLds != lds)
     {
-        resident = ResidentBlocks(kernel, lds);
+        resident = ResidentBlocks(kernel, kThreads, lds);
         residentLds = lds;
     }
     const uint32_t blocks = std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, resident}));
@@ -660,7 +769,7 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
         }
         configured = lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kBlock), lds, s, cols, stage, epi);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, cols, stage, epi);
     return hipGetLastError();
 }
 
@@ -673,18 +782,49 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
     {
         // At most one workgroup per CU: latency-bound, so each lane stages its own chunks.
         uint32_t blocks = 0;
-        LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
+        (void)LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
             s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, &blocks);
         if (blocks <= CuCount())
         {
+            // No LDS, so the workgroups can be small and spread over more CUs.
             const DirectStage<Stage> direct{stage};
-            return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, DirectStage<Stage>, Epi>,
-                                    DirectStage<Stage>, Epi>(s, units, kUnitsPerBlock, blockCap, 0, cols, direct, epi,
-                                                             blocksOut);
+            constexpr uint32_t kDirectUnits = (kDirectThreads / kWave) * UnitsPerWave<kLpr, kNr, kSingle>();
+            return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, DirectStage<Stage>, Epi, kDirectThreads>,
+                                    DirectStage<Stage>, Epi, kDirectThreads>(s, units, kDirectUnits, blockCap, 0, cols,
+                                                                             direct, epi, blocksOut);
+        }
+        // More workgroups than CUs but few enough single-wave ones that every unit gets its own
+        // segment in one round: single-wave workgroups balance the CUs (a 256-thread grid of
+        // 1.2 CUs' worth leaves most CUs with one workgroup and some with two).
+        uint32_t small = 0;
+        constexpr uint32_t kSmallUnits = UnitsPerWave<kLpr, kNr, kSingle>();
+        (void)LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
+            s, units, kSmallUnits, blockCap, lds, cols, stage, epi, &small);
+        if (static_cast<uint64_t>(small) * kSmallUnits >= units)
+        {
+            return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
+                s, units, kSmallUnits, blockCap, lds, cols, stage, epi, blocksOut);
         }
     }
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
         s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, blocksOut);
+}
+
+/// hipErrorNotSupported (nothing launched) when a workgroup's share of the rows would overflow
+/// its partial-sum table.
+template <int kCpl, class Stage, class Epi>
+hipError_t LaunchSplitRowsT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
+                            const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+{
+    constexpr auto kKernel = &FusedMatVecSplitRows<kCpl, Stage, Epi>;
+    const size_t used = Stage::kElementwise ? 0 : lds;
+    uint32_t blocks = 0;
+    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, &blocks);
+    if (CeilDiv(units, blocks) > kMaxSplitRows)
+    {
+        return hipErrorNotSupported;
+    }
+    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, blocksOut);
 }
 
 template <int kCpl, class Stage, class Epi>
@@ -734,6 +874,29 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
         MUYO_FUSED_CASE(64, 14)
         MUYO_FUSED_CASE(64, 16)
 #undef MUYO_FUSED_CASE
+        // Column quarters (a wave's quarter of a row in one batch), else one workgroup per row.
+        const uint32_t qcpl = CeilDiv(CeilDiv(nchunks, static_cast<uint32_t>(kWaves)), static_cast<uint32_t>(kWave));
+        hipError_t split = hipErrorNotSupported;
+        if (qcpl <= 8)
+        {
+            split = LaunchSplitRowsT<8, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        }
+        else if (qcpl <= 10)
+        {
+            split = LaunchSplitRowsT<10, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        }
+        else if (qcpl <= 12)
+        {
+            split = LaunchSplitRowsT<12, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        }
+        else if (qcpl <= 16)
+        {
+            split = LaunchSplitRowsT<16, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        }
+        if (split != hipErrorNotSupported)
+        {
+            return split;
+        }
         const uint32_t cpl = CeilDiv(nchunks, static_cast<uint32_t>(kBlock));
 #define MUYO_BLOCK_ROW_CASE(C)                                                                       \
     if (cpl <= C)                                                                                    \
