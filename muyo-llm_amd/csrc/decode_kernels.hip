@@ -116,7 +116,8 @@ struct DirectStage : Base
 
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
 /// sum_c e^(m_c - M) l_c (flash-decoding's combine). Every partial is requested at once, before
-/// the per-head weights are known, so the merge costs about one memory latency.
+/// the per-head weights are known. (Requesting the grid's slots before the position arrives, as
+/// the standalone merge kernel does, measured slower here.)
 struct MergeStage
 {
     const int32_t* position;
@@ -420,6 +421,119 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
             LoadBatch<kBlock, kCpl>(epi.Row(uc, 0), 0, nchunks, lir, wa);
         }
         finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f), pb);
+    }
+    epi.template Tail<kBlock>(bestValue, bestIndex);
+}
+
+/// Mid-size matrices whose units outnumber the waves resident at once: workgroup b owns kUnits
+/// consecutive units and wave w the w-th quarter of every row's chunks. Each wave requests its
+/// quarter of all kUnits units at once, so the whole matrix is in flight in one round instead of
+/// some waves waiting a second latency for a second unit. The activation quarter is read
+/// straight into registers (the norm's sum of squares meets in LDS); the quarter sums meet in
+/// LDS once, after the dots.
+template <int kCpl, int kNr, int kUnits, class Stage, class Epi>
+__global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stage stage, Epi epi)
+{
+    static_assert(Stage::kCanDirect, "each wave stages its own activation quarter");
+    __shared__ float partial[kUnits][kNr][kWaves];
+    __shared__ float squares[kWaves];
+    const uint32_t nchunks = cols / 8;
+    const uint32_t quarter = (nchunks + kWaves - 1) / kWaves;
+    const uint32_t waveId = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t begin = min(waveId * quarter, nchunks - 1);
+    const uint32_t span = min(begin + quarter, nchunks) - begin;  // this wave's chunks, >= 1
+    const uint32_t units = epi.Units();
+    const uint32_t u0 = blockIdx.x * kUnits;
+    const uint32_t count = u0 < units ? min(static_cast<uint32_t>(kUnits), units - u0) : 0;
+    typename Epi::Pre pre{};
+    if (threadIdx.x < count)
+    {
+        pre = epi.Prefetch(u0 + threadIdx.x);
+    }
+    // Every unit at once; past the last unit (the grid's last workgroup only) a slot reloads it.
+    half8 w[kUnits][kNr][kCpl];
+#pragma unroll
+    for (int k = 0; k < kUnits; ++k)
+    {
+        const uint32_t unit = min(u0 + k, units - 1);
+#pragma unroll
+        for (int r = 0; r < kNr; ++r)
+        {
+            LoadBatch<kWave, kCpl>(epi.Row(unit, r) + 8 * begin, 0, span, lane, w[k][r]);
+        }
+    }
+    float4 xlo[kCpl];
+    float4 xhi[kCpl];
+    LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, 0.0f, lane, xlo, xhi);
+    if constexpr (!Stage::kElementwise)
+    {
+        // rms_norm over the whole row: (scale * x) * w with scale = rsqrt(mean(x^2) + eps).
+        float4 glo[kCpl];
+        float4 ghi[kCpl];
+        LoadActivationDirect<kWave, kCpl, false>(stage.w + 8 * begin, nullptr, 8 * span, 0.0f, lane, glo, ghi);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCpl; ++i)
+        {
+            float part = 0.0f;
+            part = fmaf(xlo[i].x, xlo[i].x, part);
+            part = fmaf(xlo[i].y, xlo[i].y, part);
+            part = fmaf(xlo[i].z, xlo[i].z, part);
+            part = fmaf(xlo[i].w, xlo[i].w, part);
+            part = fmaf(xhi[i].x, xhi[i].x, part);
+            part = fmaf(xhi[i].y, xhi[i].y, part);
+            part = fmaf(xhi[i].z, xhi[i].z, part);
+            part = fmaf(xhi[i].w, xhi[i].w, part);
+            ss += lane + i * kWave < span ? part : 0.0f;
+        }
+        ss = GroupSum<kWave>(ss);
+        if (lane == 0)
+        {
+            squares[waveId] = ss;
+        }
+        __syncthreads();
+        const float total = (squares[0] + squares[1]) + (squares[2] + squares[3]);
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + stage.eps);
+#pragma unroll
+        for (int i = 0; i < kCpl; ++i)
+        {
+            xlo[i].x = (scale * xlo[i].x) * glo[i].x;
+            xlo[i].y = (scale * xlo[i].y) * glo[i].y;
+            xlo[i].z = (scale * xlo[i].z) * glo[i].z;
+            xlo[i].w = (scale * xlo[i].w) * glo[i].w;
+            xhi[i].x = (scale * xhi[i].x) * ghi[i].x;
+            xhi[i].y = (scale * xhi[i].y) * ghi[i].y;
+            xhi[i].z = (scale * xhi[i].z) * ghi[i].z;
+            xhi[i].w = (scale * xhi[i].w) * ghi[i].w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kUnits; ++k)
+    {
+#pragma unroll
+        for (int r = 0; r < kNr; ++r)
+        {
+            const float d = GroupSum<kWave>(DotRegisters<kWave, kCpl>(w[k][r], xlo, xhi, span, lane));
+            if (lane == 0)
+            {
+                partial[k][r][waveId] = d;
+            }
+        }
+    }
+    __syncthreads();
+    float bestValue = -INFINITY;
+    int32_t bestIndex = 0x7FFFFFFF;
+    if (threadIdx.x < count)
+    {
+        const uint32_t k = threadIdx.x;
+        float sums[kNr];
+#pragma unroll
+        for (int r = 0; r < kNr; ++r)
+        {
+            sums[r] = (partial[k][r][0] + partial[k][r][1]) + (partial[k][r][2] + partial[k][r][3]);
+        }
+        epi.Finish(u0 + k, sums, pre, bestValue, bestIndex);
     }
     epi.template Tail<kBlock>(bestValue, bestIndex);
 }
@@ -773,6 +887,26 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
     return hipGetLastError();
 }
 
+/// The column-quarter kernel with the fewest units per workgroup whose grid is resident in one
+/// round; hipErrorNotSupported (nothing launched) when none is.
+template <int kNr, int kUnits, class Stage, class Epi>
+hipError_t LaunchColumnsT(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_t cols, const Stage& stage,
+                          const Epi& epi, uint32_t* blocksOut)
+{
+    constexpr auto kKernel = &FusedMatVecColumns<2, kNr, kUnits, Stage, Epi>;
+    uint32_t blocks = 0;
+    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, &blocks);
+    if (static_cast<uint64_t>(blocks) * kUnits < units)
+    {
+        if constexpr (kUnits < 6)
+        {
+            return LaunchColumnsT<kNr, kUnits + 1, Stage, Epi>(s, units, blockCap, cols, stage, epi, blocksOut);
+        }
+        return hipErrorNotSupported;
+    }
+    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, blocksOut);
+}
+
 template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
 hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
                         const Stage& stage, const Epi& epi, uint32_t* blocksOut)
@@ -805,6 +939,20 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
             return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
                 s, units, kSmallUnits, blockCap, lds, cols, stage, epi, blocksOut);
         }
+#ifndef MUYO_NO_COLUMNS
+        // Units past one round of resident waves: column quarters with several units per
+        // workgroup put the whole matrix in flight at once (rows of 257..512 chunks, where a
+        // quarter is two chunks per lane).
+        if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
+        {
+            const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
+                                                                        blocksOut);
+            if (status != hipErrorNotSupported)
+            {
+                return status;
+            }
+        }
+#endif
     }
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
         s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, blocksOut);
@@ -1202,10 +1350,12 @@ __global__ __launch_bounds__(128) void AttentionMergeKernel(const int32_t* __res
     float a[kMaxAttnChunks];
     for (uint32_t d = threadIdx.x; d < headDim; d += blockDim.x)
     {
+        // Every slot of the grid is requested with the position, not after it: slots past the
+        // step's last chunk hold earlier values and are dropped by selection below.
 #pragma unroll
         for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
         {
-            const uint32_t cc = min(c, chunks - 1);
+            const uint32_t cc = min(c, maxChunks - 1);
             const uint64_t slot = (static_cast<uint64_t>(g) * maxChunks + cc) * group + hh;
             m[c] = sc.attnMax[slot];
             l[c] = sc.attnSum[slot];
