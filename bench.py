@@ -40,8 +40,8 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per LM-head launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what the
 # counter reads for a 256 MiB device copy (profiles/lm_head_0.5b_pmc.md), and the L2 hit rate
 # (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)) of the same runs.
-LM_HEAD_TRAFFIC_BYTES = 273_033_326
-LM_HEAD_L2_HIT_RATE = 0.032
+LM_HEAD_TRAFFIC_BYTES = 273_033_388
+LM_HEAD_L2_HIT_RATE = 0.031
 
 
 def step_bytes(c: dict, position: int) -> int:
@@ -439,7 +439,7 @@ def main() -> int:
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "bytes_per_step": total_bytes // args.steps,
         "roofline": {
-            "kernel": "FusedMatVec<16,7,1,true,NormStage,LmHeadEpi> (final norm + tied LM head 151936x896 + argmax)",
+            "kernel": "FusedMatVec<16,7,1,true,NormStage,LmHeadEpi,256> (final norm + tied LM head 151936x896 + argmax)",
             "bound": "hbm",
             "achieved": round(lm_gbs, 1),
             "peak": HBM_PEAK_GBS,
