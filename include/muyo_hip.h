@@ -293,6 +293,45 @@ int muyo_decoder_enqueue_kernel(MuyoDecoder* decoder, uint32_t kernel, uint32_t 
 int muyo_self_test(const char* mode);
 
 /* ---------------------------------------------------------------------------------------------
+ * Token sampling on the device. Replaces the reference's host sampler, muyo_llm::Sampler
+ * (src/Sampler.h:16-42, src/Sampler.cpp:10-100), which its decode loop calls on the mapped
+ * logits after every step (src/FullModel.cpp:1111-1117).
+ *
+ * MuyoSamplerParams mirrors SamplerParams (src/Sampler.h:16-23) field for field; `reserved` pads
+ * the seed to 8 bytes. The engine is the reference's std::mt19937_64(seed), kept on the device in
+ * an opaque state of muyo_sampler_state_bytes() bytes; one uniform double is drawn per token
+ * sampled with temperature > 0, as uniform_real_distribution<double>(0, 1) of libstdc++ draws it
+ * (one 64-bit word / 2^64).
+ *
+ * muyo_sample_f32 is Sampler::Sample on device memory: the repetition penalty over the last
+ * repeat_last_n entries of history[0..history_count) (each occurrence applies it once; negative
+ * means all), temperature <= 0 as greedy (lowest index on ties), else division by the
+ * temperature, top-k, top-p and one draw. It modifies `logits` in place as the reference does.
+ * Among exactly equal logits the top-k order puts the lower index first (the reference leaves it
+ * to std::partial_sort). With temperature > 0 the device keeps at most 1024 candidates: top_k must
+ * be 1..1024, or <= 0 with vocab <= 1024 (else MUYO_E_UNSUPPORTED). `workspace` is device memory
+ * of muyo_sample_workspace_bytes(vocab, params) bytes; it needs no initialisation. The call
+ * enqueues a few kernels on `stream` and writes the token to device memory at `token`.
+ * ------------------------------------------------------------------------------------------- */
+typedef struct MuyoSamplerParams
+{
+    float temperature;     /* <= 0: greedy */
+    int32_t top_k;         /* <= 0: the whole vocabulary */
+    float top_p;
+    float repeat_penalty;  /* 1: off */
+    int32_t repeat_last_n; /* negative: the whole history */
+    uint32_t reserved;
+    uint64_t seed;
+} MuyoSamplerParams;
+
+size_t muyo_sampler_state_bytes(void);
+/* std::mt19937_64(seed) into `state` (device memory), stream-ordered. */
+int muyo_sampler_seed(void* state, uint64_t seed, void* stream);
+size_t muyo_sample_workspace_bytes(uint32_t vocab, const MuyoSamplerParams* params);
+int muyo_sample_f32(float* logits, uint32_t vocab, const int32_t* history, uint32_t history_count,
+                    const MuyoSamplerParams* params, void* state, void* workspace, int32_t* token, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Synthetic-input helpers (portable seeded generator; bit-identical on host and device).
  *   word(seed, i)   = mix64(mix64(seed) + i)            mix64 = SplitMix64's finaliser
  *   uniform(i)      = (word >> 40) * 2^-23 - 1          in [-1, 1), exact in f32

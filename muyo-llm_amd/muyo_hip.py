@@ -99,6 +99,19 @@ class MuyoQwen2Config(ctypes.Structure):
     ]
 
 
+class MuyoSamplerParams(ctypes.Structure):
+    """SamplerParams (src/Sampler.h:16-23); see muyo_sample_f32."""
+    _fields_ = [
+        ("temperature", f32), ("top_k", i32), ("top_p", f32), ("repeat_penalty", f32), ("repeat_last_n", i32),
+        ("reserved", u32), ("seed", ctypes.c_uint64),
+    ]
+
+
+def sampler_params(temperature=0.0, top_k=40, top_p=0.95, repeat_penalty=1.0, repeat_last_n=64, seed=0):
+    """The reference's defaults (src/Sampler.h:18-23)."""
+    return MuyoSamplerParams(temperature, top_k, top_p, repeat_penalty, repeat_last_n, 0, seed)
+
+
 CONTRACT_WORDS = {
     LlamaAddPushConstants: 29, LlamaMatVecPushConstants: 13, LlamaRopePushConstants: 30,
     LlamaGluPushConstants: 27, LlamaGenericHeadPushConstants: 6, LlamaSoftMaxPushConstants: 17,
@@ -151,6 +164,10 @@ _SIGNATURES = {
     "muyo_decoder_set_state": (ctypes.c_int, [vp, i32, i32, vp]),
     "muyo_decoder_enqueue_kernel": (ctypes.c_int, [vp, u32, u32, vp]),
     "muyo_self_test": (ctypes.c_int, [ctypes.c_char_p]),
+    "muyo_sampler_state_bytes": (ctypes.c_size_t, []),
+    "muyo_sampler_seed": (ctypes.c_int, [vp, ctypes.c_uint64, vp]),
+    "muyo_sample_workspace_bytes": (ctypes.c_size_t, [u32, vp]),
+    "muyo_sample_f32": (ctypes.c_int, [vp, u32, vp, u32, vp, vp, vp, vp, vp]),
     "muyo_fill_normal_f16": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_normal_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_uniform_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, vp]),
@@ -181,6 +198,13 @@ def load(path: os.PathLike | str | None = None) -> ctypes.CDLL:
     target = pathlib.Path(path) if path is not None else LIB_PATH
     if not target.exists():
         raise LibraryMissing(f"{target} is not built; run __graft_entry__.build() (make -C muyo-llm_amd/csrc)")
+    # torch carries its own HIP runtime. Loaded first, it is the one the library binds to, so the
+    # process holds a single runtime; loaded after the library, torch's device calls made the
+    # library's first launch fail with "no ROCm-capable device".
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(str(target))
     for name, (restype, argtypes) in _SIGNATURES.items():
         fn = getattr(lib, name)
@@ -453,6 +477,7 @@ def tensor_seed(seed: int, kind: str, layer: int) -> int:
 def _self_check_sizes() -> None:
     for cls, words in CONTRACT_WORDS.items():
         assert ctypes.sizeof(cls) == 4 * words, cls.__name__
+    assert ctypes.sizeof(MuyoSamplerParams) == 32
 
 
 _self_check_sizes()

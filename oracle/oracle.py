@@ -46,6 +46,11 @@ _SIGNATURES = {
     "oracle_attention_f16kv": (None, [vp, vp, vp, vp, u32, u32, u32, u32, i32, f32]),
     "oracle_decode_step": (i32, [vp, i32, i32, vp, vp]),
     "oracle_decode_layer": (None, [vp, u32, vp, i32, vp]),
+    "oracle_sampler_new": (vp, [f32, i32, f32, f32, i32, u64]),
+    "oracle_sampler_free": (None, [vp]),
+    "oracle_sampler_sample": (i32, [vp, vp, i32, vp, u64]),
+    "oracle_mt64_outputs": (None, [u64, u64, vp]),
+    "oracle_mt64_uniform": (None, [u64, u64, vp]),
 }
 
 # Tensor kind numbers shared with the product's seeding (muyo_tensor_seed).
@@ -220,6 +225,51 @@ def attention_f16kv(q, kcache_bits, vcache_bits, heads, kv_heads, head_dim, max_
     vc = np.ascontiguousarray(vcache_bits, dtype=np.uint16)
     out = np.empty(heads * head_dim, np.float32)
     load().oracle_attention_f16kv(_p(q), _p(kc), _p(vc), _p(out), heads, kv_heads, head_dim, max_seq, pos, scale)
+    return out
+
+
+class Sampler:
+    """The reference's host sampler (src/Sampler.cpp:10-100) restated in sampler.cpp: penalty over
+    the last-N history, temperature, top-k, top-p and one std::mt19937_64 draw per sampled token.
+    `ref=True` drives the reference's own Sampler.cpp instead, compiled into _ref/ (present only
+    where the reference tree was, when the oracle was built)."""
+
+    REF_PATH = HERE / "_ref" / "libref_sampler.so"
+
+    def __init__(self, temperature=0.0, top_k=40, top_p=0.95, repeat_penalty=1.0, repeat_last_n=64, seed=0,
+                 ref=False):
+        if ref:
+            lib = ctypes.CDLL(str(self.REF_PATH))
+            self._new, self._free, self._sample = lib.ref_sampler_new, lib.ref_sampler_free, lib.ref_sampler_sample
+            self._new.restype, self._new.argtypes = vp, [f32, i32, f32, f32, i32, u64]
+            self._free.restype, self._free.argtypes = None, [vp]
+            self._sample.restype, self._sample.argtypes = i32, [vp, vp, i32, vp, u64]
+        else:
+            lib = load()
+            self._new, self._free, self._sample = lib.oracle_sampler_new, lib.oracle_sampler_free, lib.oracle_sampler_sample
+        self._h = self._new(temperature, top_k, top_p, repeat_penalty, repeat_last_n, seed)
+
+    def sample(self, logits: np.ndarray, history) -> int:
+        """Samples from `logits` (modified in place, as the reference does)."""
+        assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+        hist = np.ascontiguousarray(history, dtype=np.int32)
+        return int(self._sample(self._h, _p(logits), logits.size, _p(hist) if hist.size else None, hist.size))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            self._free(self._h)
+            self._h = None
+
+
+def mt64_outputs(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.uint64)
+    load().oracle_mt64_outputs(seed, n, _p(out))
+    return out
+
+
+def mt64_uniform(seed: int, n: int) -> np.ndarray:
+    out = np.empty(n, np.float64)
+    load().oracle_mt64_uniform(seed, n, _p(out))
     return out
 
 
