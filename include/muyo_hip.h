@@ -324,6 +324,16 @@ typedef struct MuyoSamplerParams
     uint64_t seed;
 } MuyoSamplerParams;
 
+/* The decoder's next-token rule: Sampler::Sample with these parameters after every step, on the
+ * device, seeded now with params->seed (NULL: greedy, the default). Greedy without a penalty keeps
+ * the LM head's own argmax; anything else runs the sampler on a copy of the logits (the LOGITS
+ * tensor stays as the LM head wrote it). The penalty's history is the token embedded at each
+ * position: the steps record theirs, and muyo_decoder_set_history supplies earlier ones (a
+ * prompt). Takes effect from the next step; the step's graph is recorded again. */
+int muyo_decoder_set_sampler(MuyoDecoder* decoder, const MuyoSamplerParams* params);
+/* tokens[0..count) as the history of positions 0..count-1 (count <= maxSeq). */
+int muyo_decoder_set_history(MuyoDecoder* decoder, const int32_t* tokens, uint32_t count);
+
 size_t muyo_sampler_state_bytes(void);
 /* std::mt19937_64(seed) into `state` (device memory), stream-ordered. */
 int muyo_sampler_seed(void* state, uint64_t seed, void* stream);

@@ -1100,7 +1100,8 @@ __device__ __forceinline__ int32_t ReduceArgMaxPartials(const float* __restrict_
 }
 
 __global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, float* argValue, int32_t* argIndex,
-                                                         int32_t token, int32_t position, uint32_t argBlocks)
+                                                         int32_t* sampled, int32_t token, int32_t position,
+                                                         uint32_t argBlocks)
 {
     for (uint32_t b = threadIdx.x; b < argBlocks; b += kBlock)
     {
@@ -1109,6 +1110,10 @@ __global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, flo
     }
     if (threadIdx.x == 0)
     {
+        if (sampled != nullptr)
+        {
+            *sampled = token;
+        }
         state->token = token;
         state->position = position;
         state->start = position;
@@ -1116,13 +1121,17 @@ __global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, flo
     }
 }
 
+/// The next token is the sampler's when one ran (`sampled`), else the argmax of the LM head's
+/// partials. It is also recorded at its position in the token history the sampler's penalty reads.
 __global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __restrict__ table, DecodeState* state,
                                                           const float* __restrict__ argValue,
                                                           const int32_t* __restrict__ argIndex, uint32_t argBlocks,
-                                                          float* __restrict__ x, int32_t* __restrict__ ids,
-                                                          uint32_t idsCap, uint32_t hidden, uint32_t vocab)
+                                                          const int32_t* sampled, int32_t* history,
+                                                          uint32_t historyCap, float* __restrict__ x,
+                                                          int32_t* __restrict__ ids, uint32_t idsCap, uint32_t hidden,
+                                                          uint32_t vocab)
 {
-    const int32_t token = ReduceArgMaxPartials(argValue, argIndex, argBlocks);
+    const int32_t token = sampled != nullptr ? *sampled : ReduceArgMaxPartials(argValue, argIndex, argBlocks);
     if (blockIdx.x == 0 && threadIdx.x == 0)
     {
         const uint32_t step = state->step;
@@ -1130,9 +1139,14 @@ __global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __rest
         {
             ids[(step - 1) % idsCap] = token;
         }
+        const int32_t position = state->start + static_cast<int32_t>(step);
         state->token = token;
-        state->position = state->start + static_cast<int32_t>(step);
+        state->position = position;
         state->step = step + 1;
+        if (position >= 0 && static_cast<uint32_t>(position) < historyCap)
+        {
+            history[position] = token;
+        }
     }
     const bool ok = token >= 0 && static_cast<uint32_t>(token) < vocab;
     const uint16_t* row = table + static_cast<uint64_t>(ok ? token : 0) * hidden;
@@ -1144,9 +1158,10 @@ __global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __rest
 
 __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, const float* __restrict__ argValue,
                                                          const int32_t* __restrict__ argIndex, uint32_t argBlocks,
-                                                         int32_t* __restrict__ ids, uint32_t idsCap)
+                                                         const int32_t* sampled, int32_t* __restrict__ ids,
+                                                         uint32_t idsCap)
 {
-    const int32_t token = ReduceArgMaxPartials(argValue, argIndex, argBlocks);
+    const int32_t token = sampled != nullptr ? *sampled : ReduceArgMaxPartials(argValue, argIndex, argBlocks);
     if (threadIdx.x == 0)
     {
         const uint32_t step = state->step;
@@ -1455,8 +1470,8 @@ bool MergeInOProj(const DecodeDims& dims)
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
                           int32_t position, uint32_t argBlocks)
 {
-    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex, token,
-                       position, argBlocks);
+    hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex,
+                       scratch.sampled, token, position, argBlocks);
     return hipGetLastError();
 }
 
@@ -1465,7 +1480,8 @@ hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* st
                            uint32_t vocab)
 {
     hipLaunchKernelGGL(BeginStepKernel, dim3(CeilDiv(hidden, kBlock)), dim3(kBlock), 0, s, table, state,
-                       scratch.argValue, scratch.argIndex, argBlocks, x, ids, idsCap, hidden, vocab);
+                       scratch.argValue, scratch.argIndex, argBlocks, scratch.sampled, scratch.history,
+                       scratch.historyCap, x, ids, idsCap, hidden, vocab);
     return hipGetLastError();
 }
 
@@ -1473,7 +1489,7 @@ hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch
                           int32_t* ids, uint32_t idsCap)
 {
     hipLaunchKernelGGL(FinalizeKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex,
-                       argBlocks, ids, idsCap);
+                       argBlocks, scratch.sampled, ids, idsCap);
     return hipGetLastError();
 }
 

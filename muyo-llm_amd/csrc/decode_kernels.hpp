@@ -48,6 +48,9 @@ struct DecodeScratch
     float* attnAcc;     // [kvHeads][gridChunks][group][hd]    chunk-local P.V (relative to the max)
     float* argValue;    // [kArgMaxBlocks]                 per-workgroup LM-head max
     int32_t* argIndex;  // [kArgMaxBlocks]                 and its (lowest) index
+    int32_t* sampled;   // the sampler's token; null: the next token is the argmax of the partials
+    int32_t* history;   // [historyCap]                    the token embedded at each position
+    uint32_t historyCap;
 };
 
 constexpr uint32_t kArgMaxBlocks = 1024;

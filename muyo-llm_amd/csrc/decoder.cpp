@@ -15,6 +15,7 @@
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
+#include "sampler.hpp"
 
 using namespace muyo;
 
@@ -100,6 +101,14 @@ struct MuyoDecoder
     DecodeScratch scratch{};
     uint32_t argBlocks = 0;     // LM-head workgroups = argmax partials per step
     bool mergeInOProj = false;  // o_proj's prologue merges the attention partials
+
+    // Sampling (muyo_decoder_set_sampler): off = greedy from the LM head's argmax partials.
+    bool sampling = false;
+    SampleConfig sample{};
+    float* sampleLogits = nullptr;  // the sampler's penalised, temperature-divided copy
+    int32_t* sampledToken = nullptr;
+    Mt64State* rng = nullptr;
+    void* sampleWorkspace = nullptr;
 
     bool warm = false;
     hipGraph_t graph = nullptr;
@@ -243,6 +252,7 @@ hipError_t EnqueueLmHead(MuyoDecoder* d, hipStream_t s, const float* x)
 
 int Enqueue(MuyoDecoder* d, hipStream_t s)
 {
+    const MuyoQwen2Config& c = d->config;
     hipError_t status = EnqueueEmbed(d, s);
     if (status != hipSuccess)
     {
@@ -277,6 +287,18 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
     if ((status = EnqueueLmHead(d, s, x)) != hipSuccess)
     {
         return LaunchFailed(status, "lm_head", 0);
+    }
+    if (d->sampling)
+    {
+        // The logits stay as the LM head wrote them; the sampler works on its own copy, with the
+        // history up to the current position.
+        status = LaunchSample(s, d->At<float>(d->logits), d->sampleLogits, c.vocab, d->scratch.history,
+                              &d->state->position, c.maxSeq, d->sample, d->rng,
+                              SampleWorkspaceAt(d->sampleWorkspace, c.vocab, d->sample), d->sampledToken);
+        if (status != hipSuccess)
+        {
+            return LaunchFailed(status, "sample", 0);
+        }
     }
     return MUYO_OK;
 }
@@ -401,6 +423,13 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot argValue = place(kArgMaxBlocks * 4);
     const TensorSlot argIndex = place(kArgMaxBlocks * 4);
     const TensorSlot ropePow = place(static_cast<size_t>(c.headDim / 2) * 4);
+    const TensorSlot history = place(static_cast<size_t>(c.maxSeq) * 4);
+    const TensorSlot sampleLogits = place(static_cast<size_t>(c.vocab) * 4);
+    const TensorSlot sampledToken = place(4);
+    const TensorSlot rng = place(sizeof(Mt64State));
+    // Room for the largest top-k the sampler takes; smaller ones use a prefix of each part.
+    const SampleConfig widest{1.0F, static_cast<int32_t>(kSampleMaxTopK), 1.0F, 1.0F, 0};
+    const TensorSlot sampleWorkspace = place(SampleWorkspaceBytes(c.vocab, widest));
     d->arenaBytes = cursor;
 
     hipError_t status = hipGetDevice(&d->device);
@@ -458,6 +487,12 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->dims.ropePow = d->At<float>(ropePow);
     d->scratch.argValue = d->At<float>(argValue);
     d->scratch.argIndex = d->At<int32_t>(argIndex);
+    d->scratch.history = d->At<int32_t>(history);
+    d->scratch.historyCap = c.maxSeq;
+    d->sampleLogits = d->At<float>(sampleLogits);
+    d->sampledToken = d->At<int32_t>(sampledToken);
+    d->rng = d->At<Mt64State>(rng);
+    d->sampleWorkspace = d->arena + sampleWorkspace.offset;
     d->argBlocks = LmHeadBlocks(d->dims);
     *out = d;
     return MUYO_OK;
@@ -751,7 +786,77 @@ extern "C" int muyo_decoder_step(MuyoDecoder* d, int32_t token, int32_t position
 
 extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
 {
-    return d == nullptr ? 0u : 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
+    if (d == nullptr)
+    {
+        return 0;
+    }
+    const uint32_t greedy = 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
+    return greedy + (d->sampling ? SampleLaunches(d->config.vocab, d->sample, true) : 0u);
+}
+
+namespace
+{
+/// The next step re-records its launches (eagerly, then a fresh capture).
+void DropGraph(MuyoDecoder* d)
+{
+    if (d->exec != nullptr)
+    {
+        (void)hipGraphExecDestroy(d->exec);
+        d->exec = nullptr;
+    }
+    if (d->graph != nullptr)
+    {
+        (void)hipGraphDestroy(d->graph);
+        d->graph = nullptr;
+    }
+    d->warm = false;
+}
+}  // namespace
+
+extern "C" int muyo_decoder_set_sampler(MuyoDecoder* d, const MuyoSamplerParams* params)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    SampleConfig c{0.0F, 40, 0.95F, 1.0F, 64};
+    uint64_t seed = 0;
+    if (params != nullptr)
+    {
+        c = SampleConfig{params->temperature, params->top_k, params->top_p, params->repeat_penalty,
+                         params->repeat_last_n};
+        seed = params->seed;
+    }
+    if (!SampleSupported(c, d->config.vocab))
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder_set_sampler: a temperature above 0 needs top_k in 1..%u; got %d",
+                    kSampleMaxTopK, c.topK);
+    }
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    DropGraph(d);
+    // Greedy without a penalty is the LM head's argmax; anything else runs the sampler.
+    d->sampling = !(c.temperature <= 0.0F && c.repeatPenalty == 1.0F);
+    d->sample = c;
+    d->scratch.sampled = d->sampling ? d->sampledToken : nullptr;
+    MUYO_HIP_CHECK(LaunchMt64Seed(d->stream, d->rng, seed));
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_set_history(MuyoDecoder* d, const int32_t* tokens, uint32_t count)
+{
+    if (d == nullptr || (tokens == nullptr && count > 0))
+    {
+        return Fail(MUYO_E_NULL, "decoder_set_history: decoder (and tokens when count > 0) required");
+    }
+    if (count > d->config.maxSeq)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_set_history: %u tokens exceed the cache (%u rows)", count,
+                    d->config.maxSeq);
+    }
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    MUYO_HIP_CHECK(hipMemcpy(d->scratch.history, tokens, static_cast<size_t>(count) * 4, hipMemcpyHostToDevice));
+    return MUYO_OK;
 }
 
 extern "C" int muyo_decoder_set_state(MuyoDecoder* d, int32_t token, int32_t position, void* stream)

@@ -113,10 +113,13 @@ __global__ __launch_bounds__(64) void Mt64SeedKernel(Mt64State* state, uint64_t 
 }
 
 /// history[0..n) with n = *position + 1 (position set) or historyCount, at most historyCount.
-__global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(float* logits, uint32_t vocab,
+/// dst[t] = penalty^d(src[t]) for each token t seen d times in the window, divided by the
+/// temperature when `temperature` > 0 (src and dst may be the same buffer).
+__global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(const float* src, float* dst, uint32_t vocab,
                                                                        const int32_t* __restrict__ history,
                                                                        const int32_t* position, uint32_t historyCount,
-                                                                       int32_t lastN, float penalty, uint32_t* counts)
+                                                                       int32_t lastN, float penalty, float temperature,
+                                                                       uint32_t* counts)
 {
     const uint32_t n = position != nullptr ? min(static_cast<uint32_t>(max(*position, -1) + 1), historyCount)
                                            : historyCount;
@@ -149,22 +152,24 @@ __global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(float* lo
             const uint32_t times = atomicExch(&counts[t], 0u);  // nonzero for one entry per token
             if (times != 0)
             {
-                float v = logits[t];
+                float v = src[t];
                 for (uint32_t j = 0; j < times; ++j)
                 {
                     v = v > 0.0f ? v / penalty : v * penalty;
                 }
-                logits[t] = v;
+                dst[t] = temperature > 0.0f ? v / temperature : v;
             }
         }
     }
 }
 
-__global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(float* logits, uint32_t vocab, float temperature)
+/// dst[i] = src[i] / temperature, or a copy when temperature <= 0.
+__global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* src, float* dst, uint32_t vocab,
+                                                                   float temperature)
 {
     for (uint32_t i = blockIdx.x * kScaleThreads + threadIdx.x; i < vocab; i += gridDim.x * kScaleThreads)
     {
-        logits[i] = logits[i] / temperature;
+        dst[i] = temperature > 0.0f ? src[i] / temperature : src[i];
     }
 }
 
@@ -348,13 +353,25 @@ SampleWorkspace SampleWorkspaceAt(void* base, uint32_t vocab, const SampleConfig
     return ws;
 }
 
+uint32_t SampleLaunches(uint32_t vocab, const SampleConfig& c, bool separate)
+{
+    const bool greedy = c.temperature <= 0.0f;
+    const uint32_t k = greedy ? 1 : SampleTopK(c, vocab);
+    uint32_t launches = (c.repeatPenalty != 1.0f ? 1 : 0) + ((separate || !greedy) ? 1 : 0) + 1;
+    for (uint32_t count = vocab; count > kSampleFinalKeys; count = CeilDiv(count, kSampleSliceKeys) * k)
+    {
+        ++launches;
+    }
+    return launches;
+}
+
 hipError_t LaunchMt64Seed(hipStream_t s, Mt64State* state, uint64_t seed)
 {
     hipLaunchKernelGGL(Mt64SeedKernel, dim3(1), dim3(64), 0, s, state, seed);
     return hipGetLastError();
 }
 
-hipError_t LaunchSample(hipStream_t s, float* logits, uint32_t vocab, const int32_t* history,
+hipError_t LaunchSample(hipStream_t s, const float* src, float* dst, uint32_t vocab, const int32_t* history,
                         const int32_t* position, uint32_t historyCount, const SampleConfig& c, Mt64State* state,
                         const SampleWorkspace& ws, int32_t* token)
 {
@@ -364,19 +381,37 @@ hipError_t LaunchSample(hipStream_t s, float* logits, uint32_t vocab, const int3
     }
     const bool greedy = c.temperature <= 0.0f;
     const uint32_t k = greedy ? 1 : SampleTopK(c, vocab);
-    if (c.repeatPenalty != 1.0f && (position != nullptr || historyCount > 0))
+    const bool penalise = c.repeatPenalty != 1.0f && (position != nullptr || historyCount > 0);
+    const uint32_t scaleBlocks = std::min<uint32_t>(CeilDiv(vocab, kScaleThreads), 1024);
+    // In place, the penalty reads the raw logits before the division; into a separate buffer,
+    // the division (or copy) goes first and the penalty then rewrites the penalised tokens from
+    // the raw logits, divided. Both leave penalty^d(x) / T, as the reference computes it.
+    if (src == dst)
     {
-        hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, logits, vocab, history, position,
-                           historyCount, c.repeatLastN, c.repeatPenalty, ws.counts);
+        if (penalise)
+        {
+            hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
+                               position, historyCount, c.repeatLastN, c.repeatPenalty, 0.0f, ws.counts);
+        }
+        if (!greedy)
+        {
+            hipLaunchKernelGGL(SampleScaleKernel, dim3(scaleBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
+                               c.temperature);
+        }
     }
-    if (!greedy)
+    else
     {
-        const uint32_t blocks = std::min<uint32_t>(CeilDiv(vocab, kScaleThreads), 1024);
-        hipLaunchKernelGGL(SampleScaleKernel, dim3(blocks), dim3(kScaleThreads), 0, s, logits, vocab, c.temperature);
+        hipLaunchKernelGGL(SampleScaleKernel, dim3(scaleBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
+                           c.temperature);
+        if (penalise)
+        {
+            hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
+                               position, historyCount, c.repeatLastN, c.repeatPenalty, c.temperature, ws.counts);
+        }
     }
     // Rounds of slice sorts until the final workgroup can hold every candidate; each round keeps
     // k of 2048 keys per slice (k <= 1024), so the count at least halves.
-    const float* values = logits;
+    const float* values = dst;
     const uint64_t* in = nullptr;
     uint32_t count = vocab;
     uint64_t* out = ws.candA;
@@ -443,7 +478,7 @@ extern "C" int muyo_sample_f32(float* logits, uint32_t vocab, const int32_t* his
                                         "most %u with top_k <= 0); got top_k %d, vocab %u",
                     name, kSampleMaxTopK, kSampleMaxTopK, params->top_k, vocab);
     }
-    const hipError_t launched = LaunchSample(AsStream(stream), logits, vocab, history, nullptr, history_count, c,
+    const hipError_t launched = LaunchSample(AsStream(stream), logits, logits, vocab, history, nullptr, history_count, c,
                                              static_cast<Mt64State*>(state), SampleWorkspaceAt(workspace, vocab, c),
                                              token);
     return launched == hipSuccess ? MUYO_OK : HipStatus(launched, name);

@@ -64,14 +64,17 @@ size_t SampleWorkspaceBytes(uint32_t vocab, const SampleConfig& c);
 /// Carves the three parts out of `base` (SampleWorkspaceBytes long).
 SampleWorkspace SampleWorkspaceAt(void* base, uint32_t vocab, const SampleConfig& c);
 
+/// Kernels LaunchSample enqueues for these parameters (separate: src != dst).
+uint32_t SampleLaunches(uint32_t vocab, const SampleConfig& c, bool separate);
+
 /// Seeds the engine state as std::mt19937_64(seed) does.
 hipError_t LaunchMt64Seed(hipStream_t s, Mt64State* state, uint64_t seed);
 
-/// Samples one token from logits[0..vocab) in place (penalty, then division by the temperature,
-/// as the reference modifies its mapped logits). The history is history[0..n), with n taken
-/// from *position + 1 when `position` is set (the decoder: every position up to the current
-/// one) and from historyCount otherwise. Writes the token to *token.
-hipError_t LaunchSample(hipStream_t s, float* logits, uint32_t vocab, const int32_t* history,
+/// Samples one token from src[0..vocab), leaving the penalised, temperature-divided logits in
+/// dst (dst == src: in place, as the reference modifies its mapped logits). The history is
+/// history[0..n), with n = *position + 1 when `position` is set (the decoder: every position up to
+/// the current one), at most historyCount. Writes the token to *token.
+hipError_t LaunchSample(hipStream_t s, const float* src, float* dst, uint32_t vocab, const int32_t* history,
                         const int32_t* position, uint32_t historyCount, const SampleConfig& c, Mt64State* state,
                         const SampleWorkspace& ws, int32_t* token);
 }  // namespace muyo

@@ -164,6 +164,8 @@ _SIGNATURES = {
     "muyo_decoder_set_state": (ctypes.c_int, [vp, i32, i32, vp]),
     "muyo_decoder_enqueue_kernel": (ctypes.c_int, [vp, u32, u32, vp]),
     "muyo_self_test": (ctypes.c_int, [ctypes.c_char_p]),
+    "muyo_decoder_set_sampler": (ctypes.c_int, [vp, vp]),
+    "muyo_decoder_set_history": (ctypes.c_int, [vp, vp, u32]),
     "muyo_sampler_state_bytes": (ctypes.c_size_t, []),
     "muyo_sampler_seed": (ctypes.c_int, [vp, ctypes.c_uint64, vp]),
     "muyo_sample_workspace_bytes": (ctypes.c_size_t, [u32, vp]),
@@ -465,6 +467,15 @@ class Decoder:
 
     def set_state(self, token: int, position: int, stream: int = 0) -> None:
         check(self.lib.muyo_decoder_set_state(self.handle, token, position, stream))
+
+    def set_sampler(self, **params) -> None:
+        """Sampler::Sample after every step (sampler_params' keywords); no keywords: greedy."""
+        p = sampler_params(**params) if params else None
+        check(self.lib.muyo_decoder_set_sampler(self.handle, ref(p) if p is not None else None))
+
+    def set_history(self, tokens) -> None:
+        arr = (i32 * max(len(tokens), 1))(*[int(t) for t in tokens])
+        check(self.lib.muyo_decoder_set_history(self.handle, arr, len(tokens)))
 
     def enqueue_kernel(self, kernel: str, layer: int = 0, stream: int = 0) -> None:
         check(self.lib.muyo_decoder_enqueue_kernel(self.handle, KERNEL[kernel], layer, stream))

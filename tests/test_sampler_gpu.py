@@ -7,8 +7,6 @@ leaves its mapped logits) bit-identical. A draw could in principle differ where 
 weight sits within a double rounding of the target, since the device's exp is not glibc's; no
 case here comes near one.
 """
-import ctypes
-
 import numpy as np
 import pytest
 
@@ -112,3 +110,79 @@ def test_unsupported_configurations_are_refused(mh, gpu):
     p = mh.sampler_params(temperature=1.0)
     assert lib.muyo_sample_f32(None, 10, None, 0, mh.ref(p), state.data_ptr(), state.data_ptr(), token.data_ptr(),
                                0) == mh.MUYO_E_NULL
+
+
+# ------------------------------------------------------------------------------------------------
+# The decoder's sampling mode: Sampler::Sample after every step, on the device.
+
+SAMPLE_SHAPE = dict(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=5000, max_seq=256)
+DECODER_PARAMS = [
+    dict(temperature=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=42),
+    dict(temperature=1.3, top_k=1024, top_p=0.9, repeat_penalty=1.0, repeat_last_n=64, seed=7),
+    dict(temperature=0.0, top_k=40, top_p=0.95, repeat_penalty=1.3, repeat_last_n=-1, seed=0),
+]
+
+
+def sampled_steps(mh, orc, shape, params, start, steps, seed):
+    """Steps one at a time; each step's token against the oracle sampler fed that step's raw
+    logits and the same history (prompt, then every token embedded since)."""
+    rng = np.random.default_rng(seed)
+    prompt = [int(t) for t in rng.integers(0, shape["vocab"], size=start)]
+    with mh.Decoder(mh.qwen2_config(**shape)) as dec:
+        dec.fill_random(seed)
+        dec.fill_kv_random(start, seed + 1)
+        dec.set_history(prompt)
+        dec.set_sampler(**params)
+        ref = orc.Sampler(**params)
+        history, token, got_ids, want_ids = list(prompt), int(rng.integers(0, shape["vocab"])), [], []
+        for i in range(steps):
+            got = dec.step(token, start + i)
+            logits = np.empty(shape["vocab"], np.float32)
+            dec.download("LOGITS", 0, logits)
+            history.append(token)
+            want = ref.sample(logits, history)
+            got_ids.append(got)
+            want_ids.append(want)
+            token = got
+        return got_ids, want_ids
+
+
+@pytest.mark.parametrize("params", DECODER_PARAMS, ids=["t0.8_k40_pen", "t1.3_k1024", "greedy_pen_all"])
+def test_decoder_sampling_matches_oracle(mh, gpu, orc, params):
+    got, want = sampled_steps(mh, orc, SAMPLE_SHAPE, params, start=60, steps=24, seed=5)
+    assert got == want
+    if params["temperature"] > 0:
+        assert len(set(got)) > 1  # the draws are not degenerate
+
+
+def test_decoder_05b_sampling_32_steps(mh, gpu, orc):
+    """Qwen2.5-0.5B shape, cache pre-filled to 1024, 32 sampled tokens with the reference's usual
+    sampling settings plus a penalty."""
+    params = dict(temperature=0.7, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=2026)
+    got, want = sampled_steps(mh, orc, mh.QWEN25_05B, params, start=1024, steps=32, seed=2027)
+    assert got == want
+
+
+def test_decoder_sampling_graph_replay_matches_steps(mh, gpu, orc):
+    """generate() (graph replay, the sampled token fed back on the device) == one step at a time,
+    from the same seed and history."""
+    params = dict(temperature=1.0, top_k=50, top_p=0.9, repeat_penalty=1.2, repeat_last_n=32, seed=9)
+    prompt = list(range(3, 43))
+    with mh.Decoder(mh.qwen2_config(**SAMPLE_SHAPE)) as dec:
+        dec.fill_random(21)
+        dec.fill_kv_random(40, 22)
+        dec.set_history(prompt)
+        dec.set_sampler(**params)
+        ids = dec.generate(5, 40, 20)
+        launches = dec.launches_per_step()
+        dec.set_history(prompt)
+        dec.set_sampler(**params)
+        token, stepped = 5, []
+        for i in range(20):
+            token = dec.step(token, 40 + i)
+            stepped.append(token)
+        dec.set_sampler()
+        greedy_launches = dec.launches_per_step()
+    assert ids == stepped
+    # Scale into the copy, penalty, one selection round (5000 > 4096 keys) and the final draw.
+    assert launches == greedy_launches + 4
