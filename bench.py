@@ -67,14 +67,18 @@ def gate_up_bytes(c: dict) -> int:
     return 2 * 2 * c["ffn"] * c["hidden"] + 4 * c["hidden"] * 2 + 4 * c["ffn"]
 
 
-def time_decode(mh, torch, shape, position, steps, warmup, seed):
-    """Returns (ms per step, positions timed, decoder launches per step)."""
+def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
+    """Returns (ms per step, positions timed, decoder launches per step). `sampler`: keyword
+    parameters of the device sampler (greedy when None), with a synthetic prompt as history."""
     stream = torch.cuda.current_stream()
     start = max(1, position - steps // 2 - warmup)
     dec = mh.Decoder(mh.qwen2_config(**shape))
     try:
         dec.fill_random(seed)
         dec.fill_kv_random(start, seed + 1)
+        if sampler is not None:
+            dec.set_history([(7919 * i) % shape["vocab"] for i in range(start)])
+            dec.set_sampler(**sampler)
         token = 9707
         dec.generate_async(token, start, warmup, stream.cuda_stream)
         torch.cuda.synchronize()
@@ -403,6 +407,14 @@ def main() -> int:
     gu_gbs = gate_up_bytes(shape) / (kern["gate_up_ms"] * 1e-3) / 1e9
 
     secondary = {}
+    # The same decode with the device sampler after every step (the reference's sampling options
+    # at common settings plus a repetition penalty): its cost per token over greedy.
+    sampling = dict(temperature=0.7, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=seed)
+    ms_s, _, launches_s, _ = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed, sampling)
+    secondary["qwen2.5-0.5b-shape-sampled"] = {
+        "sampler": sampling, "tok_per_s": round(1000.0 / ms_s, 1), "ms_per_step": round(ms_s, 5),
+        "sampler_ms_per_token": round(ms_s - ms, 5), "launches_per_step": launches_s,
+    }
     if not args.no_7b:
         shape7 = dict(mh.QWEN25_7B)
         steps7 = 16

@@ -310,8 +310,9 @@ int muyo_self_test(const char* mode);
  * Among exactly equal logits the top-k order puts the lower index first (the reference leaves it
  * to std::partial_sort). With temperature > 0 the device keeps at most 1024 candidates: top_k must
  * be 1..1024, or <= 0 with vocab <= 1024 (else MUYO_E_UNSUPPORTED). `workspace` is device memory
- * of muyo_sample_workspace_bytes(vocab, params) bytes; it needs no initialisation. The call
- * enqueues a few kernels on `stream` and writes the token to device memory at `token`.
+ * of muyo_sample_workspace_bytes(vocab, params) bytes, zero-filled before its first use (each
+ * call leaves it so). The call enqueues a few kernels on `stream` and writes the token to device
+ * memory at `token`.
  * ------------------------------------------------------------------------------------------- */
 typedef struct MuyoSamplerParams
 {

@@ -4,10 +4,16 @@
 //
 //   Penalty : one workgroup; each token of the last-N window counts its occurrences with global
 //             atomics, and one thread per distinct token applies the penalty that many times in a
-//             row (src/Sampler.cpp:12-29 penalises once per occurrence)
-//   Scale   : logits[i] /= temperature over the vocabulary (src/Sampler.cpp:44-47)
-//   Select  : rounds of workgroups that each sort 2048 (value, index) keys in LDS (bitonic) and
-//             keep their k best, until at most 4096 candidates remain
+//             row (src/Sampler.cpp:12-29 penalises once per occurrence), divides by the
+//             temperature and marks the token done
+//   Scale   : every other logit divided by the temperature (src/Sampler.cpp:44-47); each of 256
+//             workgroups also records the largest key of its slice
+//   Collect : the k-th largest of those 256 maxima is a threshold at least k keys reach, so the
+//             top k lies among the keys at or above it: those (typically a few times k) are
+//             gathered (k <= 256, vocabulary over 4096)
+//   Select  : otherwise, or when over 4096 keys tie at the top: rounds of workgroups that each
+//             sort 2048 keys in LDS (bitonic) and keep their k best, until 4096 remain (launched
+//             every time, they return at once when Collect sufficed)
 //   Final   : one workgroup sorts the candidates, forms the double weights exp(v_i - v_0), cuts
 //             at top-p, draws u from the engine and walks the kept weights to the target
 //             (src/Sampler.cpp:49-98), each sum in the reference's order by a single thread
@@ -25,9 +31,11 @@ namespace muyo
 namespace
 {
 constexpr int kSelectThreads = 256;
-constexpr int kFinalThreads = 1024;
+constexpr int kFinalThreads = 256;
 constexpr int kPenaltyThreads = 1024;
 constexpr int kScaleThreads = 256;
+constexpr uint32_t kThresholdBlocks = 256;  // slices whose maxima set the collection threshold
+constexpr uint32_t kMarked = 0xFFFFFFFFu;   // a count word of a token the penalty finished
 
 // std::mt19937_64's parameters ([rand.predef]: mersenne_twister_engine<uint_fast64_t, 64, 312,
 // 156, 31, 0xb5026f5aa96619e9, 29, 0x5555555555555555, 17, 0x71d67fffeda60000, 37,
@@ -70,31 +78,132 @@ __device__ __forceinline__ float KeyValue(uint64_t key)
 
 __device__ __forceinline__ int32_t KeyIndex(uint64_t key) { return static_cast<int32_t>(~static_cast<uint32_t>(key)); }
 
-/// Sorts kN keys in LDS into descending order (bitonic network; kN a power of two). Ends
-/// synchronised.
+/// LDS slot of key i: one pad word per 16 keys, so the runs of 8 or 16 keys that threads read in
+/// the register stages start in different banks (unpadded, every lane of a wave hit one bank).
+__device__ __forceinline__ uint32_t Slot(uint32_t i) { return i + (i >> 4); }
+
+constexpr uint32_t PaddedKeys(uint32_t n) { return n + n / 16; }
+
+/// Sorts kN keys in LDS (at Slot(i)) into descending order with a bitonic network (kN a power of
+/// two, kN / kThreads keys per thread). Thread t owns the run [t * kPer, t * kPer + kPer): the stages whose
+/// partners lie inside a run (stride < kPer) run in registers, the others through LDS, each pair
+/// as an unconditional max/min write. Ends synchronised.
 template <uint32_t kN, int kThreads>
 __device__ void SortDescending(uint64_t* keys)
 {
+    constexpr uint32_t kPer = kN / kThreads;
+    static_assert(kPer >= 2 && (kPer & (kPer - 1)) == 0, "a power-of-two run per thread");
+    auto inRegisters = [&](uint32_t size, uint32_t topStride) {
+        const uint32_t base = threadIdx.x * kPer;
+        uint64_t v[kPer];
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            v[j] = keys[Slot(base + j)];
+        }
+#pragma unroll
+        for (uint32_t stride = kPer / 2; stride > 0; stride >>= 1)
+        {
+            if (stride <= topStride)
+            {
+#pragma unroll
+                for (uint32_t j = 0; j < kPer; ++j)
+                {
+                    if ((j & stride) == 0)
+                    {
+                        // Blocks of `size` alternate direction; a run can hold several.
+                        const bool descending = ((base + j) & size) == 0;
+                        const uint64_t a = v[j];
+                        const uint64_t b = v[j + stride];
+                        const uint64_t hi = a > b ? a : b;
+                        const uint64_t lo = a > b ? b : a;
+                        v[j] = descending ? hi : lo;
+                        v[j + stride] = descending ? lo : hi;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            keys[Slot(base + j)] = v[j];
+        }
+        __syncthreads();
+    };
     for (uint32_t size = 2; size <= kN; size <<= 1)
     {
-        for (uint32_t stride = size >> 1; stride > 0; stride >>= 1)
+        uint32_t stride = size >> 1;
+        for (; stride >= kPer; stride >>= 1)
         {
-            for (uint32_t t = threadIdx.x; t < kN / 2; t += kThreads)
+            uint64_t a[kPer / 2];
+            uint64_t b[kPer / 2];
+            uint32_t lo[kPer / 2];
+#pragma unroll
+            for (uint32_t j = 0; j < kPer / 2; ++j)
             {
-                const uint32_t lo = 2 * t - (t & (stride - 1));
-                const uint32_t hi = lo + stride;
-                const uint64_t a = keys[lo];
-                const uint64_t b = keys[hi];
-                const bool descending = (lo & size) == 0;
-                if (descending ? a < b : a > b)
-                {
-                    keys[lo] = b;
-                    keys[hi] = a;
-                }
+                const uint32_t t = threadIdx.x + j * kThreads;
+                lo[j] = 2 * t - (t & (stride - 1));
+                a[j] = keys[Slot(lo[j])];
+                b[j] = keys[Slot(lo[j] + stride)];
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < kPer / 2; ++j)
+            {
+                const bool descending = (lo[j] & size) == 0;
+                const uint64_t hi = a[j] > b[j] ? a[j] : b[j];
+                const uint64_t low = a[j] > b[j] ? b[j] : a[j];
+                keys[Slot(lo[j])] = descending ? hi : low;
+                keys[Slot(lo[j] + stride)] = descending ? low : hi;
             }
             __syncthreads();
         }
+        inRegisters(size, stride);
     }
+}
+
+/// Fills LDS with keys base..base+kN-1: values[i] with index i, or earlier candidates in[i]; past
+/// `count`, key 0 (below every real key). Every load is issued before any is used (clamped
+/// indices, no branches). Ends synchronised.
+template <uint32_t kN, int kThreads>
+__device__ void LoadKeys(uint64_t* keys, const float* __restrict__ values, const uint64_t* __restrict__ in,
+                         uint32_t base, uint32_t count)
+{
+    constexpr uint32_t kPer = kN / kThreads;
+    uint64_t v[kPer];
+    if (values != nullptr)
+    {
+        float f[kPer];
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            f[j] = values[min(base + threadIdx.x + j * kThreads, count - 1)];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            const uint32_t i = base + threadIdx.x + j * kThreads;
+            v[j] = i < count ? SampleKey(f[j], i) : 0;
+        }
+    }
+    else
+    {
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            v[j] = in[min(base + threadIdx.x + j * kThreads, count - 1)];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+        {
+            v[j] = base + threadIdx.x + j * kThreads < count ? v[j] : 0;
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j)
+    {
+        keys[Slot(threadIdx.x + j * kThreads)] = v[j];
+    }
+    __syncthreads();
 }
 
 __global__ __launch_bounds__(64) void Mt64SeedKernel(Mt64State* state, uint64_t seed)
@@ -114,7 +223,8 @@ __global__ __launch_bounds__(64) void Mt64SeedKernel(Mt64State* state, uint64_t 
 
 /// history[0..n) with n = *position + 1 (position set) or historyCount, at most historyCount.
 /// dst[t] = penalty^d(src[t]) for each token t seen d times in the window, divided by the
-/// temperature when `temperature` > 0 (src and dst may be the same buffer).
+/// temperature when `temperature` > 0 (src and dst may be the same buffer), and counts[t] set to
+/// kMarked so the scale kernel leaves it (and clears the mark).
 __global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(const float* src, float* dst, uint32_t vocab,
                                                                        const int32_t* __restrict__ history,
                                                                        const int32_t* position, uint32_t historyCount,
@@ -149,8 +259,8 @@ __global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(const flo
         const int32_t t = history[i];
         if (t >= 0 && static_cast<uint32_t>(t) < vocab)
         {
-            const uint32_t times = atomicExch(&counts[t], 0u);  // nonzero for one entry per token
-            if (times != 0)
+            const uint32_t times = atomicExch(&counts[t], kMarked);  // a count for one entry per token
+            if (times != 0 && times != kMarked)
             {
                 float v = src[t];
                 for (uint32_t j = 0; j < times; ++j)
@@ -163,13 +273,126 @@ __global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(const flo
     }
 }
 
-/// dst[i] = src[i] / temperature, or a copy when temperature <= 0.
-__global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* src, float* dst, uint32_t vocab,
-                                                                   float temperature)
+/// The largest of a workgroup's 64-bit keys, in thread 0 (256 threads).
+__device__ __forceinline__ uint64_t BlockMaxKey(uint64_t key, uint64_t* scratch)
 {
-    for (uint32_t i = blockIdx.x * kScaleThreads + threadIdx.x; i < vocab; i += gridDim.x * kScaleThreads)
+    scratch[threadIdx.x] = key;
+    __syncthreads();
+    for (uint32_t half = kScaleThreads / 2; half > 0; half >>= 1)
     {
-        dst[i] = temperature > 0.0f ? src[i] / temperature : src[i];
+        if (threadIdx.x < half)
+        {
+            const uint64_t other = scratch[threadIdx.x + half];
+            scratch[threadIdx.x] = other > scratch[threadIdx.x] ? other : scratch[threadIdx.x];
+        }
+        __syncthreads();
+    }
+    return scratch[0];
+}
+
+/// Workgroup b of kThresholdBlocks owns logits [b * slice, (b + 1) * slice). dst[i] = src[i] /
+/// temperature (a copy when temperature <= 0), except for tokens the penalty marked, whose dst
+/// is final and whose mark is cleared here. With blockMax set, records the slice's largest key
+/// and (workgroup 0) zeroes the collection count.
+__global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* src, float* dst, uint32_t vocab,
+                                                                   float temperature, uint32_t* counts,
+                                                                   uint64_t* blockMax, uint32_t* collected)
+{
+    __shared__ uint64_t scratch[kScaleThreads];
+    const uint32_t slice = (vocab + gridDim.x - 1) / gridDim.x;
+    const uint32_t begin = blockIdx.x * slice;
+    const uint32_t end = min(begin + slice, vocab);
+    uint64_t best = 0;
+    for (uint32_t i = begin + threadIdx.x; i < end; i += kScaleThreads)
+    {
+        float v;
+        if (counts != nullptr && counts[i] == kMarked)
+        {
+            counts[i] = 0;
+            v = dst[i];
+        }
+        else
+        {
+            v = temperature > 0.0f ? src[i] / temperature : src[i];
+            dst[i] = v;
+        }
+        const uint64_t key = SampleKey(v, i);
+        best = key > best ? key : best;
+    }
+    if (blockMax != nullptr)
+    {
+        best = BlockMaxKey(best, scratch);
+        if (threadIdx.x == 0)
+        {
+            blockMax[blockIdx.x] = best;
+            if (blockIdx.x == 0)
+            {
+                *collected = 0;
+            }
+        }
+    }
+}
+
+/// Gathers every key of its slice at or above the threshold: the k-th largest of the
+/// kThresholdBlocks slice maxima (distinct keys when the slice holds any, so one thread finds
+/// itself at rank k - 1). At least k keys reach it: the maxima of rank 0..k-1.
+/// Appends up to kSampleFinalKeys keys to `out`; *collected counts them all, past that too.
+__global__ __launch_bounds__(kScaleThreads) void SampleCollectKernel(const float* __restrict__ values,
+                                                                     uint32_t vocab, uint32_t k,
+                                                                     const uint64_t* __restrict__ blockMax,
+                                                                     uint64_t* __restrict__ out, uint32_t* collected)
+{
+    __shared__ uint64_t maxima[kThresholdBlocks];
+    __shared__ uint64_t threshold;
+    const uint64_t mine = blockMax[threadIdx.x];
+    maxima[threadIdx.x] = mine;
+    if (threadIdx.x == 0)
+    {
+        // Empty slices (small vocabularies) have maximum 0 and share a rank; when rank k - 1 falls
+        // among them, or nowhere, every key is collected.
+        threshold = 0;
+    }
+    __syncthreads();
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < kThresholdBlocks; ++j)
+    {
+        rank += maxima[j] > mine ? 1u : 0u;
+    }
+    if (rank == k - 1 && mine != 0)
+    {
+        threshold = mine;
+    }
+    __syncthreads();
+    const uint64_t floor = threshold;
+    const uint32_t slice = (vocab + gridDim.x - 1) / gridDim.x;
+    const uint32_t begin = blockIdx.x * slice;
+    const uint32_t end = min(begin + slice, vocab);
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    for (uint32_t first = begin; first < end; first += kScaleThreads)
+    {
+        const uint32_t i = first + threadIdx.x;
+        const uint64_t key = i < end ? SampleKey(values[i], i) : 0;
+        const bool take = i < end && key >= floor;
+        // One atomic per wave: the wave's takers get consecutive slots.
+        const uint64_t mask = __ballot(take);
+        if (mask != 0)
+        {
+            const uint32_t leader = static_cast<uint32_t>(__ffsll(static_cast<unsigned long long>(mask)) - 1);
+            uint32_t base = 0;
+            if (lane == leader)
+            {
+                base = atomicAdd(collected, static_cast<uint32_t>(__popcll(mask)));
+            }
+            base = __shfl(base, leader);
+            if (take)
+            {
+                const uint32_t slot = base + static_cast<uint32_t>(__popcll(mask & ((1ull << lane) - 1)));
+                if (slot < kSampleFinalKeys)
+                {
+                    out[slot] = key;
+                }
+            }
+        }
     }
 }
 
@@ -178,48 +401,60 @@ __global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* 
 /// below every real key.
 __global__ __launch_bounds__(kSelectThreads) void SampleSelectKernel(const float* __restrict__ values,
                                                                      const uint64_t* __restrict__ in, uint32_t count,
-                                                                     uint32_t k, uint64_t* __restrict__ out)
+                                                                     uint32_t k, uint64_t* __restrict__ out,
+                                                                     const uint32_t* collected)
 {
-    __shared__ uint64_t keys[kSampleSliceKeys];
-    const uint32_t base = blockIdx.x * kSampleSliceKeys;
-    for (uint32_t j = threadIdx.x; j < kSampleSliceKeys; j += kSelectThreads)
+    if (collected != nullptr && *collected <= kSampleFinalKeys)
     {
-        const uint32_t i = base + j;
-        uint64_t key = 0;
-        if (i < count)
-        {
-            key = values != nullptr ? SampleKey(values[i], i) : in[i];
-        }
-        keys[j] = key;
+        return;  // the collection held every candidate
     }
-    __syncthreads();
+    __shared__ uint64_t keys[PaddedKeys(kSampleSliceKeys)];
+    LoadKeys<kSampleSliceKeys, kSelectThreads>(keys, values, in, blockIdx.x * kSampleSliceKeys, count);
     SortDescending<kSampleSliceKeys, kSelectThreads>(keys);
     for (uint32_t j = threadIdx.x; j < k; j += kSelectThreads)
     {
-        out[static_cast<uint64_t>(blockIdx.x) * k + j] = keys[j];
+        out[static_cast<uint64_t>(blockIdx.x) * k + j] = keys[Slot(j)];
     }
 }
 
+/// Candidates: the collection (`collected` set and at most kSampleFinalKeys keys), else values[]
+/// or the last selection round's keys in[0..count).
 __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* __restrict__ values,
                                                                    const uint64_t* __restrict__ in, uint32_t count,
-                                                                   uint32_t k, float temperature, float topP,
-                                                                   Mt64State* state, int32_t* token)
+                                                                   const uint64_t* __restrict__ gathered,
+                                                                   const uint32_t* collected, uint32_t k,
+                                                                   float temperature, float topP, Mt64State* state,
+                                                                   int32_t* token)
 {
-    __shared__ uint64_t keys[kSampleFinalKeys];
+    __shared__ uint64_t keys[PaddedKeys(kSampleFinalKeys)];
     __shared__ double weight[kSampleMaxTopK];
     __shared__ uint64_t old[kMt64Words];
     __shared__ uint64_t fresh[kMt64Words];
-    for (uint32_t j = threadIdx.x; j < kSampleFinalKeys; j += kFinalThreads)
+    // The engine's index and its next word, requested now so their latency hides under the sort.
+    const uint64_t index = state->next;  // the same for every thread: written only at the end
+    const bool twist = index >= kMt64Words;
+    const uint64_t stored = state->x[twist ? 0 : index];
+    if (collected != nullptr)
     {
-        uint64_t key = 0;
-        if (j < count)
+        const uint32_t n = *collected;
+        if (n <= kSampleFinalKeys)
         {
-            key = values != nullptr ? SampleKey(values[j], j) : in[j];
+            values = nullptr;
+            in = gathered;
+            count = n;
         }
-        keys[j] = key;
     }
-    __syncthreads();
-    SortDescending<kSampleFinalKeys, kFinalThreads>(keys);
+    // The sort covers the next of 512 or 4096 keys (pads sort last).
+    if (count <= 512)
+    {
+        LoadKeys<512, kFinalThreads>(keys, values, in, 0, count);
+        SortDescending<512, kFinalThreads>(keys);
+    }
+    else
+    {
+        LoadKeys<kSampleFinalKeys, kFinalThreads>(keys, values, in, 0, count);
+        SortDescending<kSampleFinalKeys, kFinalThreads>(keys);
+    }
     if (temperature <= 0.0f)
     {
         if (threadIdx.x == 0)
@@ -232,14 +467,12 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
     const float top = KeyValue(keys[0]);
     for (uint32_t j = threadIdx.x; j < k; j += kFinalThreads)
     {
-        weight[j] = exp(static_cast<double>(KeyValue(keys[j]) - top));
+        weight[j] = exp(static_cast<double>(KeyValue(keys[Slot(j)]) - top));
     }
     // The engine's 312 words are used up: the next generation, computed in three dependent
     // phases (words 0..155 from the old state, 156..310 from the new 0..154, 311 from the new 0
     // and 155), as the sequential twist of the standard engine produces it. The word drawn comes
     // from LDS after a twist, so the kernel never reads back state it wrote.
-    const uint64_t index = state->next;  // the same for every thread: written only below
-    const bool twist = index >= kMt64Words;
     if (twist)
     {
         for (uint32_t i = threadIdx.x; i < kMt64Words; i += kFinalThreads)
@@ -247,15 +480,13 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
             old[i] = state->x[i];
         }
         __syncthreads();
-        if (threadIdx.x < kMtShift)
+        for (uint32_t i = threadIdx.x; i < kMtShift; i += kFinalThreads)
         {
-            const uint32_t i = threadIdx.x;
             fresh[i] = MtTwistWord(old[i], old[i + 1], old[i + kMtShift]);
         }
         __syncthreads();
-        if (threadIdx.x >= kMtShift && threadIdx.x < kMt64Words - 1)
+        for (uint32_t i = kMtShift + threadIdx.x; i < kMt64Words - 1; i += kFinalThreads)
         {
-            const uint32_t i = threadIdx.x;
             fresh[i] = MtTwistWord(old[i], old[i + 1], fresh[i - kMtShift]);
         }
         __syncthreads();
@@ -303,7 +534,7 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
     // src/Sampler.cpp:86-98: uniform_real_distribution<double>(0, 1) over the 64-bit engine is
     // one tempered word over 2^64 (the word rounded to double first; a result of 1 becomes the
     // largest double below 1), scaled by the kept mass.
-    const uint64_t word = MtTemper(twist ? fresh[0] : state->x[index]);
+    const uint64_t word = MtTemper(twist ? fresh[0] : stored);
     state->next = twist ? 1 : index + 1;
     double u = static_cast<double>(word) * 0x1p-64;
     if (u >= 1.0)
@@ -322,7 +553,7 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
             break;
         }
     }
-    *token = KeyIndex(keys[chosen]);
+    *token = KeyIndex(keys[Slot(chosen)]);
 }
 
 size_t Align256(size_t bytes) { return (bytes + 255) & ~static_cast<size_t>(255); }
@@ -333,31 +564,53 @@ size_t SampleCandidateKeys(uint32_t vocab, uint32_t k)
     return vocab > kSampleFinalKeys ? static_cast<size_t>(CeilDiv(vocab, kSampleSliceKeys)) * k : 1;
 }
 
-size_t SampleWorkspaceBytes(uint32_t vocab, const SampleConfig& c)
+namespace
 {
-    const uint32_t k = c.temperature <= 0.0f ? 1 : SampleTopK(c, vocab);
-    const size_t cand = SampleCandidateKeys(vocab, k) * sizeof(uint64_t);
-    return Align256(static_cast<size_t>(vocab) * sizeof(uint32_t)) + 2 * Align256(cand);
+uint32_t RunK(const SampleConfig& c, uint32_t vocab) { return c.temperature <= 0.0f ? 1 : SampleTopK(c, vocab); }
+
+/// Collection applies above kSampleFinalKeys logits for k up to the number of slice maxima.
+bool Collects(uint32_t vocab, uint32_t k) { return vocab > kSampleFinalKeys && k <= kThresholdBlocks; }
+
+struct WorkspaceLayout
+{
+    size_t counts, candA, candB, blockMax, gathered, collected, total;
+};
+
+WorkspaceLayout Layout(uint32_t vocab, uint32_t k)
+{
+    WorkspaceLayout l{};
+    const size_t cand = Align256(SampleCandidateKeys(vocab, k) * sizeof(uint64_t));
+    l.counts = 0;
+    l.candA = Align256(static_cast<size_t>(vocab) * sizeof(uint32_t));
+    l.candB = l.candA + cand;
+    l.blockMax = l.candB + cand;
+    l.gathered = l.blockMax + Align256(kThresholdBlocks * sizeof(uint64_t));
+    l.collected = l.gathered + Align256(kSampleFinalKeys * sizeof(uint64_t));
+    l.total = l.collected + 256;
+    return l;
 }
+}  // namespace
+
+size_t SampleWorkspaceBytes(uint32_t vocab, const SampleConfig& c) { return Layout(vocab, RunK(c, vocab)).total; }
 
 SampleWorkspace SampleWorkspaceAt(void* base, uint32_t vocab, const SampleConfig& c)
 {
-    const uint32_t k = c.temperature <= 0.0f ? 1 : SampleTopK(c, vocab);
-    const size_t cand = Align256(SampleCandidateKeys(vocab, k) * sizeof(uint64_t));
+    const WorkspaceLayout l = Layout(vocab, RunK(c, vocab));
     char* p = static_cast<char*>(base);
     SampleWorkspace ws;
-    ws.counts = reinterpret_cast<uint32_t*>(p);
-    p += Align256(static_cast<size_t>(vocab) * sizeof(uint32_t));
-    ws.candA = reinterpret_cast<uint64_t*>(p);
-    ws.candB = reinterpret_cast<uint64_t*>(p + cand);
+    ws.counts = reinterpret_cast<uint32_t*>(p + l.counts);
+    ws.candA = reinterpret_cast<uint64_t*>(p + l.candA);
+    ws.candB = reinterpret_cast<uint64_t*>(p + l.candB);
+    ws.blockMax = reinterpret_cast<uint64_t*>(p + l.blockMax);
+    ws.gathered = reinterpret_cast<uint64_t*>(p + l.gathered);
+    ws.collected = reinterpret_cast<uint32_t*>(p + l.collected);
     return ws;
 }
 
-uint32_t SampleLaunches(uint32_t vocab, const SampleConfig& c, bool separate)
+uint32_t SampleLaunches(uint32_t vocab, const SampleConfig& c, bool)
 {
-    const bool greedy = c.temperature <= 0.0f;
-    const uint32_t k = greedy ? 1 : SampleTopK(c, vocab);
-    uint32_t launches = (c.repeatPenalty != 1.0f ? 1 : 0) + ((separate || !greedy) ? 1 : 0) + 1;
+    const uint32_t k = RunK(c, vocab);
+    uint32_t launches = (c.repeatPenalty != 1.0f ? 1 : 0) + 1 + (Collects(vocab, k) ? 1 : 0) + 1;
     for (uint32_t count = vocab; count > kSampleFinalKeys; count = CeilDiv(count, kSampleSliceKeys) * k)
     {
         ++launches;
@@ -379,38 +632,28 @@ hipError_t LaunchSample(hipStream_t s, const float* src, float* dst, uint32_t vo
     {
         return hipErrorInvalidValue;
     }
-    const bool greedy = c.temperature <= 0.0f;
-    const uint32_t k = greedy ? 1 : SampleTopK(c, vocab);
+    const uint32_t k = RunK(c, vocab);
     const bool penalise = c.repeatPenalty != 1.0f && (position != nullptr || historyCount > 0);
-    const uint32_t scaleBlocks = std::min<uint32_t>(CeilDiv(vocab, kScaleThreads), 1024);
-    // In place, the penalty reads the raw logits before the division; into a separate buffer,
-    // the division (or copy) goes first and the penalty then rewrites the penalised tokens from
-    // the raw logits, divided. Both leave penalty^d(x) / T, as the reference computes it.
-    if (src == dst)
+    const bool collect = Collects(vocab, k);
+    // The penalty goes first and finishes its tokens (penalty, then the division) from the raw
+    // logits; the scale kernel divides the rest. In place or into a separate buffer alike, dst
+    // ends as penalty^d(x) / T, as the reference leaves its logits.
+    if (penalise)
     {
-        if (penalise)
-        {
-            hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
-                               position, historyCount, c.repeatLastN, c.repeatPenalty, 0.0f, ws.counts);
-        }
-        if (!greedy)
-        {
-            hipLaunchKernelGGL(SampleScaleKernel, dim3(scaleBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
-                               c.temperature);
-        }
+        hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
+                           position, historyCount, c.repeatLastN, c.repeatPenalty, c.temperature, ws.counts);
     }
-    else
+    hipLaunchKernelGGL(SampleScaleKernel, dim3(kThresholdBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
+                       c.temperature, penalise ? ws.counts : nullptr, collect ? ws.blockMax : nullptr,
+                       ws.collected);
+    if (collect)
     {
-        hipLaunchKernelGGL(SampleScaleKernel, dim3(scaleBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
-                           c.temperature);
-        if (penalise)
-        {
-            hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
-                               position, historyCount, c.repeatLastN, c.repeatPenalty, c.temperature, ws.counts);
-        }
+        hipLaunchKernelGGL(SampleCollectKernel, dim3(kThresholdBlocks), dim3(kScaleThreads), 0, s, dst, vocab, k,
+                           ws.blockMax, ws.gathered, ws.collected);
     }
     // Rounds of slice sorts until the final workgroup can hold every candidate; each round keeps
-    // k of 2048 keys per slice (k <= 1024), so the count at least halves.
+    // k of 2048 keys per slice (k <= 1024), so the count at least halves. After a collection they
+    // run only when it overflowed.
     const float* values = dst;
     const uint64_t* in = nullptr;
     uint32_t count = vocab;
@@ -418,14 +661,16 @@ hipError_t LaunchSample(hipStream_t s, const float* src, float* dst, uint32_t vo
     while (count > kSampleFinalKeys)
     {
         const uint32_t slices = CeilDiv(count, kSampleSliceKeys);
-        hipLaunchKernelGGL(SampleSelectKernel, dim3(slices), dim3(kSelectThreads), 0, s, values, in, count, k, out);
+        hipLaunchKernelGGL(SampleSelectKernel, dim3(slices), dim3(kSelectThreads), 0, s, values, in, count, k, out,
+                           collect ? ws.collected : nullptr);
         count = slices * k;
         values = nullptr;
         in = out;
         out = out == ws.candA ? ws.candB : ws.candA;
     }
-    hipLaunchKernelGGL(SampleFinalKernel, dim3(1), dim3(kFinalThreads), 0, s, values, in, count, k, c.temperature,
-                       c.topP, state, token);
+    hipLaunchKernelGGL(SampleFinalKernel, dim3(1), dim3(kFinalThreads), 0, s, values, in, count,
+                       collect ? ws.gathered : nullptr, collect ? ws.collected : nullptr, k, c.temperature, c.topP,
+                       state, token);
     return hipGetLastError();
 }
 }  // namespace muyo

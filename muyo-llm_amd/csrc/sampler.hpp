@@ -33,13 +33,17 @@ struct SampleConfig
     int32_t repeatLastN;
 };
 
-/// Device scratch of one sampler: penalty counts (one word per vocabulary entry) and two
-/// candidate buffers of 64-bit (value, index) keys.
+/// Device scratch of one sampler: penalty counts (one word per vocabulary entry; zero between
+/// calls), two candidate buffers of 64-bit (value, index) keys for the selection rounds, the slice
+/// maxima, and the collection with its count.
 struct SampleWorkspace
 {
     uint32_t* counts;
     uint64_t* candA;
     uint64_t* candB;
+    uint64_t* blockMax;
+    uint64_t* gathered;
+    uint32_t* collected;
 };
 
 /// k of the top-k: topK <= 0 means the whole vocabulary (src/Sampler.cpp:49).
@@ -58,10 +62,11 @@ inline bool SampleSupported(const SampleConfig& c, uint32_t vocab)
 /// Candidate keys one buffer holds at most for this vocabulary and k.
 size_t SampleCandidateKeys(uint32_t vocab, uint32_t k);
 
-/// Bytes of SampleWorkspace for the vocabulary and parameters, 256-byte aligned parts.
+/// Bytes of SampleWorkspace for the vocabulary and parameters, 256-byte aligned parts. The
+/// counts must be zero before the first call; every call leaves them zero.
 size_t SampleWorkspaceBytes(uint32_t vocab, const SampleConfig& c);
 
-/// Carves the three parts out of `base` (SampleWorkspaceBytes long).
+/// Carves the parts out of `base` (SampleWorkspaceBytes long).
 SampleWorkspace SampleWorkspaceAt(void* base, uint32_t vocab, const SampleConfig& c);
 
 /// Kernels LaunchSample enqueues for these parameters (separate: src != dst).

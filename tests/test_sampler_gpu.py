@@ -22,7 +22,7 @@ class DeviceSampler:
         self.state = torch.empty(lib.muyo_sampler_state_bytes(), dtype=torch.uint8, device="cuda")
         ws = lib.muyo_sample_workspace_bytes(vocab, mh.ref(self.params))
         assert ws > 0
-        self.ws = torch.empty(ws, dtype=torch.uint8, device="cuda")
+        self.ws = torch.zeros(ws, dtype=torch.uint8, device="cuda")  # zero before the first use
         self.token = torch.empty(1, dtype=torch.int32, device="cuda")
         self.stream = torch.cuda.current_stream().cuda_stream
         mh.check(lib.muyo_sampler_seed(self.state.data_ptr(), self.params.seed, self.stream))
@@ -53,6 +53,9 @@ CASES = [
     (151936, 1.2, 1024, 0.8, 1.0, 64, 1.5),
     (152064, 1.0, 1, 0.95, 1.0, 64, 1.0),
     (151936, 0.0, 40, 0.95, 1.3, -1, 1.0),
+    (4097, 1.0, 256, 0.9, 1.0, 64, 1.0),     # empty slices: the collection takes every key and overflows
+    (20000, 1.0, 256, 0.95, 1.2, 64, 1.0),   # k at the number of slice maxima
+    (20000, 1.0, 257, 0.95, 1.0, 64, 1.0),   # one past: selection rounds only
 ]
 
 
@@ -96,6 +99,24 @@ def test_ties_go_to_the_lower_index(mh, gpu, orc):
     assert dev.sample(logits, [5])[0] == 7
 
 
+@pytest.mark.parametrize("tied", [151936, 5000])
+def test_ties_at_the_top_fall_back_to_the_selection_rounds(mh, gpu, orc, tied):
+    """More than 4096 keys at the collection threshold (all logits equal, or 5000 tied at the top):
+    the collection overflows and the selection rounds decide, still matching the oracle."""
+    vocab = 151936
+    params = dict(temperature=1.0, top_k=40, top_p=0.95, repeat_penalty=1.0, seed=3)
+    dev = DeviceSampler(mh, gpu, vocab, **params)
+    ref = orc.Sampler(**params)
+    rng = np.random.default_rng(tied)
+    logits = (rng.standard_normal(vocab) * 0.5 - 10.0).astype(np.float32)
+    logits[rng.permutation(vocab)[:tied]] = 2.0
+    for step in range(6):
+        got, after = dev.sample(logits, [])
+        expect = logits.copy()
+        assert got == ref.sample(expect, []), f"step {step}"
+        assert np.array_equal(after, expect)
+
+
 def test_unsupported_configurations_are_refused(mh, gpu):
     lib = mh.load()
     state = gpu.empty(lib.muyo_sampler_state_bytes(), dtype=gpu.uint8, device="cuda")
@@ -103,7 +124,7 @@ def test_unsupported_configurations_are_refused(mh, gpu):
     token = gpu.empty(1, dtype=gpu.int32, device="cuda")
     for top_k in (0, 1025):
         p = mh.sampler_params(temperature=1.0, top_k=top_k)
-        ws = gpu.empty(1 << 20, dtype=gpu.uint8, device="cuda")
+        ws = gpu.zeros(1 << 20, dtype=gpu.uint8, device="cuda")
         status = lib.muyo_sample_f32(logits.data_ptr(), 151936, None, 0, mh.ref(p), state.data_ptr(), ws.data_ptr(),
                                      token.data_ptr(), 0)
         assert status == mh.MUYO_E_UNSUPPORTED, top_k
@@ -184,5 +205,6 @@ def test_decoder_sampling_graph_replay_matches_steps(mh, gpu, orc):
         dec.set_sampler()
         greedy_launches = dec.launches_per_step()
     assert ids == stepped
-    # Scale into the copy, penalty, one selection round (5000 > 4096 keys) and the final draw.
-    assert launches == greedy_launches + 4
+    # Penalty, scale with the slice maxima, collection, one selection round (5000 > 4096 keys; it
+    # returns at once unless the collection overflowed) and the final draw.
+    assert launches == greedy_launches + 5
