@@ -155,3 +155,24 @@ int main() {
     }
     for name, pc in want.items():
         assert got[name] == mh.contract_bytes(pc).hex(), name
+
+
+def test_sampler_header_compiles_and_mirrors_sampler_params(tmp_path):
+    """include/muyo/Sampler.h (the device-backed mirror of src/Sampler.h) compiles as C++, and
+    MuyoSamplerParams is the C layout the bindings assume (32 bytes, seed at offset 24)."""
+    probe = tmp_path / "sampler.cpp"
+    probe.write_text(r'''
+#include <cstddef>
+#include <cstdio>
+#include "muyo/Sampler.h"
+static_assert(sizeof(MuyoSamplerParams) == 32, "MuyoSamplerParams layout");
+static_assert(offsetof(MuyoSamplerParams, seed) == 24, "seed offset");
+int Use(float* logits) {
+    muyo_llm::hip::SamplerParams params;
+    params.temperature = 0.7F;
+    muyo_llm::hip::Sampler sampler(params, 151936);
+    return sampler.Sample(logits, 151936, {1, 2, 3});
+}
+''')
+    subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-Wall", "-Werror", "-Wno-unused-command-line-argument",
+                    "-fsyntax-only", "-I", str(ROOT / "include"), str(probe)], check=True)
