@@ -190,12 +190,14 @@ typedef struct MuyoQwen2Config
     uint32_t maxSeq;
     float rmsEps;
     float ropeBase;
+    uint32_t untiedOutput; /* 0: the LM head is TOKEN_EMBD (tied); 1: a separate OUTPUT tensor */
 } MuyoQwen2Config;
 
 typedef struct MuyoDecoder MuyoDecoder;
 
 /* Tensor kinds a caller may address (per layer where noted). Shapes, row-major:
- *   TOKEN_EMBD   fp16 [vocab][hidden]   (also the tied LM head)
+ *   TOKEN_EMBD   fp16 [vocab][hidden]   (also the LM head unless untiedOutput)
+ *   OUTPUT       fp16 [vocab][hidden]   (the LM head when untiedOutput; absent otherwise)
  *   OUTPUT_NORM  f32  [hidden]
  *   ATTN_NORM    f32  [hidden]                               per layer
  *   ATTN_QKV     fp16 [heads*hd + 2*kvHeads*hd][hidden]      per layer (q rows, then k, then v)
@@ -222,12 +224,15 @@ enum
     MUYO_TENSOR_FFN_DOWN = 9,
     MUYO_TENSOR_KCACHE = 10,
     MUYO_TENSOR_VCACHE = 11,
-    MUYO_TENSOR_LOGITS = 12
+    MUYO_TENSOR_LOGITS = 12,
+    MUYO_TENSOR_OUTPUT = 13
 };
 
 /* Allocate a decoder for `config` on the current HIP device. Caches are zeroed. */
 int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** out);
 void muyo_decoder_destroy(MuyoDecoder* decoder);
+/* The configuration the decoder was created with. */
+int muyo_decoder_config(const MuyoDecoder* decoder, MuyoQwen2Config* out);
 
 /* Device address and byte size of one tensor. */
 int muyo_decoder_tensor(MuyoDecoder* decoder, uint32_t kind, uint32_t layer, void** device_ptr, uint64_t* bytes);
@@ -291,6 +296,50 @@ int muyo_decoder_enqueue_kernel(MuyoDecoder* decoder, uint32_t kernel, uint32_t 
  * all. Runs on the current device, synchronously. Returns 0 when every selected test matches its
  * CPU reference, 1 when one does not, MUYO_E_RANGE for an unknown mode. */
 int muyo_self_test(const char* mode);
+
+/* ---------------------------------------------------------------------------------------------
+ * GGUF model files. Replaces the reference's GgufReader (src/Gguf.h:40-103, src/Gguf.cpp:155-373)
+ * and its model load (src/FullModel.cpp:85-108 config, :582-600 tensors, :1022-1032 upload).
+ *
+ * muyo_gguf_open maps the file read-only and parses the header, metadata and tensor table
+ * (MUYO_E_CONTRACT for a bad magic or a truncated table). The lookups convert as GgufReader's do:
+ * *_uint_or and *_float_or cast any numeric or boolean scalar (fallback when absent or not
+ * scalar), *_string_or returns a string value, *_string_array_size the length of a string array
+ * (0 otherwise). Returned strings live until the next string lookup or the close. The data
+ * section starts at the header's end rounded up to general.alignment (32 when absent).
+ * muyo_gguf_tensor_data points into the mapping at an F32 or F16 tensor's bytes
+ * (MUYO_E_UNSUPPORTED for other types, MUYO_E_RANGE past the end of the file).
+ *
+ * muyo_gguf_qwen2_config reads the qwen2.* dimensions and the vocabulary (the length of
+ * tokenizer.ggml.tokens) as the reference does, with headDim = hidden / heads, maxSeq = max_seq,
+ * and untiedOutput = 1 when the file has output.weight. muyo_decoder_load_gguf uploads every
+ * weight of such a file into a decoder of that configuration: token_embd, output_norm, output
+ * (if untied) and per layer attn_norm, attn_q|k|v (stacked into ATTN_QKV), their biases
+ * (ATTN_QKV_B), attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down. Weights must be F16 and norms
+ * and biases F32 with the configuration's dimensions (else MUYO_E_CONTRACT, or
+ * MUYO_E_UNSUPPORTED for quantised types).
+ * ------------------------------------------------------------------------------------------- */
+typedef struct MuyoGguf MuyoGguf;
+
+int muyo_gguf_open(const char* path, MuyoGguf** out);
+void muyo_gguf_close(MuyoGguf* gguf);
+uint32_t muyo_gguf_version(const MuyoGguf* gguf);
+uint64_t muyo_gguf_data_offset(const MuyoGguf* gguf);
+uint64_t muyo_gguf_metadata_count(const MuyoGguf* gguf);
+uint64_t muyo_gguf_tensor_count(const MuyoGguf* gguf);
+/* Entry `index` of the tensor table: name (valid until close), ggml type, dimension count and
+ * dims[0..3] (fastest-varying first, unused ones 1), offset from the data section. */
+int muyo_gguf_tensor_info(const MuyoGguf* gguf, uint64_t index, const char** name, uint32_t* type, uint32_t* n_dims,
+                          uint64_t* dims, uint64_t* offset);
+int muyo_gguf_has(const MuyoGguf* gguf, const char* key);
+uint64_t muyo_gguf_uint_or(const MuyoGguf* gguf, const char* key, uint64_t fallback);
+double muyo_gguf_float_or(const MuyoGguf* gguf, const char* key, double fallback);
+const char* muyo_gguf_string_or(MuyoGguf* gguf, const char* key, const char* fallback);
+uint64_t muyo_gguf_string_array_size(const MuyoGguf* gguf, const char* key);
+const char* muyo_gguf_string_array_at(MuyoGguf* gguf, const char* key, uint64_t index);
+int muyo_gguf_tensor_data(const MuyoGguf* gguf, const char* name, const void** data, uint64_t* bytes);
+int muyo_gguf_qwen2_config(const MuyoGguf* gguf, uint32_t max_seq, MuyoQwen2Config* out);
+int muyo_decoder_load_gguf(MuyoDecoder* decoder, const MuyoGguf* gguf);
 
 /* ---------------------------------------------------------------------------------------------
  * Token sampling on the device. Replaces the reference's host sampler, muyo_llm::Sampler

@@ -88,6 +88,7 @@ struct MuyoDecoder
     char* arena = nullptr;
     size_t arenaBytes = 0;
     TensorSlot tokenEmbd, outputNorm, logits;
+    TensorSlot output;  // the untied LM head (config.untiedOutput); empty when tied to tokenEmbd
     std::vector<TensorSlot> layers;  // layer * kLayerTensorCount + tensor
 
     float* xA = nullptr;
@@ -134,6 +135,10 @@ int Validate(const MuyoQwen2Config& c)
         c.vocab == 0 || c.maxSeq == 0)
     {
         return Fail(MUYO_E_RANGE, "decoder: every dimension must be >= 1");
+    }
+    if (c.untiedOutput > 1)
+    {
+        return Fail(MUYO_E_RANGE, "decoder: untiedOutput must be 0 or 1");
     }
     if (c.heads % c.kvHeads != 0 || c.heads / c.kvHeads > 8)
     {
@@ -246,7 +251,8 @@ hipError_t EnqueueDown(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* r
 
 hipError_t EnqueueLmHead(MuyoDecoder* d, hipStream_t s, const float* x)
 {
-    return LaunchLmHeadArgMax(s, d->dims, x, d->At<float>(d->outputNorm), d->At<uint16_t>(d->tokenEmbd),
+    const TensorSlot& head = d->config.untiedOutput != 0 ? d->output : d->tokenEmbd;
+    return LaunchLmHeadArgMax(s, d->dims, x, d->At<float>(d->outputNorm), d->At<uint16_t>(head),
                               d->At<float>(d->logits), d->scratch);
 }
 
@@ -396,6 +402,10 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->tokenEmbd = place(static_cast<size_t>(c.vocab) * c.hidden * 2);
     d->outputNorm = place(static_cast<size_t>(c.hidden) * 4);
     d->logits = place(static_cast<size_t>(c.vocab) * 4);
+    if (c.untiedOutput != 0)
+    {
+        d->output = place(static_cast<size_t>(c.vocab) * c.hidden * 2);
+    }
     d->layers.resize(static_cast<size_t>(c.layers) * kLayerTensorCount);
     for (uint32_t l = 0; l < c.layers; ++l)
     {
@@ -498,6 +508,16 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     return MUYO_OK;
 }
 
+extern "C" int muyo_decoder_config(const MuyoDecoder* d, MuyoQwen2Config* out)
+{
+    if (d == nullptr || out == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder_config: decoder and out are required");
+    }
+    *out = d->config;
+    return MUYO_OK;
+}
+
 extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
 {
     if (d == nullptr)
@@ -546,6 +566,13 @@ int Lookup(MuyoDecoder* d, uint32_t kind, uint32_t layer, TensorSlot& slot)
             return MUYO_OK;
         case MUYO_TENSOR_LOGITS:
             slot = d->logits;
+            return MUYO_OK;
+        case MUYO_TENSOR_OUTPUT:
+            if (d->config.untiedOutput == 0)
+            {
+                return Fail(MUYO_E_RANGE, "decoder: the LM head is tied to TOKEN_EMBD (config.untiedOutput is 0)");
+            }
+            slot = d->output;
             return MUYO_OK;
         default:
             break;
@@ -629,6 +656,10 @@ extern "C" int muyo_decoder_fill_random(MuyoDecoder* d, uint64_t seed)
     if (status == MUYO_OK)
     {
         status = FillTensor(d, d->outputNorm, false, muyo_tensor_seed(seed, MUYO_TENSOR_OUTPUT_NORM, 0), 1.0, 0.1);
+    }
+    if (status == MUYO_OK && d->config.untiedOutput != 0)
+    {
+        status = FillTensor(d, d->output, true, muyo_tensor_seed(seed, MUYO_TENSOR_OUTPUT, 0), 0.0, 0.02);
     }
     static const struct
     {

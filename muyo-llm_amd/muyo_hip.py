@@ -96,6 +96,7 @@ class MuyoQwen2Config(ctypes.Structure):
     _fields_ = [
         ("layers", u32), ("hidden", u32), ("feedForward", u32), ("heads", u32), ("kvHeads", u32),
         ("headDim", u32), ("vocab", u32), ("maxSeq", u32), ("rmsEps", f32), ("ropeBase", f32),
+        ("untiedOutput", u32),
     ]
 
 
@@ -129,7 +130,7 @@ KERNEL = dict(EMBED=0, QKV=1, ATTENTION=2, O_PROJ=3, GATE_UP=4, DOWN=5, LM_HEAD=
 
 TENSOR = dict(
     TOKEN_EMBD=0, OUTPUT_NORM=1, ATTN_NORM=2, ATTN_QKV=3, ATTN_QKV_B=4, ATTN_OUTPUT=5, FFN_NORM=6,
-    FFN_GATE=7, FFN_UP=8, FFN_DOWN=9, KCACHE=10, VCACHE=11, LOGITS=12,
+    FFN_GATE=7, FFN_UP=8, FFN_DOWN=9, KCACHE=10, VCACHE=11, LOGITS=12, OUTPUT=13,
 )
 
 _SIGNATURES = {
@@ -164,6 +165,25 @@ _SIGNATURES = {
     "muyo_decoder_set_state": (ctypes.c_int, [vp, i32, i32, vp]),
     "muyo_decoder_enqueue_kernel": (ctypes.c_int, [vp, u32, u32, vp]),
     "muyo_self_test": (ctypes.c_int, [ctypes.c_char_p]),
+    "muyo_decoder_config": (ctypes.c_int, [vp, vp]),
+    "muyo_gguf_open": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+    "muyo_gguf_close": (None, [vp]),
+    "muyo_gguf_version": (u32, [vp]),
+    "muyo_gguf_data_offset": (ctypes.c_uint64, [vp]),
+    "muyo_gguf_metadata_count": (ctypes.c_uint64, [vp]),
+    "muyo_gguf_tensor_count": (ctypes.c_uint64, [vp]),
+    "muyo_gguf_tensor_info": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_char_p),
+                                             ctypes.POINTER(u32), ctypes.POINTER(u32),
+                                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "muyo_gguf_has": (ctypes.c_int, [vp, ctypes.c_char_p]),
+    "muyo_gguf_uint_or": (ctypes.c_uint64, [vp, ctypes.c_char_p, ctypes.c_uint64]),
+    "muyo_gguf_float_or": (ctypes.c_double, [vp, ctypes.c_char_p, ctypes.c_double]),
+    "muyo_gguf_string_or": (ctypes.c_char_p, [vp, ctypes.c_char_p, ctypes.c_char_p]),
+    "muyo_gguf_string_array_size": (ctypes.c_uint64, [vp, ctypes.c_char_p]),
+    "muyo_gguf_string_array_at": (ctypes.c_char_p, [vp, ctypes.c_char_p, ctypes.c_uint64]),
+    "muyo_gguf_tensor_data": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.POINTER(vp), ctypes.POINTER(ctypes.c_uint64)]),
+    "muyo_gguf_qwen2_config": (ctypes.c_int, [vp, u32, vp]),
+    "muyo_decoder_load_gguf": (ctypes.c_int, [vp, vp]),
     "muyo_decoder_set_sampler": (ctypes.c_int, [vp, vp]),
     "muyo_decoder_set_history": (ctypes.c_int, [vp, vp, u32]),
     "muyo_sampler_state_bytes": (ctypes.c_size_t, []),
@@ -395,15 +415,83 @@ def contract_bytes(struct_value) -> bytes:
     return bytes(memoryview(struct_value).cast("B"))
 
 
-def qwen2_config(layers, hidden, ffn, heads, kv_heads, head_dim, vocab, max_seq, eps=1e-6, rope_base=1e6):
+def qwen2_config(layers, hidden, ffn, heads, kv_heads, head_dim, vocab, max_seq, eps=1e-6, rope_base=1e6,
+                 untied_output=False):
     c = MuyoQwen2Config()
     c.layers, c.hidden, c.feedForward, c.heads, c.kvHeads = layers, hidden, ffn, heads, kv_heads
     c.headDim, c.vocab, c.maxSeq, c.rmsEps, c.ropeBase = head_dim, vocab, max_seq, eps, rope_base
+    c.untiedOutput = 1 if untied_output else 0
     return c
 
 
 QWEN25_05B = dict(layers=24, hidden=896, ffn=4864, heads=14, kv_heads=2, head_dim=64, vocab=151936, max_seq=2048)
 QWEN25_7B = dict(layers=28, hidden=3584, ffn=18944, heads=28, kv_heads=4, head_dim=128, vocab=152064, max_seq=2048)
+
+
+class Gguf:
+    """A mapped GGUF file (muyo_gguf_* in include/muyo_hip.h)."""
+
+    def __init__(self, path):
+        self.lib = load()
+        handle = vp()
+        check(self.lib.muyo_gguf_open(os.fsencode(path), ctypes.byref(handle)))
+        self.handle = handle
+
+    def close(self):
+        if self.handle:
+            self.lib.muyo_gguf_close(self.handle)
+            self.handle = vp()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def version(self) -> int:
+        return int(self.lib.muyo_gguf_version(self.handle))
+
+    @property
+    def data_offset(self) -> int:
+        return int(self.lib.muyo_gguf_data_offset(self.handle))
+
+    def tensors(self) -> list[tuple[str, int, list[int], int]]:
+        """(name, ggml type, dims fastest-varying first, offset) per table entry."""
+        out = []
+        for i in range(int(self.lib.muyo_gguf_tensor_count(self.handle))):
+            name, typ, nd = ctypes.c_char_p(), u32(), u32()
+            dims, off = (ctypes.c_uint64 * 4)(), ctypes.c_uint64()
+            check(self.lib.muyo_gguf_tensor_info(self.handle, i, ctypes.byref(name), ctypes.byref(typ),
+                                                 ctypes.byref(nd), dims, ctypes.byref(off)))
+            out.append((name.value.decode(), typ.value, list(dims)[:nd.value], off.value))
+        return out
+
+    def uint_or(self, key: str, fallback: int) -> int:
+        return int(self.lib.muyo_gguf_uint_or(self.handle, key.encode(), fallback))
+
+    def float_or(self, key: str, fallback: float) -> float:
+        return float(self.lib.muyo_gguf_float_or(self.handle, key.encode(), fallback))
+
+    def string_or(self, key: str, fallback: str) -> str:
+        return self.lib.muyo_gguf_string_or(self.handle, key.encode(), fallback.encode()).decode()
+
+    def string_array_size(self, key: str) -> int:
+        return int(self.lib.muyo_gguf_string_array_size(self.handle, key.encode()))
+
+    def string_array_at(self, key: str, index: int) -> str | None:
+        v = self.lib.muyo_gguf_string_array_at(self.handle, key.encode(), index)
+        return None if v is None else v.decode()
+
+    def tensor_bytes(self, name: str) -> bytes:
+        data, n = vp(), ctypes.c_uint64()
+        check(self.lib.muyo_gguf_tensor_data(self.handle, name.encode(), ctypes.byref(data), ctypes.byref(n)))
+        return ctypes.string_at(data, n.value)
+
+    def qwen2_config(self, max_seq: int) -> MuyoQwen2Config:
+        c = MuyoQwen2Config()
+        check(self.lib.muyo_gguf_qwen2_config(self.handle, max_seq, ref(c)))
+        return c
 
 
 class Decoder:
@@ -467,6 +555,9 @@ class Decoder:
 
     def set_state(self, token: int, position: int, stream: int = 0) -> None:
         check(self.lib.muyo_decoder_set_state(self.handle, token, position, stream))
+
+    def load_gguf(self, gguf: "Gguf") -> None:
+        check(self.lib.muyo_decoder_load_gguf(self.handle, gguf.handle))
 
     def set_sampler(self, **params) -> None:
         """Sampler::Sample after every step (sampler_params' keywords); no keywords: greedy."""

@@ -533,7 +533,9 @@ int32_t oracle_decode_step(const OracleQwen2* m, int32_t token, int32_t pos, flo
         memcpy(h, next, sizeof(float) * m->hidden);
     }
     oracle_rms_norm(h, m->output_norm, hn, 1, m->hidden, m->rms_eps);               /* final_norm */
-    oracle_mat_vec_f16_f64acc(m->token_embd, hn, logits, m->vocab, m->hidden, m->hidden); /* tied head */
+    /* LM head: output.weight when the model has one (src/FullModel.cpp:583), else the tied table. */
+    const uint16_t* head = m->output != NULL ? m->output : m->token_embd;
+    oracle_mat_vec_f16_f64acc(head, hn, logits, m->vocab, m->hidden, m->hidden);
     const int32_t best = oracle_argmax(logits, m->vocab);
     if (top2 != NULL)
     {

@@ -106,10 +106,11 @@ typedef struct OracleQwen2
     const uint16_t* const* ffn_down; /* [layers] -> [hidden][ffn] */
     uint16_t* const* kcache;         /* [layers] -> [kv_heads][max_seq][head_dim] */
     uint16_t* const* vcache;         /* [layers] -> [kv_heads][max_seq][head_dim] */
+    const uint16_t* output;          /* [vocab][hidden] untied LM head (output.weight), or NULL: token_embd */
 } OracleQwen2;
 
 /* One decode step: embed `token`, run every layer at cache row `pos` (appending k/v as fp16),
- * final norm, tied LM head. Writes `logits` [vocab]; returns the greedy id; top2 (optional)
+ * final norm, LM head (output, or the tied token_embd). Writes `logits` [vocab]; returns the greedy id; top2 (optional)
  * receives the largest two logits. Returns -1 on bad arguments. */
 int32_t oracle_decode_step(const OracleQwen2* m, int32_t token, int32_t pos, float* logits, float* top2);
 

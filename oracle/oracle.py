@@ -56,7 +56,7 @@ _SIGNATURES = {
 # Tensor kind numbers shared with the product's seeding (muyo_tensor_seed).
 KIND = dict(
     TOKEN_EMBD=0, OUTPUT_NORM=1, ATTN_NORM=2, ATTN_QKV=3, ATTN_QKV_B=4, ATTN_OUTPUT=5, FFN_NORM=6,
-    FFN_GATE=7, FFN_UP=8, FFN_DOWN=9, KCACHE=10, VCACHE=11,
+    FFN_GATE=7, FFN_UP=8, FFN_DOWN=9, KCACHE=10, VCACHE=11, OUTPUT=13,
 )
 
 _lib = None
@@ -279,7 +279,7 @@ class _OracleQwen2(ctypes.Structure):
         ("vocab", u32), ("max_seq", u32), ("rms_eps", f32), ("rope_base", f32),
         ("token_embd", vp), ("output_norm", vp),
         ("attn_norm", vp), ("attn_qkv", vp), ("attn_qkv_b", vp), ("attn_out", vp), ("ffn_norm", vp),
-        ("ffn_gate", vp), ("ffn_up", vp), ("ffn_down", vp), ("kcache", vp), ("vcache", vp),
+        ("ffn_gate", vp), ("ffn_up", vp), ("ffn_down", vp), ("kcache", vp), ("vcache", vp), ("output", vp),
     ]
 
 
@@ -293,7 +293,8 @@ class Model:
     PER_LAYER = ("ATTN_NORM", "ATTN_QKV", "ATTN_QKV_B", "ATTN_OUTPUT", "FFN_NORM", "FFN_GATE", "FFN_UP",
                  "FFN_DOWN", "KCACHE", "VCACHE")
 
-    def __init__(self, layers, hidden, ffn, heads, kv_heads, head_dim, vocab, max_seq, eps=1e-6, rope_base=1e6):
+    def __init__(self, layers, hidden, ffn, heads, kv_heads, head_dim, vocab, max_seq, eps=1e-6, rope_base=1e6,
+                 untied_output=False):
         self.layers, self.hidden, self.ffn = layers, hidden, ffn
         self.heads, self.kv_heads, self.head_dim = heads, kv_heads, head_dim
         self.vocab, self.max_seq, self.eps, self.rope_base = vocab, max_seq, eps, rope_base
@@ -306,9 +307,11 @@ class Model:
             "FFN_NORM": ((hidden,), np.float32), "FFN_GATE": ((ffn, hidden), np.uint16),
             "FFN_UP": ((ffn, hidden), np.uint16), "FFN_DOWN": ((hidden, ffn), np.uint16),
             "KCACHE": ((kv_heads, max_seq, head_dim), np.uint16), "VCACHE": ((kv_heads, max_seq, head_dim), np.uint16),
+            "OUTPUT": ((vocab, hidden), np.uint16),
         }
+        self.untied_output = untied_output
         self.t = {}
-        for name in ("TOKEN_EMBD", "OUTPUT_NORM"):
+        for name in ("TOKEN_EMBD", "OUTPUT_NORM") + (("OUTPUT",) if untied_output else ()):
             shape, dt = self.shapes[name]
             self.t[(name, 0)] = np.zeros(shape, dt)
         for layer in range(layers):
@@ -321,7 +324,7 @@ class Model:
     DISTRIBUTION = {
         "TOKEN_EMBD": (0.0, 0.02), "OUTPUT_NORM": (1.0, 0.1), "ATTN_NORM": (1.0, 0.1), "ATTN_QKV": (0.0, 0.02),
         "ATTN_QKV_B": (0.0, 0.02), "ATTN_OUTPUT": (0.0, 0.02), "FFN_NORM": (1.0, 0.1), "FFN_GATE": (0.0, 0.02),
-        "FFN_UP": (0.0, 0.02), "FFN_DOWN": (0.0, 0.02),
+        "FFN_UP": (0.0, 0.02), "FFN_DOWN": (0.0, 0.02), "OUTPUT": (0.0, 0.02),
     }
 
     def fill_random(self, seed: int) -> None:
@@ -350,6 +353,7 @@ class Model:
             self.head_dim, self.vocab, self.max_seq, self.eps, self.rope_base)
         m.token_embd = _p(self.t[("TOKEN_EMBD", 0)])
         m.output_norm = _p(self.t[("OUTPUT_NORM", 0)])
+        m.output = _p(self.t[("OUTPUT", 0)]) if self.untied_output else None
         keep = []
         fields = dict(attn_norm="ATTN_NORM", attn_qkv="ATTN_QKV", attn_qkv_b="ATTN_QKV_B", attn_out="ATTN_OUTPUT",
                       ffn_norm="FFN_NORM", ffn_gate="FFN_GATE", ffn_up="FFN_UP", ffn_down="FFN_DOWN",
