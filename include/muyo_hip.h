@@ -342,6 +342,58 @@ int muyo_gguf_qwen2_config(const MuyoGguf* gguf, uint32_t max_seq, MuyoQwen2Conf
 int muyo_decoder_load_gguf(MuyoDecoder* decoder, const MuyoGguf* gguf);
 
 /* ---------------------------------------------------------------------------------------------
+ * Batched prefill. The reference feeds a prompt one token at a time, a full decode step per
+ * token (feedToken inside runTurn, src/FullModel.cpp:1096-1108,1162-1170), and names batched
+ * prefill with mul_mm and flash_attn as deferred work (docs/Plan.md:277, README.md:120-121,
+ * shaders/llama/mul_mm.comp). muyo_decoder_prefill is that feed done at once: the prompt's rows go
+ * through each layer as GEMMs on the matrix cores and one causal attention, the K/V rows land in
+ * the cache as the steps would have written them, and the last position's logits give the next
+ * token as sampleNext would (greedy, or the decoder's sampler over the whole history).
+ *
+ * Activations reach the matrix cores as split planes: hi = f16(x), lo = f16(x - hi), two uint16
+ * arrays of the same shape; W.hi + W.lo accumulated in f32 keeps ~22 bits of every activation,
+ * so results agree with the f32 token-by-token path to f32 rounding. Every activation must stay
+ * below 65504 in magnitude (f16's range).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Feed tokens[0..count) at cache rows position..position+count-1 (in passes of at most 2048 rows)
+ * and return the next token, as `count` calls of muyo_decoder_step would (their K/V rows, the
+ * token history, the LOGITS of the last position). Synchronous; continue with
+ * muyo_decoder_generate(next_token, position + count, ...). */
+int muyo_decoder_prefill(MuyoDecoder* decoder, const int32_t* tokens, uint32_t count, int32_t position,
+                         int32_t* next_token);
+
+/* The prefill's kernels, on device memory, enqueued on `stream`. Planes and f16 weights are
+ * uint16 arrays; every buffer 16-byte aligned. */
+/* hi/lo planes of x[0..count), count % 4 == 0. */
+int muyo_split_f32_f16x2(const float* x, uint64_t count, void* hi, void* lo, void* stream);
+/* rms_norm (x * rsqrt(mean(x^2) + eps)) * w of each row of x [rows][cols] into planes, cols % 4 == 0. */
+int muyo_rms_norm_split_f16x2(const float* x, const float* w, uint32_t rows, uint32_t cols, float eps, void* hi,
+                              void* lo, void* stream);
+/* out[m][n] = sum_k (a_hi + a_lo)[m][k] * w[n][k] (+ bias[n]) (+ residual[m][n]); a planes
+ * [rows][k], w fp16 [n][k], out/residual f32 [rows][n]; bias and residual may be NULL;
+ * n % 4 == 0, k % 8 == 0. */
+int muyo_gemm_split_f16(const void* a_hi, const void* a_lo, const void* w, const float* bias, const float* residual,
+                        float* out, uint32_t rows, uint32_t n, uint32_t k, void* stream);
+/* h[m][f] = silu(g) * u, g and u the split products with w_gate[f] and w_up[f] (fp16 [ffn][k]),
+ * written as planes [rows][ffn]; ffn % 4 == 0, k % 8 == 0. */
+int muyo_gemm_swiglu_split_f16(const void* a_hi, const void* a_lo, const void* w_gate, const void* w_up, void* h_hi,
+                               void* h_lo, uint32_t rows, uint32_t ffn, uint32_t k, void* stream);
+/* From qkv [rows][(heads + 2 kv_heads) * head_dim] (q rows, k rows, v rows, bias included):
+ * rope_neox at positions pos0 + m with angles pos * rope_pow[j] (rope_pow: device f32
+ * [head_dim / 2], theta_scale^j), q into planes [rows][heads * head_dim], k and v as fp16 into
+ * the caches [kv_heads][max_seq][head_dim] at rows pos0 + m. */
+int muyo_rope_split_append_f16kv(const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads, uint32_t kv_heads,
+                                 uint32_t head_dim, uint32_t max_seq, const float* rope_pow, void* q_hi, void* q_lo,
+                                 void* kcache, void* vcache, void* stream);
+/* Causal GQA attention of the queries at positions pos0 + m (q planes [rows][heads * head_dim])
+ * over cache rows 0..pos0 + m: softmax(scale * K q) . V into planes [rows][heads * head_dim].
+ * head_dim 64 or 128, heads / kv_heads <= 8. */
+int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, const void* kcache, const void* vcache,
+                                 void* out_hi, void* out_lo, uint32_t rows, int32_t pos0, uint32_t heads,
+                                 uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq, float scale, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
  * Token sampling on the device. Replaces the reference's host sampler, muyo_llm::Sampler
  * (src/Sampler.h:16-42, src/Sampler.cpp:10-100), which its decode loop calls on the mapped
  * logits after every step (src/FullModel.cpp:1111-1117).

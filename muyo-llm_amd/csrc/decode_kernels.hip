@@ -1101,7 +1101,7 @@ __device__ __forceinline__ int32_t ReduceArgMaxPartials(const float* __restrict_
 
 __global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, float* argValue, int32_t* argIndex,
                                                          int32_t* sampled, int32_t token, int32_t position,
-                                                         uint32_t argBlocks)
+                                                         uint32_t argBlocks, uint32_t step)
 {
     for (uint32_t b = threadIdx.x; b < argBlocks; b += kBlock)
     {
@@ -1117,7 +1117,7 @@ __global__ __launch_bounds__(kBlock) void SetStateKernel(DecodeState* state, flo
         state->token = token;
         state->position = position;
         state->start = position;
-        state->step = 0;
+        state->step = step;
     }
 }
 
@@ -1468,10 +1468,10 @@ bool MergeInOProj(const DecodeDims& dims)
 }
 
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
-                          int32_t position, uint32_t argBlocks)
+                          int32_t position, uint32_t argBlocks, uint32_t step)
 {
     hipLaunchKernelGGL(SetStateKernel, dim3(1), dim3(kBlock), 0, s, state, scratch.argValue, scratch.argIndex,
-                       scratch.sampled, token, position, argBlocks);
+                       scratch.sampled, token, position, argBlocks, step);
     return hipGetLastError();
 }
 

@@ -94,8 +94,11 @@ uint32_t LmHeadBlocks(const DecodeDims& dims);
 bool MergeInOProj(const DecodeDims& dims);
 
 // Launchers. All return hipGetLastError() after the launch.
+
+/// The state of a run whose next step embeds `token` at `position`; `step` 1 marks that step as
+/// already run (a prefill's last position), so Finalize files its successor as id 0.
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
-                          int32_t position, uint32_t argBlocks);
+                          int32_t position, uint32_t argBlocks, uint32_t step = 0);
 
 hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* state, const DecodeScratch& scratch,
                            uint32_t argBlocks, float* x, int32_t* ids, uint32_t idsCap, uint32_t hidden,

@@ -15,6 +15,7 @@
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
+#include "prefill.hpp"
 #include "sampler.hpp"
 
 using namespace muyo;
@@ -114,6 +115,24 @@ struct MuyoDecoder
     bool warm = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+
+    // Batched prefill (muyo_decoder_prefill): row-major activations of up to prefillRows prompt
+    // tokens, allocated on first use. Split planes (hi, lo) feed the matrix cores.
+    char* prefillArena = nullptr;
+    uint32_t prefillRows = 0;
+    int32_t* pTokens = nullptr;
+    float* pxA = nullptr;   // [rows][hidden] residual stream, ping
+    float* pxB = nullptr;   // pong
+    float* pxMid = nullptr; // after attention
+    float* pQkv = nullptr;  // [rows][qkvRows] projection with bias
+    uint16_t* pNormHi = nullptr;  // [rows][hidden] normalised input of QKV and gate/up
+    uint16_t* pNormLo = nullptr;
+    uint16_t* pQHi = nullptr;  // [rows][qdim] roped queries
+    uint16_t* pQLo = nullptr;
+    uint16_t* pAttnHi = nullptr;  // [rows][qdim] attention output
+    uint16_t* pAttnLo = nullptr;
+    uint16_t* pActHi = nullptr;  // [rows][ffn] swiglu output
+    uint16_t* pActLo = nullptr;
 
     template <typename T>
     T* At(const TensorSlot& slot) const
@@ -536,10 +555,11 @@ extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
     {
         (void)hipStreamSynchronize(d->stream);
     }
-    if (d->arena != nullptr)
+    if (d->arena != nullptr || d->prefillArena != nullptr)
     {
         (void)hipDeviceSynchronize();
         (void)hipFree(d->arena);
+        (void)hipFree(d->prefillArena);
     }
     if (d->stream != nullptr)
     {
@@ -945,4 +965,204 @@ extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint
             return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: unknown kernel %u", kernel);
     }
     return status == hipSuccess ? MUYO_OK : HipStatus(status, "decoder_enqueue_kernel");
+}
+
+namespace
+{
+int EnsurePrefill(MuyoDecoder* d)
+{
+    if (d->prefillArena != nullptr)
+    {
+        return MUYO_OK;
+    }
+    const MuyoQwen2Config& c = d->config;
+    const size_t rows = std::min<uint32_t>(kPrefillRows, c.maxSeq);
+    const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
+    const size_t qkvRows = (static_cast<size_t>(c.heads) + 2 * c.kvHeads) * c.headDim;
+    size_t cursor = 0;
+    auto place = [&cursor](size_t bytes)
+    {
+        const size_t at = cursor;
+        cursor = AlignUp(cursor + bytes);
+        return at;
+    };
+    const size_t tokens = place(rows * 4);
+    const size_t xA = place(rows * c.hidden * 4);
+    const size_t xB = place(rows * c.hidden * 4);
+    const size_t xMid = place(rows * c.hidden * 4);
+    const size_t qkv = place(rows * qkvRows * 4);
+    const size_t normHi = place(rows * c.hidden * 2);
+    const size_t normLo = place(rows * c.hidden * 2);
+    const size_t qHi = place(rows * qdim * 2);
+    const size_t qLo = place(rows * qdim * 2);
+    const size_t attnHi = place(rows * qdim * 2);
+    const size_t attnLo = place(rows * qdim * 2);
+    const size_t actHi = place(rows * c.feedForward * 2);
+    const size_t actLo = place(rows * c.feedForward * 2);
+    char* arena = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&arena), cursor) != hipSuccess)
+    {
+        return Fail(MUYO_E_NOMEM, "decoder_prefill: hipMalloc of %zu bytes failed", cursor);
+    }
+    d->prefillArena = arena;
+    d->prefillRows = static_cast<uint32_t>(rows);
+    d->pTokens = reinterpret_cast<int32_t*>(arena + tokens);
+    d->pxA = reinterpret_cast<float*>(arena + xA);
+    d->pxB = reinterpret_cast<float*>(arena + xB);
+    d->pxMid = reinterpret_cast<float*>(arena + xMid);
+    d->pQkv = reinterpret_cast<float*>(arena + qkv);
+    d->pNormHi = reinterpret_cast<uint16_t*>(arena + normHi);
+    d->pNormLo = reinterpret_cast<uint16_t*>(arena + normLo);
+    d->pQHi = reinterpret_cast<uint16_t*>(arena + qHi);
+    d->pQLo = reinterpret_cast<uint16_t*>(arena + qLo);
+    d->pAttnHi = reinterpret_cast<uint16_t*>(arena + attnHi);
+    d->pAttnLo = reinterpret_cast<uint16_t*>(arena + attnLo);
+    d->pActHi = reinterpret_cast<uint16_t*>(arena + actHi);
+    d->pActLo = reinterpret_cast<uint16_t*>(arena + actLo);
+    return MUYO_OK;
+}
+
+/// One pass of `rows` prompt tokens (already in pTokens) at positions pos0..: every layer as
+/// GEMMs and a causal attention. Returns the residual stream holding the last layer's output.
+int EnqueuePrefillPass(MuyoDecoder* d, hipStream_t s, uint32_t rows, int32_t pos0, float** result)
+{
+    const MuyoQwen2Config& c = d->config;
+    const uint32_t qdim = c.heads * c.headDim;
+    const uint32_t qkvRows = (c.heads + 2 * c.kvHeads) * c.headDim;
+    hipError_t status = LaunchEmbedRows(s, d->At<uint16_t>(d->tokenEmbd), d->pTokens, rows, c.hidden, d->pxA,
+                                        d->scratch.history, pos0, d->scratch.historyCap);
+    if (status != hipSuccess)
+    {
+        return LaunchFailed(status, "prefill embed", 0);
+    }
+    float* x = d->pxA;
+    float* other = d->pxB;
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        uint16_t* kcache = d->At<uint16_t>(d->Layer(l, kKCache));
+        uint16_t* vcache = d->At<uint16_t>(d->Layer(l, kVCache));
+        if ((status = LaunchRmsNormSplit(s, x, d->At<float>(d->Layer(l, kAttnNorm)), rows, c.hidden, c.rmsEps,
+                                         d->pNormHi, d->pNormLo)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill attn_norm", l);
+        }
+        if ((status = LaunchGemmSplit(s, d->pNormHi, d->pNormLo, d->At<uint16_t>(d->Layer(l, kQkv)),
+                                      d->At<float>(d->Layer(l, kQkvBias)), nullptr, d->pQkv, rows, qkvRows,
+                                      c.hidden)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill qkv", l);
+        }
+        if ((status = LaunchRopeSplitAppend(s, d->pQkv, rows, pos0, c.heads, c.kvHeads, c.headDim, c.maxSeq,
+                                            d->dims.ropePow, d->pQHi, d->pQLo, kcache, vcache)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill rope", l);
+        }
+        if ((status = LaunchPrefillAttention(s, d->pQHi, d->pQLo, kcache, vcache, d->pAttnHi, d->pAttnLo, rows, pos0,
+                                             c.heads, c.kvHeads, c.headDim, c.maxSeq, d->dims.attnScale)) !=
+            hipSuccess)
+        {
+            return LaunchFailed(status, "prefill attention", l);
+        }
+        if ((status = LaunchGemmSplit(s, d->pAttnHi, d->pAttnLo, d->At<uint16_t>(d->Layer(l, kOut)), nullptr, x,
+                                      d->pxMid, rows, c.hidden, qdim)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill o_proj", l);
+        }
+        if ((status = LaunchRmsNormSplit(s, d->pxMid, d->At<float>(d->Layer(l, kFfnNorm)), rows, c.hidden, c.rmsEps,
+                                         d->pNormHi, d->pNormLo)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill ffn_norm", l);
+        }
+        if ((status = LaunchGemmSwiGlu(s, d->pNormHi, d->pNormLo, d->At<uint16_t>(d->Layer(l, kGate)),
+                                       d->At<uint16_t>(d->Layer(l, kUp)), d->pActHi, d->pActLo, rows, c.feedForward,
+                                       c.hidden)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill gate_up", l);
+        }
+        if ((status = LaunchGemmSplit(s, d->pActHi, d->pActLo, d->At<uint16_t>(d->Layer(l, kDown)), nullptr,
+                                      d->pxMid, other, rows, c.hidden, c.feedForward)) != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill down", l);
+        }
+        std::swap(x, other);
+    }
+    *result = x;
+    return MUYO_OK;
+}
+}  // namespace
+
+extern "C" int muyo_decoder_prefill(MuyoDecoder* d, const int32_t* tokens, uint32_t count, int32_t position,
+                                    int32_t* next_token)
+{
+    if (d == nullptr || tokens == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder_prefill: decoder and tokens are required");
+    }
+    const MuyoQwen2Config& c = d->config;
+    if (count == 0)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_prefill: at least one token is required");
+    }
+    if (position < 0 || static_cast<uint64_t>(position) + count > c.maxSeq)
+    {
+        return Fail(MUYO_E_RANGE, "decoder_prefill: positions %d..%lld exceed the cache (%u rows)", position,
+                    static_cast<long long>(position) + count - 1, c.maxSeq);
+    }
+    for (uint32_t i = 0; i < count; ++i)
+    {
+        if (tokens[i] < 0 || static_cast<uint32_t>(tokens[i]) >= c.vocab)
+        {
+            return Fail(MUYO_E_RANGE, "decoder_prefill: token %d (index %u) outside [0, %u)", tokens[i], i, c.vocab);
+        }
+    }
+    int status = EnsurePrefill(d);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    // Work queued earlier on other streams (an asynchronous generation) writes the same caches.
+    MUYO_HIP_CHECK(hipDeviceSynchronize());
+    hipStream_t s = d->stream;
+    float* x = nullptr;
+    uint32_t rows = 0;
+    for (uint32_t done = 0; done < count; done += rows)
+    {
+        rows = std::min(d->prefillRows, count - done);
+        MUYO_HIP_CHECK(hipMemcpyAsync(d->pTokens, tokens + done, static_cast<size_t>(rows) * 4,
+                                      hipMemcpyHostToDevice, s));
+        status = EnqueuePrefillPass(d, s, rows, position + static_cast<int32_t>(done), &x);
+        if (status != MUYO_OK)
+        {
+            return status;
+        }
+    }
+    // The last prompt position is the step just run: its logits give the next token, greedy or
+    // sampled, exactly as after a decode step there.
+    const int32_t last = position + static_cast<int32_t>(count) - 1;
+    MUYO_HIP_CHECK(LaunchSetState(s, d->state, d->scratch, tokens[count - 1], last, d->argBlocks, 1));
+    const hipError_t head = EnqueueLmHead(d, s, x + static_cast<size_t>(rows - 1) * c.hidden);
+    if (head != hipSuccess)
+    {
+        return LaunchFailed(head, "prefill lm_head", 0);
+    }
+    if (d->sampling)
+    {
+        const hipError_t sampled =
+            LaunchSample(s, d->At<float>(d->logits), d->sampleLogits, c.vocab, d->scratch.history,
+                         &d->state->position, c.maxSeq, d->sample, d->rng,
+                         SampleWorkspaceAt(d->sampleWorkspace, c.vocab, d->sample), d->sampledToken);
+        if (sampled != hipSuccess)
+        {
+            return LaunchFailed(sampled, "prefill sample", 0);
+        }
+    }
+    MUYO_HIP_CHECK(LaunchFinalize(s, d->state, d->scratch, d->argBlocks, d->ids, kIdsCapacity));
+    int32_t next = 0;
+    MUYO_HIP_CHECK(hipMemcpyAsync(&next, d->ids, sizeof(next), hipMemcpyDeviceToHost, s));
+    MUYO_HIP_CHECK(hipStreamSynchronize(s));
+    if (next_token != nullptr)
+    {
+        *next_token = next;
+    }
+    return MUYO_OK;
 }

@@ -1,0 +1,877 @@
+// Batched-prefill kernels for gfx950: split-f16 GEMMs on v_mfma_f32_32x32x16_f16 with fused
+// epilogues, a causal flash attention over the fp16 cache, and the row-wise glue (embedding,
+// rms_norm into split planes, rope + cache append).
+//
+// Matrix-core lane layout of v_mfma_f32_32x32x16_f16 (D = A.B, A 32x16, B 16x32), as used below:
+// lane l supplies A[l % 32][8 * (l / 32) .. +8] and B[8 * (l / 32) .. +8][l % 32], and receives
+// D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32] in accumulator r (0..15).
+#include <cmath>
+#include <initializer_list>
+
+#include "common.hpp"
+#include "prefill.hpp"
+
+namespace muyo
+{
+namespace
+{
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx16 Mfma(half8 a, half8 b, floatx16 c)
+{
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+/// v = hi + lo to ~21 bits. hi is v with its 13 low mantissa bits cleared: 11 significant bits,
+/// exact in f16. Rounding hi to f16 instead is not safe here: with contraction the compiler feeds
+/// a product straight into v_fma_mix*_f16 (one rounding to f16) for one use and rounds it to f32
+/// first (two roundings) for another, so the stored hi and the hi subtracted for lo can differ by
+/// an f16 ulp near a tie. The bit mask works on the f32 value, and lo = v - hi is exact in f32
+/// before its one rounding into f16. |v| must stay below 65536 (f16's range).
+__device__ __forceinline__ float HiPart(float v) { return __uint_as_float(__float_as_uint(v) & 0xFFFFE000u); }
+
+__device__ __forceinline__ _Float16 HiHalf(float v) { return static_cast<_Float16>(HiPart(v)); }
+
+__device__ __forceinline__ _Float16 LoHalf(float v) { return static_cast<_Float16>(v - HiPart(v)); }
+
+__device__ __forceinline__ void StoreSplit4(uint16_t* hi, uint16_t* lo, uint64_t at, float a, float b, float c,
+                                            float d)
+{
+    const half4 h = {HiHalf(a), HiHalf(b), HiHalf(c), HiHalf(d)};
+    const half4 l = {LoHalf(a), LoHalf(b), LoHalf(c), LoHalf(d)};
+    *reinterpret_cast<half4*>(hi + at) = h;
+    *reinterpret_cast<half4*>(lo + at) = l;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Row-wise glue.
+
+__global__ __launch_bounds__(256) void EmbedRowsKernel(const uint16_t* __restrict__ table,
+                                                       const int32_t* __restrict__ tokens, uint32_t hidden,
+                                                       float* __restrict__ x, int32_t* history, int32_t pos0,
+                                                       uint32_t historyCap)
+{
+    const uint32_t m = blockIdx.x;
+    const int32_t token = tokens[m];
+    const uint16_t* row = table + static_cast<uint64_t>(token) * hidden;
+    float* out = x + static_cast<uint64_t>(m) * hidden;
+    for (uint32_t i = threadIdx.x; i < hidden; i += 256)
+    {
+        out[i] = HalfBitsToFloat(row[i]);
+    }
+    const int64_t position = static_cast<int64_t>(pos0) + m;
+    if (threadIdx.x == 0 && history != nullptr && position >= 0 && position < historyCap)
+    {
+        history[position] = token;
+    }
+}
+
+/// One wave per row: sum of squares across the wave, then (scale * x) * w split into planes.
+__global__ __launch_bounds__(256) void RmsNormSplitKernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          uint32_t rows, uint32_t cols, float eps,
+                                                          uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+{
+    const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+    if (row >= rows)
+    {
+        return;
+    }
+    const uint32_t lane = threadIdx.x % kWave;
+    const float* xr = x + static_cast<uint64_t>(row) * cols;
+    float ss = 0.0f;
+    for (uint32_t i = lane * 4; i < cols; i += 4 * kWave)
+    {
+        const float4 v = *reinterpret_cast<const float4*>(xr + i);
+        ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    ss = GroupSum<kWave>(ss);
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+    for (uint32_t i = lane * 4; i < cols; i += 4 * kWave)
+    {
+        const float4 v = *reinterpret_cast<const float4*>(xr + i);
+        const float4 g = *reinterpret_cast<const float4*>(w + i);
+        StoreSplit4(hi, lo, static_cast<uint64_t>(row) * cols + i, (scale * v.x) * g.x, (scale * v.y) * g.y,
+                    (scale * v.z) * g.z, (scale * v.w) * g.w);
+    }
+}
+
+__global__ __launch_bounds__(256) void SplitF32Kernel(const float* __restrict__ x, uint64_t quads,
+                                                      uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+{
+    for (uint64_t i = blockIdx.x * 256ull + threadIdx.x; i < quads; i += static_cast<uint64_t>(gridDim.x) * 256)
+    {
+        const float4 v = *reinterpret_cast<const float4*>(x + 4 * i);
+        StoreSplit4(hi, lo, 4 * i, v.x, v.y, v.z, v.w);
+    }
+}
+
+/// The decode step's rope and cache append (rope_funcs.glsl:76-114; the fp16 cache rows of
+/// src/FullModel.cpp:771-784) for many positions: one thread per (row, unit), units as in the
+/// decode QKV epilogue: rope pairs (j, j + hd/2) of each q and k head, then pairs of v channels.
+__global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __restrict__ qkv, uint32_t rows,
+                                                             int32_t pos0, uint32_t heads, uint32_t kvHeads,
+                                                             uint32_t headDim, uint32_t maxSeq,
+                                                             const float* __restrict__ ropePow,
+                                                             uint16_t* __restrict__ qhi, uint16_t* __restrict__ qlo,
+                                                             uint16_t* __restrict__ kcache,
+                                                             uint16_t* __restrict__ vcache)
+{
+    const uint32_t half = headDim / 2;
+    const uint32_t ropeUnits = (heads + kvHeads) * half;
+    const uint32_t units = (heads + 2 * kvHeads) * half;
+    const uint64_t index = blockIdx.x * 256ull + threadIdx.x;
+    if (index >= static_cast<uint64_t>(rows) * units)
+    {
+        return;
+    }
+    const uint32_t m = static_cast<uint32_t>(index / units);
+    const uint32_t unit = static_cast<uint32_t>(index % units);
+    const int32_t pos = pos0 + static_cast<int32_t>(m);
+    const uint32_t width = (heads + 2 * kvHeads) * headDim;
+    const float* row = qkv + static_cast<uint64_t>(m) * width;
+    if (unit < ropeUnits)
+    {
+        const uint32_t head = unit / half;
+        const uint32_t j = unit % half;
+        const float s0 = row[head * headDim + j];
+        const float s1 = row[head * headDim + j + half];
+        const float theta = static_cast<float>(pos) * ropePow[j];
+        const float c = cosf(theta);
+        const float sn = sinf(theta);
+        const float o0 = s0 * c - s1 * sn;
+        const float o1 = s0 * sn + s1 * c;
+        if (head < heads)
+        {
+            const uint64_t at = static_cast<uint64_t>(m) * heads * headDim + head * headDim + j;
+            const _Float16 h0 = HiHalf(o0);
+            const _Float16 h1 = HiHalf(o1);
+            qhi[at] = __builtin_bit_cast(uint16_t, h0);
+            qlo[at] = __builtin_bit_cast(uint16_t, LoHalf(o0));
+            qhi[at + half] = __builtin_bit_cast(uint16_t, h1);
+            qlo[at + half] = __builtin_bit_cast(uint16_t, LoHalf(o1));
+        }
+        else
+        {
+            const uint64_t base = (static_cast<uint64_t>(head - heads) * maxSeq + pos) * headDim;
+            kcache[base + j] = FloatToHalfBits(o0);
+            kcache[base + j + half] = FloatToHalfBits(o1);
+        }
+    }
+    else
+    {
+        const uint32_t channel = 2 * (unit - ropeUnits);  // within kvHeads * headDim
+        const uint32_t g = channel / headDim;
+        const uint64_t base = (static_cast<uint64_t>(g) * maxSeq + pos) * headDim + channel % headDim;
+        const float* v = row + (heads + kvHeads) * headDim + channel;
+        vcache[base] = FloatToHalfBits(v[0]);
+        vcache[base + 1] = FloatToHalfBits(v[1]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Split GEMM: out[m][n] = sum_k (ahi + alo)[m][k] * W[n][k]. Each wave owns a 64 (n) x 64 (m)
+// tile as 2 x 2 blocks of 32 x 32 accumulators; the weights are the matrix core's A operand
+// (rows n), the activation planes its B operand (columns m), so a lane ends with four
+// consecutive n of one m per accumulator group: 16-byte stores into row-major [m][n].
+// K advances 64 halves at a time through one LDS tile per operand (rows padded to 144 bytes, so
+// the 16-byte fragment reads of 8 consecutive rows touch distinct banks); the next tile's global
+// loads are in flight while the current one is multiplied.
+
+constexpr int kGemmBK = 64;
+constexpr int kGemmStride = kGemmBK + 8;
+
+/// out = acc + bias[n] + residual[m][n] (either may be null); virtual rows are the weight rows.
+struct PlainEpi
+{
+    const uint16_t* w;
+    const float* bias;
+    const float* residual;
+    float* out;
+    uint32_t n, k;
+
+    __device__ const uint16_t* WRow(uint32_t row) const
+    {
+        return w + static_cast<uint64_t>(row < n ? row : n - 1) * k;
+    }
+
+    __device__ void Finish(const floatx16 (&acc)[2][2], uint32_t n0, uint32_t m0, uint32_t rows) const
+    {
+        const uint32_t lane = threadIdx.x % kWave;
+        const uint32_t h = lane / 32;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+        {
+            const uint32_t m = m0 + mb * 32 + lane % 32;
+            if (m >= rows)
+            {
+                continue;
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+            {
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                {
+                    const uint32_t nn = n0 + nb * 32 + 8 * g + 4 * h;
+                    if (nn >= n)
+                    {
+                        continue;
+                    }
+                    float4 v = make_float4(acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2],
+                                           acc[nb][mb][4 * g + 3]);
+                    const uint64_t at = static_cast<uint64_t>(m) * n + nn;
+                    if (bias != nullptr)
+                    {
+                        const float4 b = *reinterpret_cast<const float4*>(bias + nn);
+                        v.x += b.x;
+                        v.y += b.y;
+                        v.z += b.z;
+                        v.w += b.w;
+                    }
+                    if (residual != nullptr)
+                    {
+                        const float4 r = *reinterpret_cast<const float4*>(residual + at);
+                        v.x = r.x + v.x;
+                        v.y = r.y + v.y;
+                        v.z = r.z + v.z;
+                        v.w = r.w + v.w;
+                    }
+                    *reinterpret_cast<float4*>(out + at) = v;
+                }
+            }
+        }
+    }
+};
+
+/// Gate and up interleaved per wave tile: virtual rows [64 t, 64 t + 32) are gate rows
+/// [32 t, 32 t + 32) and the next 32 the same up rows, so a lane holds g and u of the same
+/// (m, f) and writes silu(g) * u (swiglu.comp's op) as split planes.
+struct SwiGluEpi
+{
+    const uint16_t* gate;
+    const uint16_t* up;
+    uint16_t* hhi;
+    uint16_t* hlo;
+    uint32_t ffn, k;
+
+    __device__ const uint16_t* WRow(uint32_t row) const
+    {
+        const uint32_t f = (row / 64) * 32 + row % 32;
+        const uint64_t offset = static_cast<uint64_t>(f < ffn ? f : ffn - 1) * k;
+        return (row % 64 < 32 ? gate : up) + offset;
+    }
+
+    __device__ void Finish(const floatx16 (&acc)[2][2], uint32_t n0, uint32_t m0, uint32_t rows) const
+    {
+        const uint32_t lane = threadIdx.x % kWave;
+        const uint32_t h = lane / 32;
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+        {
+            const uint32_t m = m0 + mb * 32 + lane % 32;
+            if (m >= rows)
+            {
+                continue;
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+            {
+                const uint32_t f = n0 / 2 + 8 * g + 4 * h;
+                if (f >= ffn)
+                {
+                    continue;
+                }
+                float a[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                {
+                    const float gv = acc[0][mb][4 * g + t];
+                    a[t] = gv / (1.0f + expf(-gv)) * acc[1][mb][4 * g + t];
+                }
+                StoreSplit4(hhi, hlo, static_cast<uint64_t>(m) * ffn + f, a[0], a[1], a[2], a[3]);
+            }
+        }
+    }
+};
+
+template <int kWm, int kWn, typename Epi>
+__global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
+                                                                     const uint16_t* __restrict__ alo, Epi epi,
+                                                                     uint32_t rows, uint32_t k)
+{
+    constexpr int kThreads = kWave * kWm * kWn;
+    constexpr int kBM = 64 * kWm;
+    constexpr int kBN = 64 * kWn;
+    constexpr int kChunks = kGemmBK / 8;  // 16-byte chunks per tile row
+    constexpr int kALoads = 2 * kBM * kChunks / kThreads;
+    constexpr int kWLoads = kBN * kChunks / kThreads;
+    static_assert((2 * kBM * kChunks) % kThreads == 0 && (kBN * kChunks) % kThreads == 0, "tile loads");
+    __shared__ __attribute__((aligned(16))) uint16_t lds[(2 * kBM + kBN) * kGemmStride];
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t m0 = blockIdx.y * kBM;
+    const uint32_t n0 = blockIdx.x * kBN;
+
+    const uint16_t* aSrc[kALoads];
+    uint32_t aDst[kALoads];
+    uint32_t aCol[kALoads];
+#pragma unroll
+    for (int i = 0; i < kALoads; ++i)
+    {
+        const uint32_t c = tid + i * kThreads;
+        const uint32_t plane = c / (kBM * kChunks);
+        const uint32_t row = (c / kChunks) % kBM;
+        const uint32_t cc = c % kChunks;
+        const uint32_t m = m0 + row < rows ? m0 + row : rows - 1;
+        aSrc[i] = (plane == 0 ? ahi : alo) + static_cast<uint64_t>(m) * k + cc * 8;
+        aDst[i] = (plane * kBM + row) * kGemmStride + cc * 8;
+        aCol[i] = cc * 8;
+    }
+    const uint16_t* wSrc[kWLoads];
+    uint32_t wDst[kWLoads];
+    uint32_t wCol[kWLoads];
+#pragma unroll
+    for (int i = 0; i < kWLoads; ++i)
+    {
+        const uint32_t c = tid + i * kThreads;
+        const uint32_t row = c / kChunks;
+        const uint32_t cc = c % kChunks;
+        wSrc[i] = epi.WRow(n0 + row) + cc * 8;
+        wDst[i] = (2 * kBM + row) * kGemmStride + cc * 8;
+        wCol[i] = cc * 8;
+    }
+
+    half8 aReg[kALoads];
+    half8 wReg[kWLoads];
+    auto load = [&](uint32_t k0)
+    {
+#pragma unroll
+        for (int i = 0; i < kALoads; ++i)
+        {
+            aReg[i] = k0 + aCol[i] < k ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
+        }
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i)
+        {
+            wReg[i] = k0 + wCol[i] < k ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
+        }
+    };
+
+    const uint32_t wave = tid / kWave;
+    const uint32_t lane = tid % kWave;
+    const uint32_t wm = wave / kWn;
+    const uint32_t wn = wave % kWn;
+    const uint32_t lrow = lane % 32;
+    const uint32_t lk = (lane / 32) * 8;
+    const uint16_t* wFrag = lds + (2 * kBM + wn * 64 + lrow) * kGemmStride + lk;
+    const uint16_t* hiFrag = lds + (wm * 64 + lrow) * kGemmStride + lk;
+    const uint16_t* loFrag = lds + (kBM + wm * 64 + lrow) * kGemmStride + lk;
+
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+    {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+        {
+            acc[a][b] = floatx16{};
+        }
+    }
+
+    load(0);
+    for (uint32_t k0 = 0; k0 < k; k0 += kGemmBK)
+    {
+        __syncthreads();  // every wave is done with the previous tile
+#pragma unroll
+        for (int i = 0; i < kALoads; ++i)
+        {
+            *reinterpret_cast<half8*>(lds + aDst[i]) = aReg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kWLoads; ++i)
+        {
+            *reinterpret_cast<half8*>(lds + wDst[i]) = wReg[i];
+        }
+        __syncthreads();
+        if (k0 + kGemmBK < k)
+        {
+            load(k0 + kGemmBK);
+        }
+#pragma unroll
+        for (int s = 0; s < kGemmBK / 16; ++s)
+        {
+            half8 wf[2], xh[2], xl[2];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+            {
+                wf[b] = *reinterpret_cast<const half8*>(wFrag + b * 32 * kGemmStride + s * 16);
+                xh[b] = *reinterpret_cast<const half8*>(hiFrag + b * 32 * kGemmStride + s * 16);
+                xl[b] = *reinterpret_cast<const half8*>(loFrag + b * 32 * kGemmStride + s * 16);
+            }
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb)
+            {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                {
+                    acc[nb][mb] = Mfma(wf[nb], xh[mb], acc[nb][mb]);
+                    acc[nb][mb] = Mfma(wf[nb], xl[mb], acc[nb][mb]);
+                }
+            }
+        }
+    }
+    epi.Finish(acc, n0 + wn * 64, m0 + wm * 64, rows);
+}
+
+template <typename Epi>
+hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const Epi& epi, uint32_t rows,
+                      uint32_t virtualRows, uint32_t k)
+{
+    if (rows == 0 || virtualRows == 0 || k == 0)
+    {
+        return hipErrorInvalidValue;
+    }
+    // 128 x 128 tiles when they alone give two workgroups per CU; 64-token tiles otherwise.
+    const uint64_t big = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128);
+    if (big >= 512)
+    {
+        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128)),
+                           dim3(256), 0, s, ahi, alo, epi, rows, k);
+    }
+    else
+    {
+        hipLaunchKernelGGL((GemmSplitKernel<1, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 64)),
+                           dim3(128), 0, s, ahi, alo, epi, rows, k);
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Causal flash attention. A workgroup owns one kv head and 32 consecutive queries; its waves are
+// the query heads of that kv head's group and share each 32-key tile of K and V through LDS (V
+// stored transposed, channel-major). Per wave and tile:
+//   S^T (keys x queries) = K . Q^T on the matrix cores (K the A operand from LDS, Q the B operand
+//   held in registers as split planes), so a lane holds 16 keys of one query and the online
+//   softmax needs only one exchange with the lane 32 away;
+//   O^T (channels x queries) += V^T . P^T with P^T split into planes straight from the S^T
+//   accumulators: the B operand's k slot (h, v) of lane j + 32h is key 16 s + 8 (v / 4) + 4 h +
+//   v % 4 of the tile, and the V^T fragment reads the same keys (two 8-byte LDS reads).
+
+constexpr int kAttnKeys = 32;
+constexpr int kVStride = kAttnKeys + 8;  // halves per transposed V row
+
+template <int kHd>
+__global__ __launch_bounds__(512) void PrefillAttentionKernel(
+    const uint16_t* __restrict__ qhi, const uint16_t* __restrict__ qlo, const uint16_t* __restrict__ kcache,
+    const uint16_t* __restrict__ vcache, uint16_t* __restrict__ ohi, uint16_t* __restrict__ olo, uint32_t rows,
+    int32_t pos0, uint32_t heads, uint32_t kvHeads, uint32_t maxSeq, float scale)
+{
+    constexpr int kKStride = kHd + 8;
+    constexpr int kChunks = kHd / 8;
+    __shared__ __attribute__((aligned(16))) uint16_t kTile[kAttnKeys * kKStride];
+    __shared__ __attribute__((aligned(16))) uint16_t vTile[kHd * kVStride];
+
+    const uint32_t group = heads / kvHeads;
+    const uint32_t tiles = gridDim.x;
+    const uint32_t qtile = tiles - 1 - blockIdx.x;  // longest rows first
+    const uint32_t g = blockIdx.y;
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t h = lane / 32;
+    const uint32_t head = g * group + wave;
+    const uint32_t qdim = heads * kHd;
+    const uint32_t m0 = qtile * 32;
+    const uint32_t mq = m0 + lane % 32 < rows ? m0 + lane % 32 : rows - 1;
+    const int32_t qpos = pos0 + static_cast<int32_t>(mq);
+    const int32_t lastPos = pos0 + static_cast<int32_t>(m0 + 31 < rows ? m0 + 31 : rows - 1);
+    const uint32_t keyTiles = static_cast<uint32_t>(lastPos) / kAttnKeys + 1;
+
+    half8 qh[kHd / 16], ql[kHd / 16];
+    {
+        const uint64_t at = static_cast<uint64_t>(mq) * qdim + head * kHd + 8 * h;
+#pragma unroll
+        for (int s = 0; s < kHd / 16; ++s)
+        {
+            qh[s] = *reinterpret_cast<const half8*>(qhi + at + 16 * s);
+            ql[s] = *reinterpret_cast<const half8*>(qlo + at + 16 * s);
+        }
+    }
+    floatx16 o[kHd / 32];
+#pragma unroll
+    for (int c = 0; c < kHd / 32; ++c)
+    {
+        o[c] = floatx16{};
+    }
+    float runMax = -INFINITY;
+    float runSum = 0.0f;
+    const uint16_t* kBase = kcache + static_cast<uint64_t>(g) * maxSeq * kHd;
+    const uint16_t* vBase = vcache + static_cast<uint64_t>(g) * maxSeq * kHd;
+
+    for (uint32_t kt = 0; kt < keyTiles; ++kt)
+    {
+        __syncthreads();  // every wave is done with the previous tile
+        for (uint32_t c = threadIdx.x; c < kAttnKeys * kChunks; c += blockDim.x)
+        {
+            const uint32_t r = c % kAttnKeys;  // key within the tile
+            const uint32_t cc = c / kAttnKeys;  // 8-channel chunk
+            const uint32_t key = kt * kAttnKeys + r < maxSeq ? kt * kAttnKeys + r : maxSeq - 1;
+            const half8 kv = *reinterpret_cast<const half8*>(kBase + static_cast<uint64_t>(key) * kHd + cc * 8);
+            const half8 vv = *reinterpret_cast<const half8*>(vBase + static_cast<uint64_t>(key) * kHd + cc * 8);
+            *reinterpret_cast<half8*>(kTile + r * kKStride + cc * 8) = kv;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+            {
+                reinterpret_cast<_Float16*>(vTile)[(cc * 8 + i) * kVStride + r] = vv[i];
+            }
+        }
+        __syncthreads();
+
+        floatx16 st = floatx16{};
+        const uint16_t* kFrag = kTile + (lane % 32) * kKStride + 8 * h;
+#pragma unroll
+        for (int s = 0; s < kHd / 16; ++s)
+        {
+            const half8 kf = *reinterpret_cast<const half8*>(kFrag + 16 * s);
+            st = Mfma(kf, qh[s], st);
+            st = Mfma(kf, ql[s], st);
+        }
+        float p[16];
+        float tileMax = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            const int32_t key = static_cast<int32_t>(kt * kAttnKeys + 8 * (r / 4) + 4 * h + r % 4);
+            p[r] = key <= qpos ? st[r] * scale : -INFINITY;
+            tileMax = fmaxf(tileMax, p[r]);
+        }
+        tileMax = fmaxf(tileMax, __shfl_xor(tileMax, 32));
+        const float newMax = fmaxf(runMax, tileMax);  // finite: key 0 is in every query's range
+        const float factor = expf(runMax - newMax);
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+        {
+            p[r] = expf(p[r] - newMax);
+            sum += p[r];
+        }
+        runSum = runSum * factor + sum;
+        runMax = newMax;
+#pragma unroll
+        for (int c = 0; c < kHd / 32; ++c)
+        {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+            {
+                o[c][r] *= factor;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+        {
+            half8 ph, pl;
+#pragma unroll
+            for (int v = 0; v < 8; ++v)
+            {
+                ph[v] = HiHalf(p[8 * s + v]);
+                pl[v] = LoHalf(p[8 * s + v]);
+            }
+#pragma unroll
+            for (int c = 0; c < kHd / 32; ++c)
+            {
+                const _Float16* row =
+                    reinterpret_cast<const _Float16*>(vTile) + (c * 32 + lane % 32) * kVStride + 16 * s + 4 * h;
+                const half4 v0 = *reinterpret_cast<const half4*>(row);
+                const half4 v1 = *reinterpret_cast<const half4*>(row + 8);
+                const half8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[c] = Mfma(vf, ph, o[c]);
+                o[c] = Mfma(vf, pl, o[c]);
+            }
+        }
+    }
+
+    const float total = runSum + __shfl_xor(runSum, 32);
+    const uint32_t m = m0 + lane % 32;
+    if (m < rows)
+    {
+        const float inv = 1.0f / total;
+        const uint64_t base = static_cast<uint64_t>(m) * qdim + head * kHd;
+#pragma unroll
+        for (int c = 0; c < kHd / 32; ++c)
+        {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const uint32_t channel = c * 32 + 8 * q + 4 * h;
+                StoreSplit4(ohi, olo, base + channel, o[c][4 * q] * inv, o[c][4 * q + 1] * inv,
+                            o[c][4 * q + 2] * inv, o[c][4 * q + 3] * inv);
+            }
+        }
+    }
+}
+}  // namespace
+
+hipError_t LaunchEmbedRows(hipStream_t s, const uint16_t* table, const int32_t* tokens, uint32_t rows,
+                           uint32_t hidden, float* x, int32_t* history, int32_t pos0, uint32_t historyCap)
+{
+    hipLaunchKernelGGL(EmbedRowsKernel, dim3(rows), dim3(256), 0, s, table, tokens, hidden, x, history, pos0,
+                       historyCap);
+    return hipGetLastError();
+}
+
+hipError_t LaunchRmsNormSplit(hipStream_t s, const float* x, const float* w, uint32_t rows, uint32_t cols, float eps,
+                              uint16_t* hi, uint16_t* lo)
+{
+    if (rows == 0 || cols == 0 || cols % 4 != 0)
+    {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo);
+    return hipGetLastError();
+}
+
+hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_t* hi, uint16_t* lo)
+{
+    if (count == 0 || count % 4 != 0)
+    {
+        return hipErrorInvalidValue;
+    }
+    const uint64_t quads = count / 4;
+    const uint32_t blocks = static_cast<uint32_t>(quads / 256 + 1 < 4096 ? quads / 256 + 1 : 4096);
+    hipLaunchKernelGGL(SplitF32Kernel, dim3(blocks), dim3(256), 0, s, x, quads, hi, lo);
+    return hipGetLastError();
+}
+
+hipError_t LaunchGemmSplit(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* w,
+                           const float* bias, const float* residual, float* out, uint32_t rows, uint32_t n,
+                           uint32_t k)
+{
+    if (n % 4 != 0 || k % 8 != 0)
+    {
+        return hipErrorInvalidValue;
+    }
+    return LaunchGemm(s, ahi, alo, PlainEpi{w, bias, residual, out, n, k}, rows, n, k);
+}
+
+hipError_t LaunchGemmSwiGlu(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* wgate,
+                            const uint16_t* wup, uint16_t* hhi, uint16_t* hlo, uint32_t rows, uint32_t ffn,
+                            uint32_t k)
+{
+    if (ffn % 4 != 0 || k % 8 != 0)
+    {
+        return hipErrorInvalidValue;
+    }
+    // Two virtual rows (gate, up) per output, in whole 32-row blocks.
+    const uint32_t virtualRows = 2 * CeilDiv(ffn, 32) * 32;
+    return LaunchGemm(s, ahi, alo, SwiGluEpi{wgate, wup, hhi, hlo, ffn, k}, rows, virtualRows, k);
+}
+
+hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads,
+                                 uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, const float* ropePow,
+                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache)
+{
+    const uint64_t total = static_cast<uint64_t>(rows) * (heads + 2 * kvHeads) * (headDim / 2);
+    if (total == 0 || pos0 < 0 || static_cast<uint64_t>(pos0) + rows > maxSeq)
+    {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(RopeSplitAppendKernel, dim3(CeilDiv(total, 256)), dim3(256), 0, s, qkv, rows, pos0, heads,
+                       kvHeads, headDim, maxSeq, ropePow, qhi, qlo, kcache, vcache);
+    return hipGetLastError();
+}
+
+hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint16_t* qlo, const uint16_t* kcache,
+                                  const uint16_t* vcache, uint16_t* ohi, uint16_t* olo, uint32_t rows, int32_t pos0,
+                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale)
+{
+    if (rows == 0 || kvHeads == 0 || heads % kvHeads != 0 || heads / kvHeads > 8 || pos0 < 0 ||
+        static_cast<uint64_t>(pos0) + rows > maxSeq)
+    {
+        return hipErrorInvalidValue;
+    }
+    const dim3 grid(CeilDiv(rows, 32), kvHeads);
+    const dim3 block(kWave * (heads / kvHeads));
+    switch (headDim)
+    {
+        case 64:
+            hipLaunchKernelGGL(PrefillAttentionKernel<64>, grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, olo,
+                               rows, pos0, heads, kvHeads, maxSeq, scale);
+            break;
+        case 128:
+            hipLaunchKernelGGL(PrefillAttentionKernel<128>, grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, olo,
+                               rows, pos0, heads, kvHeads, maxSeq, scale);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+}  // namespace muyo
+
+// ------------------------------------------------------------------------------------------------
+// C ABI (include/muyo_hip.h).
+
+using namespace muyo;
+
+namespace
+{
+bool AllAligned16(std::initializer_list<const void*> pointers)
+{
+    for (const void* p : pointers)
+    {
+        if (p != nullptr && !Aligned16(p))
+        {
+            return false;
+        }
+    }
+    return true;
+}
+
+int Launched(hipError_t status, const char* name)
+{
+    return status == hipSuccess ? MUYO_OK : HipStatus(status, name);
+}
+}  // namespace
+
+extern "C" int muyo_split_f32_f16x2(const float* x, uint64_t count, void* hi, void* lo, void* stream)
+{
+    const char* name = "split_f32_f16x2";
+    if (x == nullptr || hi == nullptr || lo == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: x, hi and lo are required", name);
+    }
+    if (count == 0 || count % 4 != 0 || !AllAligned16({x, hi, lo}))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: count must be a positive multiple of 4 and the buffers 16-byte aligned",
+                    name);
+    }
+    return Launched(LaunchSplitF32(AsStream(stream), x, count, static_cast<uint16_t*>(hi), static_cast<uint16_t*>(lo)),
+                    name);
+}
+
+extern "C" int muyo_rms_norm_split_f16x2(const float* x, const float* w, uint32_t rows, uint32_t cols, float eps,
+                                         void* hi, void* lo, void* stream)
+{
+    const char* name = "rms_norm_split_f16x2";
+    if (x == nullptr || w == nullptr || hi == nullptr || lo == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: x, w, hi and lo are required", name);
+    }
+    if (rows == 0 || cols == 0 || cols % 4 != 0 || !AllAligned16({x, w, hi, lo}))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: rows >= 1, cols a positive multiple of 4, buffers 16-byte aligned", name);
+    }
+    return Launched(LaunchRmsNormSplit(AsStream(stream), x, w, rows, cols, eps, static_cast<uint16_t*>(hi),
+                                       static_cast<uint16_t*>(lo)),
+                    name);
+}
+
+extern "C" int muyo_gemm_split_f16(const void* a_hi, const void* a_lo, const void* w, const float* bias,
+                                   const float* residual, float* out, uint32_t rows, uint32_t n, uint32_t k,
+                                   void* stream)
+{
+    const char* name = "gemm_split_f16";
+    if (a_hi == nullptr || a_lo == nullptr || w == nullptr || out == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: a_hi, a_lo, w and out are required", name);
+    }
+    if (rows == 0 || n == 0 || k == 0 || n % 4 != 0 || k % 8 != 0)
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: rows >= 1, n a positive multiple of 4, k of 8 (got %u x %u x %u)", name,
+                    rows, n, k);
+    }
+    if (!AllAligned16({a_hi, a_lo, w, bias, residual, out}))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: every buffer must be 16-byte aligned", name);
+    }
+    return Launched(LaunchGemmSplit(AsStream(stream), static_cast<const uint16_t*>(a_hi),
+                                    static_cast<const uint16_t*>(a_lo), static_cast<const uint16_t*>(w), bias,
+                                    residual, out, rows, n, k),
+                    name);
+}
+
+extern "C" int muyo_gemm_swiglu_split_f16(const void* a_hi, const void* a_lo, const void* w_gate, const void* w_up,
+                                          void* h_hi, void* h_lo, uint32_t rows, uint32_t ffn, uint32_t k,
+                                          void* stream)
+{
+    const char* name = "gemm_swiglu_split_f16";
+    if (a_hi == nullptr || a_lo == nullptr || w_gate == nullptr || w_up == nullptr || h_hi == nullptr ||
+        h_lo == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: every buffer is required", name);
+    }
+    if (rows == 0 || ffn == 0 || k == 0 || ffn % 4 != 0 || k % 8 != 0)
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: rows >= 1, ffn a positive multiple of 4, k of 8 (got %u x %u x %u)", name,
+                    rows, ffn, k);
+    }
+    if (!AllAligned16({a_hi, a_lo, w_gate, w_up, h_hi, h_lo}))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: every buffer must be 16-byte aligned", name);
+    }
+    return Launched(LaunchGemmSwiGlu(AsStream(stream), static_cast<const uint16_t*>(a_hi),
+                                     static_cast<const uint16_t*>(a_lo), static_cast<const uint16_t*>(w_gate),
+                                     static_cast<const uint16_t*>(w_up), static_cast<uint16_t*>(h_hi),
+                                     static_cast<uint16_t*>(h_lo), rows, ffn, k),
+                    name);
+}
+
+extern "C" int muyo_rope_split_append_f16kv(const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads,
+                                            uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq,
+                                            const float* rope_pow, void* q_hi, void* q_lo, void* kcache,
+                                            void* vcache, void* stream)
+{
+    const char* name = "rope_split_append_f16kv";
+    if (qkv == nullptr || rope_pow == nullptr || q_hi == nullptr || q_lo == nullptr || kcache == nullptr ||
+        vcache == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: every buffer is required", name);
+    }
+    if (rows == 0 || heads == 0 || kv_heads == 0 || head_dim == 0 || head_dim % 2 != 0)
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: rows, heads, kv_heads >= 1 and an even head_dim are required", name);
+    }
+    if (pos0 < 0 || static_cast<uint64_t>(pos0) + rows > max_seq)
+    {
+        return Fail(MUYO_E_RANGE, "%s: positions %d..%lld exceed the cache (%u rows)", name, pos0,
+                    static_cast<long long>(pos0) + rows - 1, max_seq);
+    }
+    return Launched(LaunchRopeSplitAppend(AsStream(stream), qkv, rows, pos0, heads, kv_heads, head_dim, max_seq,
+                                          rope_pow, static_cast<uint16_t*>(q_hi), static_cast<uint16_t*>(q_lo),
+                                          static_cast<uint16_t*>(kcache), static_cast<uint16_t*>(vcache)),
+                    name);
+}
+
+extern "C" int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, const void* kcache,
+                                            const void* vcache, void* out_hi, void* out_lo, uint32_t rows,
+                                            int32_t pos0, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                            uint32_t max_seq, float scale, void* stream)
+{
+    const char* name = "prefill_attention_f16kv";
+    if (q_hi == nullptr || q_lo == nullptr || kcache == nullptr || vcache == nullptr || out_hi == nullptr ||
+        out_lo == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "%s: every buffer is required", name);
+    }
+    if (rows == 0 || kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 8 ||
+        (head_dim != 64 && head_dim != 128))
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "%s: needs rows >= 1, heads %% kv_heads == 0, group <= 8, head_dim 64 or 128",
+                    name);
+    }
+    if (pos0 < 0 || static_cast<uint64_t>(pos0) + rows > max_seq)
+    {
+        return Fail(MUYO_E_RANGE, "%s: positions %d..%lld exceed the cache (%u rows)", name, pos0,
+                    static_cast<long long>(pos0) + rows - 1, max_seq);
+    }
+    if (!AllAligned16({q_hi, q_lo, kcache, vcache, out_hi, out_lo}))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: every buffer must be 16-byte aligned", name);
+    }
+    return Launched(LaunchPrefillAttention(AsStream(stream), static_cast<const uint16_t*>(q_hi),
+                                           static_cast<const uint16_t*>(q_lo), static_cast<const uint16_t*>(kcache),
+                                           static_cast<const uint16_t*>(vcache), static_cast<uint16_t*>(out_hi),
+                                           static_cast<uint16_t*>(out_lo), rows, pos0, heads, kv_heads, head_dim,
+                                           max_seq, scale),
+                    name);
+}

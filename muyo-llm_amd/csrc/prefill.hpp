@@ -1,0 +1,54 @@
+// Batched prefill: a prompt of many tokens through every layer at once, as GEMMs on the matrix
+// cores and a causal flash attention, instead of one decode step per prompt token.
+//
+// Activations enter the matrix cores as two f16 planes: hi = x with its 13 low mantissa bits
+// cleared (exact in f16) and lo = f16(x - hi). The weights are exact in f16, so W.hi + W.lo with
+// f32 accumulation carries ~21 bits of each activation, close to the f32 path that feeds the
+// prompt one token at a time.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace muyo
+{
+/// Rows (prompt tokens) of one prefill pass; longer prompts run in passes of at most this many.
+constexpr uint32_t kPrefillRows = 2048;
+
+/// x[m] = f32(table[tokens[m]]) for m < rows; history[pos0 + m] = tokens[m] where it fits.
+hipError_t LaunchEmbedRows(hipStream_t s, const uint16_t* table, const int32_t* tokens, uint32_t rows,
+                           uint32_t hidden, float* x, int32_t* history, int32_t pos0, uint32_t historyCap);
+
+/// y = (x * rsqrt(mean(x^2) + eps)) * w per row of `cols`, written as f16 hi/lo planes [rows][cols].
+hipError_t LaunchRmsNormSplit(hipStream_t s, const float* x, const float* w, uint32_t rows, uint32_t cols, float eps,
+                              uint16_t* hi, uint16_t* lo);
+
+/// hi/lo planes of a plain f32 matrix (no norm): count values, count % 4 == 0.
+hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_t* hi, uint16_t* lo);
+
+/// out[m][n] = sum_k (ahi + alo)[m][k] * w[n][k] + bias[n] (bias may be null) + residual[m][n]
+/// (residual may be null). A is [rows][k] (two planes), W is [n][k] f16, out is [rows][n] f32.
+hipError_t LaunchGemmSplit(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* w,
+                           const float* bias, const float* residual, float* out, uint32_t rows, uint32_t n,
+                           uint32_t k);
+
+/// h[m][f] = silu(g) * u with g = A.gate[f], u = A.up[f] (same split product), written as f16
+/// hi/lo planes [rows][ffn].
+hipError_t LaunchGemmSwiGlu(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* wgate,
+                            const uint16_t* wup, uint16_t* hhi, uint16_t* hlo, uint32_t rows, uint32_t ffn,
+                            uint32_t k);
+
+/// From the QKV projection rows [rows][(heads + 2 kvHeads) * headDim] (bias included): rope_neox
+/// on q and k at positions pos0 + m, q as hi/lo planes [rows][heads * headDim], k and v appended
+/// to the fp16 caches [kvHeads][maxSeq][headDim] at rows pos0 + m.
+hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads,
+                                 uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, const float* ropePow,
+                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache);
+
+/// Causal attention of the queries at positions pos0 + m (m < rows) over cache rows 0..pos0 + m:
+/// out[m][h * headDim + c] as hi/lo planes [rows][heads * headDim].
+hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint16_t* qlo, const uint16_t* kcache,
+                                  const uint16_t* vcache, uint16_t* ohi, uint16_t* olo, uint32_t rows, int32_t pos0,
+                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale);
+}  // namespace muyo

@@ -190,6 +190,13 @@ _SIGNATURES = {
     "muyo_sampler_seed": (ctypes.c_int, [vp, ctypes.c_uint64, vp]),
     "muyo_sample_workspace_bytes": (ctypes.c_size_t, [u32, vp]),
     "muyo_sample_f32": (ctypes.c_int, [vp, u32, vp, u32, vp, vp, vp, vp, vp]),
+    "muyo_decoder_prefill": (ctypes.c_int, [vp, vp, u32, i32, ctypes.POINTER(i32)]),
+    "muyo_split_f32_f16x2": (ctypes.c_int, [vp, ctypes.c_uint64, vp, vp, vp]),
+    "muyo_rms_norm_split_f16x2": (ctypes.c_int, [vp, vp, u32, u32, f32, vp, vp, vp]),
+    "muyo_gemm_split_f16": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, u32, vp]),
+    "muyo_gemm_swiglu_split_f16": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, u32, vp]),
+    "muyo_rope_split_append_f16kv": (ctypes.c_int, [vp, u32, i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp]),
+    "muyo_prefill_attention_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, i32, u32, u32, u32, u32, f32, vp]),
     "muyo_fill_normal_f16": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_normal_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_uniform_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, vp]),
@@ -535,6 +542,15 @@ class Decoder:
     def step(self, token: int, position: int) -> int:
         nxt = i32()
         check(self.lib.muyo_decoder_step(self.handle, token, position, ctypes.byref(nxt)))
+        return nxt.value
+
+    def prefill(self, tokens, position: int = 0) -> int:
+        """Feed a prompt at cache rows position.. in one batched pass; returns the next token."""
+        import numpy as np
+
+        arr = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32))
+        nxt = i32()
+        check(self.lib.muyo_decoder_prefill(self.handle, arr.ctypes.data, arr.size, position, ctypes.byref(nxt)))
         return nxt.value
 
     def generate(self, token: int, position: int, count: int, stream: int = 0) -> list[int]:

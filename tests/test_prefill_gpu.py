@@ -1,0 +1,436 @@
+"""Batched prefill on the GPU against the token-by-token path it replaces.
+
+The reference feeds a prompt one decode step per token (feedToken, src/FullModel.cpp:1096-1108,
+1162-1170), so the oracle for a prompt is the oracle's decode step run at each of its positions,
+and for each prefill kernel the oracle's per-token op at each row: GEMV (MatVec.cpp:52-60, f64
+accumulation), rms_norm (RmsNorm.cpp:194-216), rope_neox (Rope.cpp:48-51,191-203), swiglu
+(Swiglu.cpp:56) and the cache attention (Attention.cpp:253-294).
+
+Tolerances, mixed form |a - e| <= tol * (1 + |e|): the decode bar (GEMV, swiglu, rope 1e-3;
+rms_norm 1e-5; logits 1e-3; greedy ids identical) and, for the split products, a bound 50x
+tighter than what f16-rounded activations alone reach, which fails if the lo plane is dropped.
+Split planes and cache rows are checked bit-for-bit where f16 rounding fixes them.
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from conftest import close, worst
+
+pytestmark = pytest.mark.gpu
+
+_libm = ctypes.CDLL("libm.so.6")
+_libm.powf.restype = ctypes.c_float
+_libm.powf.argtypes = [ctypes.c_float, ctypes.c_float]
+
+
+def dev(torch, array):
+    return torch.from_numpy(np.ascontiguousarray(array)).cuda()
+
+
+def host(t):
+    return t.detach().cpu().numpy()
+
+
+def stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def run(mh, torch, status):
+    mh.check(status)
+    torch.cuda.synchronize()
+
+
+def planes(torch, shape):
+    return (torch.zeros(shape, dtype=torch.int16, device="cuda"), torch.zeros(shape, dtype=torch.int16, device="cuda"))
+
+
+def joined(hi, lo):
+    """hi + lo as f64 from two uint16 planes (device tensors)."""
+    h = host(hi).view(np.uint16).view(np.float16).astype(np.float64)
+    l = host(lo).view(np.uint16).view(np.float16).astype(np.float64)
+    return h + l
+
+
+def split_np(x):
+    """The split the kernels make: hi = x with its 13 low mantissa bits cleared (exact in f16 in
+    f16's normal range), lo = f16(x - hi) rounded to nearest even."""
+    x = np.ascontiguousarray(x, np.float32)
+    hi32 = (x.view(np.uint32) & np.uint32(0xFFFFE000)).view(np.float32)
+    return hi32.astype(np.float16).view(np.uint16), (x - hi32).astype(np.float16).view(np.uint16)
+
+
+def rope_pow(theta_scale, head_dim):
+    """theta_scale^j with the C library's powf, as the decoder computes its table."""
+    return np.array([_libm.powf(theta_scale, float(j)) for j in range(head_dim // 2)], np.float32)
+
+
+# ------------------------------------------------------------------------------------------------
+# Split planes
+
+
+def test_split_planes_are_f16_and_remainder(mh, gpu):
+    torch = gpu
+    rng = np.random.default_rng(1)
+    x = np.concatenate([rng.normal(0, 1, 4000), rng.normal(0, 300, 4000), [0.0, -0.0, 1e-8, 65000.0, -3.1415927]])
+    x = np.resize(x.astype(np.float32), 8012)
+    hi, lo = planes(torch, x.shape)
+    xd = dev(torch, x)
+    run(mh, torch, mh.load().muyo_split_f32_f16x2(xd.data_ptr(), x.size, hi.data_ptr(), lo.data_ptr(), stream(torch)))
+    want_hi, want_lo = split_np(x)
+    normal = np.abs(x) >= 2.0 ** -14  # below, hi itself is an f16 subnormal and rounds
+    assert np.array_equal(host(hi).view(np.uint16)[normal], want_hi[normal])
+    assert np.array_equal(host(lo).view(np.uint16)[normal], want_lo[normal])
+    # hi + lo holds x to 2^-21 of its magnitude (f16 subnormals aside).
+    err = np.abs(joined(hi, lo) - x.astype(np.float64))
+    assert np.all(err <= np.abs(x) * 2.0 ** -21 + 2.0 ** -24)
+
+
+def test_rms_norm_split_matches_oracle(mh, gpu, orc):
+    torch = gpu
+    for rows, cols, seed in ((1, 896, 3), (37, 896, 4), (5, 3584, 5), (9, 200, 6)):
+        x = orc.normal_f32(rows * cols, seed).reshape(rows, cols) * 3
+        w = orc.normal_f32(cols, seed + 100, 1.0, 0.1)
+        hi, lo = planes(torch, (rows, cols))
+        xd, wd = dev(torch, x), dev(torch, w)
+        run(mh, torch, mh.load().muyo_rms_norm_split_f16x2(xd.data_ptr(), wd.data_ptr(), rows, cols, 1e-6,
+                                                           hi.data_ptr(), lo.data_ptr(), stream(torch)))
+        want = orc.rms_norm(x, w, 1e-6)
+        assert close(joined(hi, lo), want, 1e-5) == 0, (rows, cols)
+        assert worst(joined(hi, lo), want) < 1e-6
+
+
+# ------------------------------------------------------------------------------------------------
+# GEMMs
+
+GEMM_SHAPES = [
+    (1, 8, 8),          # one token, one 16-byte chunk of K
+    (37, 100, 72),      # ragged rows, n not a multiple of 32, k not of 64
+    (128, 128, 64),     # exactly one 128 x 128 tile
+    (200, 1152, 896),   # 0.5B QKV
+    (300, 896, 896),    # 0.5B o_proj
+    (67, 896, 4864),    # 0.5B down: long K
+    (640, 1152, 896),   # enough tiles for the 128 x 128 launch
+]
+
+
+def oracle_gemm(orc, w_bits, a):
+    """Each row through the oracle's GEMV (f64 accumulation), as the token-by-token feed does."""
+    return np.stack([orc.mat_vec_f16(w_bits, row, f64acc=True) for row in a])
+
+
+@pytest.mark.parametrize("rows,n,k", GEMM_SHAPES)
+def test_gemm_split_matches_per_token_gemv(mh, gpu, orc, rows, n, k):
+    torch = gpu
+    seed = rows * 7 + n * 3 + k
+    a = orc.normal_f32(rows * k, seed).reshape(rows, k)
+    w = orc.normal_f16(n * k, seed + 1, 0.0, 0.02).reshape(n, k)
+    bias = orc.normal_f32(n, seed + 2, 0.0, 0.02)
+    residual = orc.normal_f32(rows * n, seed + 3).reshape(rows, n)
+    ahi, alo = split_np(a)
+    out = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    lib = mh.load()
+    keep = [dev(torch, ahi), dev(torch, alo), dev(torch, w), dev(torch, bias), dev(torch, residual)]
+    args = tuple(t.data_ptr() for t in keep[:3])
+    run(mh, torch, lib.muyo_gemm_split_f16(*args, keep[3].data_ptr(), None, out.data_ptr(), rows, n, k,
+                                           stream(torch)))
+    plain = oracle_gemm(orc, w, a)
+    got = host(out)
+    want = plain + bias
+    assert close(got, want, 1e-3) == 0
+    # Split precision: f16-rounded activations alone miss by ~1e-3 relative; the planes must do
+    # 50x better than that.
+    f16_only = oracle_gemm(orc, w, a.astype(np.float16).astype(np.float32)) + bias
+    assert worst(got, want) * 50 < max(worst(f16_only, want), 1e-5) or worst(got, want) < 2e-7
+    run(mh, torch, lib.muyo_gemm_split_f16(*args, None, keep[4].data_ptr(), out.data_ptr(), rows, n, k,
+                                           stream(torch)))
+    assert close(host(out), plain + residual, 1e-5) == 0
+
+
+def test_gemm_split_integer_inputs_are_exact(mh, gpu):
+    """Small integers are exact in f16 and their sums in f32: any index or layout slip shows."""
+    torch = gpu
+    rng = np.random.default_rng(9)
+    rows, n, k = 150, 260, 136
+    a = rng.integers(-8, 9, (rows, k)).astype(np.float32)
+    w = rng.integers(-8, 9, (n, k)).astype(np.float16)
+    ahi, alo = split_np(a)
+    assert not alo.any()
+    out = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    keep = [dev(torch, ahi), dev(torch, alo), dev(torch, w.view(np.uint16))]
+    run(mh, torch, mh.load().muyo_gemm_split_f16(*(t.data_ptr() for t in keep), None, None, out.data_ptr(),
+                                                 rows, n, k, stream(torch)))
+    assert np.array_equal(host(out), a.astype(np.float64) @ w.astype(np.float64).T)
+
+
+@pytest.mark.parametrize("rows,ffn,k", [(1, 8, 8), (45, 100, 72), (200, 4864, 896), (700, 4864, 896)])
+def test_gemm_swiglu_matches_per_token_path(mh, gpu, orc, rows, ffn, k):
+    torch = gpu
+    seed = rows + ffn + k
+    a = orc.normal_f32(rows * k, seed).reshape(rows, k)
+    wg = orc.normal_f16(ffn * k, seed + 1, 0.0, 0.05).reshape(ffn, k)
+    wu = orc.normal_f16(ffn * k, seed + 2, 0.0, 0.05).reshape(ffn, k)
+    ahi, alo = split_np(a)
+    hhi, hlo = planes(torch, (rows, ffn))
+    keep = [dev(torch, ahi), dev(torch, alo), dev(torch, wg), dev(torch, wu)]
+    run(mh, torch, mh.load().muyo_gemm_swiglu_split_f16(*(t.data_ptr() for t in keep), hhi.data_ptr(),
+                                                        hlo.data_ptr(), rows, ffn, k, stream(torch)))
+    want = orc.swiglu(oracle_gemm(orc, wg, a), oracle_gemm(orc, wu, a))
+    got = joined(hhi, hlo)
+    assert close(got, want, 1e-3) == 0
+    assert worst(got, want) < 2e-5
+
+
+def test_gemm_refusals(mh, gpu):
+    lib = mh.load()
+    fake = ctypes.c_void_p(256)
+    assert lib.muyo_gemm_split_f16(None, fake, fake, None, None, fake, 1, 8, 8, 0) == mh.MUYO_E_NULL
+    assert lib.muyo_gemm_split_f16(fake, fake, fake, None, None, fake, 1, 6, 8, 0) == mh.MUYO_E_CONTRACT
+    assert lib.muyo_gemm_split_f16(fake, fake, fake, None, None, fake, 1, 8, 12, 0) == mh.MUYO_E_CONTRACT
+    assert lib.muyo_gemm_split_f16(fake, fake, ctypes.c_void_p(258), None, None, fake, 1, 8, 8, 0) == mh.MUYO_E_CONTRACT
+    assert lib.muyo_gemm_swiglu_split_f16(fake, fake, fake, fake, fake, fake, 0, 8, 8, 0) == mh.MUYO_E_CONTRACT
+
+
+# ------------------------------------------------------------------------------------------------
+# Rope + cache append, attention
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rows,pos0", [(14, 2, 64, 45, 0), (28, 4, 128, 33, 1990),
+                                                                (4, 1, 64, 1, 7)])
+def test_rope_split_append_matches_oracle(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0):
+    torch = gpu
+    max_seq = 2048
+    width = (heads + 2 * kv_heads) * head_dim
+    qkv = orc.normal_f32(rows * width, heads + rows).reshape(rows, width)
+    theta_scale = np.float32(_libm.powf(np.float32(1e6), np.float32(-2.0 / head_dim)))
+    table = dev(torch, rope_pow(theta_scale, head_dim))
+    qhi, qlo = planes(torch, (rows, heads * head_dim))
+    kc = torch.zeros((kv_heads, max_seq, head_dim), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    qkv_d = dev(torch, qkv)
+    run(mh, torch, mh.load().muyo_rope_split_append_f16kv(qkv_d.data_ptr(), rows, pos0, heads, kv_heads,
+                                                          head_dim, max_seq, table.data_ptr(), qhi.data_ptr(),
+                                                          qlo.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                                                          stream(torch)))
+    qdim, kvdim = heads * head_dim, kv_heads * head_dim
+    want_k = np.zeros((kv_heads, max_seq, head_dim), np.uint16)
+    want_v = np.zeros_like(want_k)
+    for m in range(rows):
+        q = orc.rope_neox(qkv[m, :qdim].reshape(heads, head_dim), pos0 + m, float(theta_scale)).reshape(-1)
+        assert close(joined(qhi[m], qlo[m]), q, 1e-3) == 0
+        assert worst(joined(qhi[m], qlo[m]), q) < 1e-6, m
+        k = orc.rope_neox(qkv[m, qdim:qdim + kvdim].reshape(kv_heads, head_dim), pos0 + m, float(theta_scale))
+        want_k[:, pos0 + m] = orc.float_to_half(k)
+        want_v[:, pos0 + m] = orc.float_to_half(qkv[m, qdim + kvdim:].reshape(kv_heads, head_dim))
+    got_k = host(kc).view(np.uint16)
+    # The cache rows outside pos0..pos0+rows stay untouched; inside, k is the f16 of the oracle's
+    # f32 rope (last-bit rounding aside) and v is bit-exact.
+    assert np.array_equal(host(vc).view(np.uint16), want_v)
+    assert not got_k[:, :pos0].any() and not got_k[:, pos0 + rows:].any()
+    want_f = orc.half_to_float(want_k)
+    assert np.all(np.abs(orc.half_to_float(got_k) - want_f) <= np.abs(want_f) * 2.0 ** -10 + 2.0 ** -24)  # 1 ulp
+
+
+def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed):
+    q = orc.normal_f32(rows * heads * head_dim, seed).reshape(rows, heads * head_dim)
+    kc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 1).reshape(kv_heads, max_seq, head_dim)
+    vc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 2).reshape(kv_heads, max_seq, head_dim)
+    qhi, qlo = split_np(q)
+    ohi, olo = planes(torch, (rows, heads * head_dim))
+    scale = 1.0 / math.sqrt(head_dim)
+    keep = [dev(torch, qhi), dev(torch, qlo), dev(torch, kc), dev(torch, vc)]
+    run(mh, torch, mh.load().muyo_prefill_attention_f16kv(*(t.data_ptr() for t in keep),
+                                                          ohi.data_ptr(), olo.data_ptr(), rows, pos0, heads,
+                                                          kv_heads, head_dim, max_seq, scale, stream(torch)))
+    got = joined(ohi, olo)
+    for m in range(rows):
+        want = orc.attention_f16kv(q[m], kc, vc, heads, kv_heads, head_dim, max_seq, pos0 + m, scale)
+        assert close(got[m], want, 1e-3) == 0, m
+        assert worst(got[m], want) < 2e-5, (m, worst(got[m], want))
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rows,pos0,max_seq", [
+    (14, 2, 64, 1, 0, 64),        # one query at row 0: a single key
+    (14, 2, 64, 70, 0, 128),      # three query tiles, ragged
+    (14, 2, 64, 40, 1000, 2048),  # after an earlier prompt
+    (28, 4, 128, 33, 2015, 2048), # 7B heads, ending at the last cache row
+    (8, 1, 128, 64, 5, 100),      # a full group of 8, cache not a multiple of 32 keys
+    (4, 4, 64, 31, 17, 48),       # no grouping
+])
+def test_prefill_attention_matches_per_token_attention(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq):
+    prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, heads + rows + pos0)
+
+
+def test_prefill_attention_refusals(mh, gpu):
+    lib = mh.load()
+    fake = ctypes.c_void_p(256)
+    args = [fake] * 6
+    assert lib.muyo_prefill_attention_f16kv(*args, 4, 0, 14, 2, 96, 64, 0.1, 0) == mh.MUYO_E_UNSUPPORTED
+    assert lib.muyo_prefill_attention_f16kv(*args, 4, 0, 18, 2, 64, 64, 0.1, 0) == mh.MUYO_E_UNSUPPORTED
+    assert lib.muyo_prefill_attention_f16kv(*args, 4, 62, 14, 2, 64, 64, 0.1, 0) == mh.MUYO_E_RANGE
+    assert lib.muyo_prefill_attention_f16kv(*args, 4, -1, 14, 2, 64, 64, 0.1, 0) == mh.MUYO_E_RANGE
+
+
+# ------------------------------------------------------------------------------------------------
+# The decoder's prefill
+
+SMALL = dict(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, max_seq=256)
+
+
+def make_pair(mh, orc, shape, seed, kv_positions=0, kv_seed=7):
+    dec = mh.Decoder(mh.qwen2_config(**shape))
+    dec.fill_random(seed)
+    model = orc.Model(**shape)
+    model.fill_random(seed)
+    if kv_positions:
+        dec.fill_kv_random(kv_positions, kv_seed)
+        model.fill_kv_random(kv_positions, kv_seed)
+    return dec, model
+
+
+def download(dec, kind, layer, like):
+    out = np.empty_like(like)
+    dec.download(kind, layer, out)
+    return out
+
+
+def prompt(orc, count, vocab, seed):
+    return (orc.uniform_f32(count, seed) * 0.5 * vocab + 0.5 * vocab).astype(np.int32)
+
+
+def check_against_oracle(dec, model, orc, shape, tokens, pos0):
+    got = dec.prefill(tokens, pos0)
+    for i, t in enumerate(tokens):
+        want, logits, (top1, top2) = model.step(int(t), pos0 + i)
+    gpu_logits = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+    assert close(gpu_logits, logits, 1e-3) == 0
+    assert got == want, f"prefill {got} oracle {want} (margin {top1 - top2:.3g})"
+    end = pos0 + len(tokens)
+    for layer in range(shape["layers"]):
+        for kind in ("KCACHE", "VCACHE"):
+            ref = model.t[(kind, layer)]
+            cache = download(dec, kind, layer, ref)
+            assert np.array_equal(cache[:, :pos0], ref[:, :pos0])
+            assert np.array_equal(cache[:, end:], ref[:, end:])
+            diff = np.abs(orc.half_to_float(cache[:, pos0:end]) - orc.half_to_float(ref[:, pos0:end]))
+            assert diff.max() <= 2e-3 * (1 + np.abs(orc.half_to_float(ref[:, pos0:end])).max()), (kind, layer)
+    return got
+
+
+def test_decoder_prefill_small_matches_oracle_steps(mh, gpu, orc):
+    dec, model = make_pair(mh, orc, SMALL, seed=41, kv_positions=30, kv_seed=42)
+    with dec:
+        tokens = prompt(orc, 40, SMALL["vocab"], 43)
+        nxt = check_against_oracle(dec, model, orc, SMALL, tokens, 30)
+        # Generation continues from the prefilled cache as after 40 steps.
+        ids = dec.generate(nxt, 70, 12)
+    want, _ = model.greedy(nxt, 70, 12)
+    assert ids == want
+
+
+ODD = {
+    "group8_hd128": dict(layers=1, hidden=512, ffn=1000, heads=8, kv_heads=1, head_dim=128, vocab=500, max_seq=300),
+    "qdim1280_hd64": dict(layers=2, hidden=640, ffn=1792, heads=20, kv_heads=4, head_dim=64, vocab=700, max_seq=333),
+}
+
+
+@pytest.mark.parametrize("name", sorted(ODD))
+def test_decoder_prefill_odd_shapes(mh, gpu, orc, name):
+    shape = ODD[name]
+    dec, model = make_pair(mh, orc, shape, seed=51)
+    with dec:
+        check_against_oracle(dec, model, orc, shape, prompt(orc, shape["max_seq"] - 5, shape["vocab"], 52), 0)
+
+
+def test_decoder_prefill_05b_prompt_then_greedy(mh, gpu, orc, capsys):
+    """Qwen2.5-0.5B shape: a 96-token prompt from row 0, then 16 greedy tokens, against the oracle
+    fed token by token."""
+    orc.set_threads(16)
+    shape = mh.QWEN25_05B
+    dec, model = make_pair(mh, orc, shape, seed=2026)
+    tokens = prompt(orc, 96, shape["vocab"], 2028)
+    with dec:
+        nxt = dec.prefill(tokens, 0)
+        ids = dec.generate(nxt, 96, 16)
+    margins = []
+    for i, t in enumerate(tokens):
+        want, _, (top1, top2) = model.step(int(t), i)
+    margins.append(top1 - top2)
+    rest, more = model.greedy(want, 96, 16)
+    with capsys.disabled():
+        print(f"\n[0.5b prefill 96] next {nxt} ids {ids[:6]}... min margin {min(margins + more):.3g}")
+    assert nxt == want
+    assert ids == rest
+
+
+def test_decoder_prefill_equals_steps_on_gpu(mh, gpu, orc):
+    """Prefill vs the decoder's own steps on the 0.5B shape after a 500-row cache: same logits,
+    same cache rows, same continuation."""
+    shape = mh.QWEN25_05B
+    tokens = prompt(orc, 300, shape["vocab"], 61)
+    with mh.Decoder(mh.qwen2_config(**shape)) as dec:
+        dec.fill_random(60)
+        dec.fill_kv_random(500, 62)
+        nxt = dec.prefill(tokens, 500)
+        logits_p = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+        cache_p = download(dec, "KCACHE", 23, np.empty((2, 2048, 64), np.uint16))
+        ids_p = dec.generate(nxt, 800, 8)
+        dec.fill_kv_random(500, 62)
+        for i, t in enumerate(tokens):
+            stepped = dec.step(int(t), 500 + i)
+        logits_s = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+        cache_s = download(dec, "KCACHE", 23, np.empty((2, 2048, 64), np.uint16))
+        ids_s = dec.generate(stepped, 800, 8)
+    assert close(logits_p, logits_s, 1e-3) == 0
+    assert nxt == stepped
+    assert np.abs(orc.half_to_float(cache_p) - orc.half_to_float(cache_s)).max() <= 2e-3 * (
+        1 + np.abs(orc.half_to_float(cache_s)).max())
+    assert ids_p == ids_s
+
+
+def test_decoder_prefill_in_passes(mh, gpu, orc):
+    """A prompt longer than one pass (2048 rows) runs in two; the second pass attends to the first
+    through the cache."""
+    shape = dict(layers=2, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=1000, max_seq=2300)
+    dec, model = make_pair(mh, orc, shape, seed=71)
+    with dec:
+        check_against_oracle(dec, model, orc, shape, prompt(orc, 2200, shape["vocab"], 72), 50)
+
+
+def test_decoder_prefill_7b_shape_two_layers(mh, gpu, orc):
+    orc.set_threads(16)
+    shape = dict(mh.QWEN25_7B, layers=2)
+    dec, model = make_pair(mh, orc, shape, seed=80, kv_positions=2000, kv_seed=81)
+    with dec:
+        check_against_oracle(dec, model, orc, shape, prompt(orc, 24, shape["vocab"], 82), 2000)
+
+
+def test_decoder_prefill_samples_like_a_step(mh, gpu, orc):
+    """With a sampler set, the prefill draws once from the last position's logits with the prompt
+    as history, as runTurn's sampleNext does after the feed (src/FullModel.cpp:1162-1176)."""
+    params = dict(temperature=0.8, top_k=40, top_p=0.9, repeat_penalty=1.3, repeat_last_n=64, seed=99)
+    tokens = prompt(orc, 50, SMALL["vocab"], 91)
+    with mh.Decoder(mh.qwen2_config(**SMALL)) as dec:
+        dec.fill_random(90)
+        dec.set_sampler(**params)
+        got = dec.prefill(tokens, 0)
+        dec.set_sampler()
+        for i, t in enumerate(tokens[:-1]):
+            dec.step(int(t), i)
+        dec.set_sampler(**params)
+        want = dec.step(int(tokens[-1]), len(tokens) - 1)
+    assert got == want
+
+
+def test_decoder_prefill_refusals(mh, gpu):
+    with mh.Decoder(mh.qwen2_config(**SMALL)) as dec:
+        lib = mh.load()
+        toks = (ctypes.c_int32 * 4)(1, 2, 3, SMALL["vocab"])
+        nxt = ctypes.c_int32()
+        assert lib.muyo_decoder_prefill(dec.handle, toks, 0, 0, ctypes.byref(nxt)) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_prefill(dec.handle, toks, 4, 0, ctypes.byref(nxt)) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_prefill(dec.handle, toks, 3, SMALL["max_seq"] - 2, ctypes.byref(nxt)) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_prefill(dec.handle, toks, 3, -1, ctypes.byref(nxt)) == mh.MUYO_E_RANGE
+        assert lib.muyo_decoder_prefill(dec.handle, None, 3, 0, ctypes.byref(nxt)) == mh.MUYO_E_NULL
