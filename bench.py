@@ -37,6 +37,7 @@ sys.path.insert(0, str(ROOT / "muyo-llm_amd"))
 
 METRIC = "F16 GEMV+norm HBM GB/s (% of MI355X peak); Qwen2.5-0.5B-shape decode tok/s"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core flop/s of MI355X
 # HBM bytes per LM-head launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what the
 # counter reads for a 256 MiB device copy (profiles/lm_head_0.5b_pmc.md), and the L2 hit rate
 # (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)) of the same runs.
@@ -96,6 +97,50 @@ def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
     finally:
         dec.close()
     return ms, list(range(first, first + steps)), launches, ids
+
+
+def prefill_flops(c: dict, prompt: int) -> int:
+    """Algorithmic flops of a prompt fed from row 0, each multiply-add counted once: the layers'
+    projections for every token, causal attention over rows 0..i for token i, and the LM head for
+    the last token only."""
+    hd, qdim = c["head_dim"], c["heads"] * c["head_dim"]
+    qkv_rows = (c["heads"] + 2 * c["kv_heads"]) * hd
+    per_token = 2 * (qkv_rows * c["hidden"] + c["hidden"] * qdim + 3 * c["ffn"] * c["hidden"])
+    attention = 4 * hd * c["heads"] * prompt * (prompt + 1) // 2
+    return c["layers"] * (per_token * prompt + attention) + 2 * c["vocab"] * c["hidden"]
+
+
+def time_prefill(mh, torch, shape, prompt, reps, seed):
+    """Milliseconds per muyo_decoder_prefill of `prompt` tokens at row 0 (a synchronous call:
+    host clock around it, token upload and next-token readback included)."""
+    import time
+
+    tokens = [(7919 * i + 13) % shape["vocab"] for i in range(prompt)]
+    dec = mh.Decoder(mh.qwen2_config(**shape))
+    try:
+        dec.fill_random(seed)
+        first = dec.prefill(tokens, 0)
+        torch.cuda.synchronize()
+        begin = time.perf_counter()
+        for _ in range(reps):
+            again = dec.prefill(tokens, 0)
+        ms = (time.perf_counter() - begin) * 1e3 / reps
+        assert again == first
+    finally:
+        dec.close()
+    return ms, first
+
+
+def prefill_line(mh, torch, shape, prompt, reps, seed, decode_ms):
+    ms, first = time_prefill(mh, torch, shape, prompt, reps, seed)
+    flops = prefill_flops(shape, prompt)
+    return {
+        "prompt_tokens": prompt, "ms": round(ms, 3), "tok_per_s": round(prompt / (ms * 1e-3), 1),
+        "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 1), "flops": flops,
+        "pct_of_f16_mfma_peak": round(100 * flops / (ms * 1e-3) / MFMA_F16_PEAK, 1),
+        "token_by_token_ms": round(prompt * decode_ms, 2) if decode_ms else None,
+        "next_token": first,
+    }
 
 
 def time_kernels(mh, torch, shape, seed, rounds):
@@ -377,6 +422,8 @@ def main() -> int:
     ap.add_argument("--kernel-only", choices=["lm_head", "copy"],
                     help="only launch one kernel back to back (for rocprofv3 traces and counters)")
     ap.add_argument("--launches", type=int, default=20, help="launches for --kernel-only")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the batched-prefill figures (2048-token prompts, 0.5B and 7B shapes)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -396,6 +443,12 @@ def main() -> int:
         return 0
     shape = dict(mh.QWEN25_05B)
     seed = 20261201
+    if args.prefill_only:
+        lines = {"qwen2.5-0.5b-shape-prefill": prefill_line(mh, torch, shape, 2048, 5, seed, None)}
+        if not args.no_7b:
+            lines["qwen2.5-7b-shape-prefill"] = prefill_line(mh, torch, dict(mh.QWEN25_7B), 2048, 3, seed + 7, None)
+        print(json.dumps(lines), flush=True)
+        return 0
 
     ms, positions, launches, ids = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed)
     total_bytes = sum(step_bytes(shape, p) for p in positions)
@@ -415,6 +468,9 @@ def main() -> int:
         "sampler": sampling, "tok_per_s": round(1000.0 / ms_s, 1), "ms_per_step": round(ms_s, 5),
         "sampler_ms_per_token": round(ms_s - ms, 5), "launches_per_step": launches_s,
     }
+    # Batched prefill of a 2048-token prompt, against feeding it one decode step per token (the
+    # reference's feedToken loop) at this run's decode rate.
+    secondary["qwen2.5-0.5b-shape-prefill"] = prefill_line(mh, torch, shape, 2048, 5, seed, ms)
     if not args.no_7b:
         shape7 = dict(mh.QWEN25_7B)
         steps7 = 16
@@ -426,6 +482,7 @@ def main() -> int:
             "tok_per_s": round(1000.0 / ms7, 1), "ms_per_step": round(ms7, 4),
             "positions": f"{pos7[0]}..{pos7[-1]}", "bytes_per_step": bytes7 // steps7,
         }
+        secondary["qwen2.5-7b-shape-prefill"] = prefill_line(mh, torch, shape7, 2048, 3, seed + 7, ms7)
 
     line = {
         "metric": METRIC,
