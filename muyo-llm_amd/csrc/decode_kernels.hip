@@ -6,19 +6,21 @@
 //   per layer:
 //   QkvRopeAppend  : rms_norm prologue -> fused q|k|v GEMV + bias -> NeoX rope of q and k ->
 //                    q to a buffer, k and v appended as fp16 at the position's cache row
-//   Attention      : one workgroup per (256-key chunk, kv head); 64-key tiles of the fp16 cache
-//                    staged in LDS (next tile prefetched), online softmax, P.V for the whole GQA
-//                    group; chunk partials (max, sum, P.V) to scratch
+//   Attention      : one workgroup per (chunk, kv head, query head); blocks of keys dealt to the
+//                    chunks round-robin, so the first K/V rows are requested before the position
+//                    arrives; online softmax in log2 units; chunk partials (max, sum, P.V) to
+//                    scratch (neutral for a chunk without keys)
 //   [AttentionMerge: combine the chunk partials, when o_proj does not do it itself]
 //   OProj          : [merge prologue] o_proj GEMV + residual add
 //   GateUpSwiGlu   : rms_norm prologue -> gate and up GEMV rows -> silu(g)*u
 //   Down           : down GEMV + residual add
 //   LmHeadArgMax   : final rms_norm prologue -> tied LM head -> logits + per-workgroup argmax
 //
-// GEMV core (gemv_core.hpp): the activation is staged once per workgroup in LDS; a wave64
-// splits into segments of LPR lanes, each segment streaming one fp16 weight row in 16-byte
-// chunks with all of a lane's loads in flight at once; the first batch is requested before the
-// activation is staged and the next row's batch before the current row's reduction.
+// GEMV core (gemv_core.hpp): a wave64 splits into segments of LPR lanes, each segment streaming
+// one fp16 weight row in 16-byte chunks with all of a lane's loads in flight at once; the first
+// batch is requested before the activation is staged (in LDS, or per lane straight from memory)
+// and the next row's batch before the current row's reduction. Work that does not depend on the
+// dot products (the rope angle's cosine and sine) runs while the loads are in flight.
 #include <algorithm>
 
 #include "common.hpp"
@@ -42,6 +44,7 @@ constexpr int kMaxGroup = 8;           // query heads per kv head
 #endif
 constexpr int kDirectThreads = MUYO_DIRECT_THREADS;
 constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
+constexpr uint32_t kWideUnits = 2048;  // most units of a short-row GEMV launched a wave per unit
 constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
 constexpr uint32_t kMergeSlots = 512;  // (head, chunk) weights that prologue holds in LDS
 
@@ -71,10 +74,10 @@ struct PlainStage
     static constexpr bool kCanDirect = true;  // see DirectStage
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = true;  // any column range stages on its own
-    template <int kLpr, int kCpl>
-    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
+    template <int kLpr, int kCpl, class Between>
+    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
     {
-        LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, 0.0f, lir, xlo, xhi);
+        LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, 0.0f, lir, xlo, xhi, between);
     }
     template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
@@ -91,10 +94,10 @@ struct NormStage
     static constexpr bool kCanDirect = true;
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = false;  // the norm needs the whole row
-    template <int kLpr, int kCpl>
-    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl]) const
+    template <int kLpr, int kCpl, class Between>
+    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
     {
-        LoadActivationDirect<kLpr, kCpl, true>(x, w, n, eps, lir, xlo, xhi);
+        LoadActivationDirect<kLpr, kCpl, true>(x, w, n, eps, lir, xlo, xhi, between);
     }
     template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
@@ -114,13 +117,12 @@ struct DirectStage : Base
     static constexpr bool kDirect = true;
 };
 
-/// The attention output, merged from the chunk partials: out[h][d] = sum_c e^(m_c - M) acc_c /
-/// sum_c e^(m_c - M) l_c (flash-decoding's combine). Every partial is requested at once, before
-/// the per-head weights are known. (Requesting the grid's slots before the position arrives, as
-/// the standalone merge kernel does, measured slower here.)
+/// The attention output, merged from the chunk partials: out[h][d] = sum_c 2^(m_c - M) acc_c /
+/// sum_c 2^(m_c - M) l_c (flash-decoding's combine, maxima in log2 units). Every slot of the
+/// grid takes part; chunks without keys hold the neutral partial, so no position is needed and
+/// every partial is requested at entry.
 struct MergeStage
 {
-    const int32_t* position;
     const float* attnMax;
     const float* attnSum;
     const float* attnAcc;
@@ -131,7 +133,7 @@ struct MergeStage
 
     __device__ uint64_t Slot(uint32_t h, uint32_t c) const
     {
-        return (static_cast<uint64_t>(h / group) * gridChunks + c) * group + h % group;
+        return (static_cast<uint64_t>(h / group) * gridChunks + min(c, gridChunks - 1)) * group + h % group;
     }
 
     template <int kThreads, int kVec>
@@ -139,9 +141,6 @@ struct MergeStage
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
         __shared__ float weight[kMergeSlots];
-        // Positions outside the cache are rejected on the host; clamping keeps every read in bounds.
-        const uint32_t keys = static_cast<uint32_t>(max(*position, 0)) + 1;
-        const uint32_t chunks = min(AttnChunkCount(keys, headDim, kMergeAttnChunks), gridChunks);
         const uint32_t nchunks = n / 8;
         uint32_t items[kMergeItems];
         float acc[kMergeItems][kMergeAttnChunks];
@@ -153,7 +152,7 @@ struct MergeStage
 #pragma unroll
             for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                acc[k][c] = attnAcc[Slot(h, min(c, chunks - 1)) * headDim + items[k] % headDim];
+                acc[k][c] = attnAcc[Slot(h, c) * headDim + items[k] % headDim];
             }
         }
         if (threadIdx.x < heads)
@@ -164,27 +163,27 @@ struct MergeStage
 #pragma unroll
             for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                m[c] = attnMax[Slot(h, min(c, chunks - 1))];
-                l[c] = attnSum[Slot(h, min(c, chunks - 1))];
+                m[c] = c < gridChunks ? attnMax[Slot(h, c)] : -INFINITY;
+                l[c] = attnSum[Slot(h, c)];
             }
             float top = -INFINITY;
 #pragma unroll
             for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                top = c < chunks ? fmaxf(top, m[c]) : top;
+                top = fmaxf(top, m[c]);
             }
             float den = 0.0f;
 #pragma unroll
             for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                m[c] = c < chunks ? expf(m[c] - top) : 0.0f;
+                m[c] = top == -INFINITY ? 0.0f : exp2f(m[c] - top);  // 0 for neutral and absent slots
                 den = fmaf(m[c], l[c], den);
             }
-            const float inv = 1.0f / den;
+            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
 #pragma unroll
             for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
             {
-                weight[h * kMergeAttnChunks + c] = m[c] * inv;  // 0 past the last chunk
+                weight[h * kMergeAttnChunks + c] = m[c] * inv;
             }
         }
         __syncthreads();
@@ -274,12 +273,14 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
         }
         float4 xlo[kCpl];
         float4 xhi[kCpl];
+        // The epilogue's own work (Ready) runs while the weights and the activation are in flight.
         if constexpr (Stage::kDirect)
         {
-            stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi);
+            stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] { epi.Ready(pre); });
         }
         else
         {
+            epi.Ready(pre);
             stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols);
             LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
         }
@@ -299,6 +300,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
             {
                 next = epi.Prefetch(unit + stride);
                 load(unit + stride);
+                epi.Ready(next);
             }
             // Every lane of the segment ends with the unit's row sums.
 #pragma unroll
@@ -321,6 +323,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
         {
             pre = epi.Prefetch(first + unitInWave);
             LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
+            epi.Ready(pre);
         }
         stage.template Run<kBlock, kStageVec>(xs, cols);
         const float4* lo = xs;
@@ -340,6 +343,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
             {
                 nextPre = epi.Prefetch(next);
                 LoadBatch<kLpr, kCpl>(epi.Row(next, part), 0, nchunks, lir, w);
+                epi.Ready(nextPre);
             }
             // Every lane of a segment holds its row's sum; the unit's second row sits in the
             // partner segment.
@@ -397,6 +401,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
     {
         pa = epi.Prefetch(unit);
         LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
+        epi.Ready(pa);
     }
     stage.template Run<kBlock, kStageVec>(xs, cols);
     const float4* lo = xs;
@@ -408,6 +413,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         {
             pb = epi.Prefetch(ub);
             LoadBatch<kBlock, kCpl>(epi.Row(ub, 0), 0, nchunks, lir, wb);
+            epi.Ready(pb);
         }
         finish(unit, DotBatch<kBlock, kCpl>(wa, 0, nchunks, lir, lo, hi, 0.0f), pa);
         if (ub >= units)
@@ -419,6 +425,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         {
             pa = epi.Prefetch(uc);
             LoadBatch<kBlock, kCpl>(epi.Row(uc, 0), 0, nchunks, lir, wa);
+            epi.Ready(pa);
         }
         finish(ub, DotBatch<kBlock, kCpl>(wb, 0, nchunks, lir, lo, hi, 0.0f), pb);
     }
@@ -533,6 +540,9 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stag
         {
             sums[r] = (partial[k][r][0] + partial[k][r][1]) + (partial[k][r][2] + partial[k][r][3]);
         }
+        // Here the epilogue's own work (Ready) is left to the end: wave 0 reaching the norm's
+        // barrier late held all four waves back (7B-shape QKV 8.3 -> 8.9 us).
+        epi.Ready(pre);
         epi.Finish(u0 + k, sums, pre, bestValue, bestIndex);
     }
     epi.template Tail<kBlock>(bestValue, bestIndex);
@@ -579,6 +589,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
     if (count > 0)
     {
         load(0, wa);
+    }
+    if (threadIdx.x < count)
+    {
+        epi.Ready(pre);
     }
     float4 xlo[kCpl];
     float4 xhi[kCpl];
@@ -658,11 +672,25 @@ struct QkvEpi
     {
         float bias0, bias1, pow;
         int32_t pos;
+        float cos, sin;
     };
 
     __device__ Pre Prefetch(uint32_t unit) const
     {
-        return Pre{bias[RowOf(unit, 0)], bias[RowOf(unit, 1)], ropePow[unit % (headDim / 2)], state->position};
+        return Pre{bias[RowOf(unit, 0)], bias[RowOf(unit, 1)], ropePow[unit % (headDim / 2)], state->position,
+                   0.0f, 0.0f};
+    }
+
+    /// Called once the unit's weights are requested: the rope angle's cosine and sine are worked
+    /// out while those loads are in flight instead of after the dot products. The empty asm keeps
+    /// the compiler from sinking them into the epilogue.
+    __device__ void Ready(Pre& pre) const
+    {
+        // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
+        const float theta = static_cast<float>(pre.pos) * pre.pow;
+        pre.cos = cosf(theta);
+        pre.sin = sinf(theta);
+        asm volatile("" : "+v"(pre.cos), "+v"(pre.sin));
     }
 
     __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
@@ -674,12 +702,10 @@ struct QkvEpi
         const float s1 = s[1] + pre.bias1;
         if (unit < ropeUnits)
         {
-            // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
             const uint32_t head = unit / half;
             const uint32_t j = unit % half;
-            const float theta = static_cast<float>(pos) * pre.pow;
-            const float c = cosf(theta);
-            const float sn = sinf(theta);
+            const float c = pre.cos;
+            const float sn = pre.sin;
             const float o0 = s0 * c - s1 * sn;
             const float o1 = s0 * sn + s1 * c;
             if (head < heads)
@@ -724,6 +750,7 @@ struct ResidualEpi
         float residual;
     };
     __device__ Pre Prefetch(uint32_t unit) const { return Pre{residual[unit]}; }
+    __device__ void Ready(Pre&) const {}
     __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
     {
         out[unit] = pre.residual + s[0];
@@ -750,6 +777,7 @@ struct GateUpEpi
     {
     };
     __device__ Pre Prefetch(uint32_t) const { return Pre{}; }
+    __device__ void Ready(Pre&) const {}
     __device__ void Finish(uint32_t unit, const float* s, const Pre&, float&, int32_t&) const
     {
         act[unit] = s[0] / (1.0f + expf(-s[0])) * s[1];  // swiglu.comp's op
@@ -811,6 +839,7 @@ struct LmHeadEpi
     {
     };
     __device__ Pre Prefetch(uint32_t) const { return Pre{}; }
+    __device__ void Ready(Pre&) const {}
     __device__ void Finish(uint32_t unit, const float* s, const Pre&, float& bestValue, int32_t& bestIndex) const
     {
         logits[unit] = s[0];
@@ -996,6 +1025,13 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     }
     const uint32_t nchunks = cols / 8;
     const size_t lds = static_cast<size_t>(cols) * sizeof(float);
+    // Short rows in a latency-bound launch (a few thousand units at most): a whole wave per unit,
+    // two chunks per lane, so each lane's serial work (norm, dot, reduction) is a quarter of the
+    // exact-fit 16 x 7 shape's. 0.5B-shape QKV: 3.62 -> 3.37 us.
+    if (nchunks > 64 && nchunks <= 128 && units <= kWideUnits)
+    {
+        return LaunchFusedT<64, 2, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+    }
     const RowShape shape = PickFusedShape(nchunks, kNr);
 #define MUYO_FUSED_CASE(L, C)                                                                                    \
     if (shape.lpr == L && shape.cpl == C)                                                                        \
@@ -1174,73 +1210,100 @@ __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, con
 }
 
 // ------------------------------------------------------------------------------------------------
-// Attention over the fp16 cache: one workgroup per (chunk of keys, kv head, query head of its
-// GQA group).
+// Attention over the fp16 cache: one workgroup per (chunk, kv head, query head of its GQA group).
 //
-// The 256 lanes form kSlices groups of kRC = headDim/8 lanes; a group owns one key at a time and
-// each of its lanes one 16-byte slice of that key's K and V rows, which stay in registers (the
-// next keys' rows are requested before the current ones are used). A group keeps its own online
-// softmax (max, sum, 8 channels of P.V per lane); at the end the groups are combined through LDS
-// and the chunk's partials written for the merge. The query heads of a group read the same K/V
-// chunk (from L2 after the first), which buys parallelism: the work per lane is one head's.
+// Keys are dealt to the chunks in blocks of kSlices consecutive keys, block b to chunk b % G (G
+// is the grid's chunk count). A chunk's first blocks are therefore known before the position is:
+// the first round of K/V rows is requested at entry, together with q, and the position, which
+// arrives meanwhile, only masks it. Dealt this way the keys also spread evenly over the chunks at
+// every position. The 256 lanes form kSlices groups of kRC = headDim/8 lanes; a group owns one
+// key of each block and each of its lanes one 16-byte slice of that key's K and V rows. Scores
+// are kept in log2 units (q.k * scale * log2 e), so each softmax weight is a single exp2. At the
+// end the slices are combined inside each wave by lane permutes and across the four waves through
+// LDS, and the chunk's partial (max, sum, P.V) goes to the merge; a chunk without keys writes the
+// neutral partial (-inf, 0, 0), so the merge needs no position either.
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kAttnBlocksPerRound = 8;  // key blocks per lane per round: 2048 keys of a 2048-row cache in one round
+
+/// Sum (kMax false) or maximum over the slices of one wave: the lanes equal modulo kRC. Every
+/// lane ends with the same bit pattern as the others of its class (each step combines the same
+/// two values).
+template <int kRC, bool kMax>
+__device__ __forceinline__ float SliceReduce(float v)
+{
+    static_assert(kRC == 8 || kRC == 16, "slice width");
+    auto op = [](float a, float b) { return kMax ? fmaxf(a, b) : a + b; };
+    if constexpr (kRC == 8)
+    {
+        // row_ror:8 pairs lane i with lane i ^ 8 inside each 16-lane row.
+        v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), 0x128, 0xF, 0xF,
+                                                             false)));
+    }
+    // Rows 2r and 2r+1, then the two halves of the wave.
+    const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = op(__uint_as_float(rows[0]), __uint_as_float(rows[1]));
+    const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return op(__uint_as_float(halves[0]), __uint_as_float(halves[1]));
+}
 
 template <int kHd>
 __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                          const uint16_t* __restrict__ vc,
                                                          const int32_t* __restrict__ position, uint32_t group,
-                                                         uint32_t maxSeq, uint32_t maxChunks, float scale,
-                                                         DecodeScratch sc)
+                                                         uint32_t maxSeq, float scale, DecodeScratch sc)
 {
     constexpr int kRC = kHd / 8;           // lanes per key
-    constexpr int kSlices = kBlock / kRC;  // keys side by side
-    constexpr int kKpt = 2;                // keys per lane per round
-    constexpr int kPad = kHd + 4;          // LDS row stride: slices of one lane position differ in bank
+    constexpr int kSlices = kBlock / kRC;  // keys of a block, side by side
+    constexpr int kR = kAttnBlocksPerRound;
     static_assert(kSlices == 2048 / kHd, "slice count must match AttnSlices");
-    __shared__ float combine[kSlices * kPad];
-    __shared__ float sliceMax[kSlices];
-    __shared__ float sliceSum[kSlices];
-    __shared__ float headMax;
-    __shared__ float headSum;
+    __shared__ float waveMax[kWaves];
+    __shared__ float waveSum[kWaves];
+    __shared__ float combine[kWaves][kHd];
 
-    const int32_t pos = *position;
-    if (pos < 0 || static_cast<uint32_t>(pos) >= maxSeq)
-    {
-        return;
-    }
-    const uint32_t keys = static_cast<uint32_t>(pos) + 1;
-    const uint32_t chunkKeys = AttnChunkKeys(keys, kHd, maxChunks);
     const uint32_t chunk = blockIdx.x;
-    if (chunk * chunkKeys >= keys)
-    {
-        return;
-    }
+    const uint32_t chunks = gridDim.x;
     const uint32_t g = blockIdx.y;
     const uint32_t h = blockIdx.z;
-    const uint32_t c0 = chunk * chunkKeys;
-    const uint32_t cn = min(chunkKeys, keys - c0);
+    const uint32_t wave = threadIdx.x / kWave;
     const uint32_t slice = threadIdx.x / kRC;
     const uint32_t part = threadIdx.x % kRC;
-    const uint32_t rounds = (cn + kSlices * kKpt - 1) / (kSlices * kKpt);
     const half8* kBase = reinterpret_cast<const half8*>(kc + static_cast<uint64_t>(g) * maxSeq * kHd) + part;
     const half8* vBase = reinterpret_cast<const half8*>(vc + static_cast<uint64_t>(g) * maxSeq * kHd) + part;
+    auto keyOf = [&](uint32_t block) { return (block * chunks + chunk) * kSlices + slice; };
 
-    // Keys of round r: (r * kKpt + k) * kSlices + slice; keys past the chunk read its last key
-    // (always in bounds) and are masked out of the softmax.
-    auto load = [&](uint32_t r, half8(&kk)[kKpt], half8(&vv)[kKpt]) {
+    // Round 0 before the position: this chunk's first kR blocks, clamped into the cache.
+    half8 kk[kR], vv[kR];
 #pragma unroll
-        for (int k = 0; k < kKpt; ++k)
-        {
-            const uint32_t key = c0 + min((r * kKpt + k) * kSlices + slice, cn - 1);
-            kk[k] = kBase[static_cast<uint64_t>(key) * kRC];
-            vv[k] = vBase[static_cast<uint64_t>(key) * kRC];
-        }
-    };
-    half8 ka[kKpt], va[kKpt], kb[kKpt], vb[kKpt];
-    load(0, ka, va);
+    for (int k = 0; k < kR; ++k)
+    {
+        const uint32_t key = min(keyOf(k), maxSeq - 1);
+        kk[k] = kBase[static_cast<uint64_t>(key) * kRC];
+        vv[k] = vBase[static_cast<uint64_t>(key) * kRC];
+    }
     const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + h) * kHd) + part * 2;
     const float4 q0 = qh[0];
     const float4 q1 = qh[1];
-
+    const int32_t pos = *position;
+    // Positions outside the cache are refused on the host; here they leave every chunk neutral.
+    const uint32_t keys = pos >= 0 && static_cast<uint32_t>(pos) < maxSeq ? static_cast<uint32_t>(pos) + 1 : 0;
+    const uint32_t blocks = (keys + kSlices - 1) / kSlices;
+    const uint32_t mine = chunk < blocks ? (blocks - chunk + chunks - 1) / chunks : 0;  // this chunk's blocks
+    const uint64_t slot = (static_cast<uint64_t>(g) * chunks + chunk) * group + h;
+    if (mine == 0)
+    {
+        for (uint32_t d = threadIdx.x; d < kHd; d += kBlock)
+        {
+            sc.attnAcc[slot * kHd + d] = 0.0f;
+        }
+        if (threadIdx.x == 0)
+        {
+            sc.attnMax[slot] = -INFINITY;
+            sc.attnSum[slot] = 0.0f;
+        }
+        return;
+    }
+    const float sl = scale * kLog2e;
     float m = -INFINITY;
     float l = 0.0f;
     float acc[8];
@@ -1249,28 +1312,37 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     {
         acc[c] = 0.0f;
     }
-    auto consume = [&](uint32_t r, const half8(&kk)[kKpt], const half8(&vv)[kKpt]) {
-        float s[kKpt];
+    // Online softmax over one round of blocks b0 .. b0 + kR - 1. Keys past the position and
+    // blocks past this chunk's are masked; their rows may hold anything, so their V is selected
+    // out rather than weighted by 0.
+    auto consume = [&](uint32_t b0) {
+        float s[kR];
+        bool valid[kR];
         float top = m;
 #pragma unroll
-        for (int k = 0; k < kKpt; ++k)
+        for (int k = 0; k < kR; ++k)
         {
-            s[k] = GroupSum<kRC>(DotChunk(kk[k], q0, q1, 0.0f)) * scale;
-            s[k] = (r * kKpt + k) * kSlices + slice < cn ? s[k] : -INFINITY;
+            valid[k] = b0 + k < mine && keyOf(b0 + k) < keys;
+            s[k] = -INFINITY;
+            if (b0 + k < mine)  // uniform over the workgroup
+            {
+                const float d = GroupSum<kRC>(DotChunk(kk[k], q0, q1, 0.0f)) * sl;
+                s[k] = valid[k] ? d : -INFINITY;
+            }
             top = fmaxf(top, s[k]);
         }
         if (top == -INFINITY)
         {
-            return;  // no valid key for this group yet
+            return;  // no valid key for this slice in this round
         }
-        const float factor = expf(m - top);  // 0 while m is still -inf
+        const float factor = exp2f(m - top);  // 0 while m is still -inf
         m = top;
-        float p[kKpt];
+        float p[kR];
         float psum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < kKpt; ++k)
+        for (int k = 0; k < kR; ++k)
         {
-            p[k] = expf(s[k] - top);
+            p[k] = valid[k] ? exp2f(s[k] - top) : 0.0f;
             psum += p[k];
         }
         l = fmaf(l, factor, psum);
@@ -1279,122 +1351,133 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         {
             float a = acc[c] * factor;
 #pragma unroll
-            for (int k = 0; k < kKpt; ++k)
+            for (int k = 0; k < kR; ++k)
             {
-                a = fmaf(p[k], static_cast<float>(vv[k][c]), a);
+                a = valid[k] ? fmaf(p[k], static_cast<float>(vv[k][c]), a) : a;
             }
             acc[c] = a;
         }
     };
-
-    for (uint32_t r = 0; r < rounds; r += 2)
+    consume(0);
+    // Caches longer than one round's reach (kR * chunks * kSlices keys): further rounds, their
+    // rows clamped to the last key.
+    for (uint32_t b0 = kR; b0 < mine; b0 += kR)
     {
-        if (r + 1 < rounds)
+#pragma unroll
+        for (int k = 0; k < kR; ++k)
         {
-            load(r + 1, kb, vb);
+            const uint32_t key = min(keyOf(b0 + k), keys - 1);
+            kk[k] = kBase[static_cast<uint64_t>(key) * kRC];
+            vv[k] = vBase[static_cast<uint64_t>(key) * kRC];
         }
-        consume(r, ka, va);
-        if (r + 1 >= rounds)
-        {
-            break;
-        }
-        if (r + 2 < rounds)
-        {
-            load(r + 2, ka, va);
-        }
-        consume(r + 1, kb, vb);
+        consume(b0);
     }
 
-    // Combine the slices: the chunk's max and sum (wave 0), then the rescaled P.V summed over
-    // slices.
-    if (part == 0)
+    // Combine the slices: the chunk's max (slices of a wave by permutes, then the waves), then
+    // the rescaled sums the same way.
+    const float mw = SliceReduce<kRC, true>(m);
+    if ((threadIdx.x & (kWave - 1)) == 0)
     {
-        sliceMax[slice] = m;
-        sliceSum[slice] = l;
+        waveMax[wave] = mw;
     }
     __syncthreads();
-    if (threadIdx.x < kWave)
+    float top = waveMax[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
     {
-        const int lane = threadIdx.x;
-        const float mi = lane < kSlices ? sliceMax[lane] : -INFINITY;
-        const float top = GroupMax<kSlices>(mi);
-        const float li = (lane < kSlices && mi != -INFINITY) ? sliceSum[lane] * expf(mi - top) : 0.0f;
-        const float sum = GroupSum<kSlices>(li);
-        if (lane == 0)
+        top = fmaxf(top, waveMax[w]);
+    }
+    const float f = m == -INFINITY ? 0.0f : exp2f(m - top);
+    const float lw = SliceReduce<kRC, false>(l * f);
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+    {
+        acc[c] = SliceReduce<kRC, false>(acc[c] * f);
+    }
+    if ((threadIdx.x & (kWave - 1)) < kRC)
+    {
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
         {
-            headMax = top;
-            headSum = sum;
+            combine[wave][part * 8 + c] = acc[c];
+        }
+        if (part == 0)
+        {
+            waveSum[wave] = lw;
         }
     }
     __syncthreads();
-    const float f = m == -INFINITY ? 0.0f : expf(m - headMax);
-    float4* dst = reinterpret_cast<float4*>(combine + slice * kPad + part * 8);
-    dst[0] = make_float4(acc[0] * f, acc[1] * f, acc[2] * f, acc[3] * f);
-    dst[1] = make_float4(acc[4] * f, acc[5] * f, acc[6] * f, acc[7] * f);
-    __syncthreads();
-    const uint64_t slot = (static_cast<uint64_t>(g) * gridDim.x + chunk) * group + h;
     for (uint32_t d = threadIdx.x; d < kHd; d += kBlock)
     {
-        float sum = 0.0f;
-#pragma unroll 8
-        for (int i = 0; i < kSlices; ++i)
+        float sum = combine[0][d];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w)
         {
-            sum += combine[i * kPad + d];
+            sum += combine[w][d];
         }
         sc.attnAcc[slot * kHd + d] = sum;
     }
     if (threadIdx.x == 0)
     {
-        sc.attnMax[slot] = headMax;
-        sc.attnSum[slot] = headSum;
+        float sum = waveSum[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w)
+        {
+            sum += waveSum[w];
+        }
+        sc.attnMax[slot] = top;
+        sc.attnSum[slot] = sum;
     }
 }
 
+/// Combine the chunk partials of one query head (max in log2 units): every slot of the grid, the
+/// neutral ones weighing 0. No valid chunk at all (a refused position) gives 0.
+__device__ __forceinline__ float MergeChunks(const float* m, const float* l, const float* a, uint32_t n, float* den)
+{
+    float top = -INFINITY;
+    for (uint32_t c = 0; c < n; ++c)
+    {
+        top = fmaxf(top, m[c]);
+    }
+    float num = 0.0f;
+    float sum = 0.0f;
+    if (top != -INFINITY)
+    {
+        for (uint32_t c = 0; c < n; ++c)
+        {
+            const float e = exp2f(m[c] - top);
+            num = fmaf(e, a[c], num);
+            sum = fmaf(e, l[c], sum);
+        }
+    }
+    *den = sum;
+    return num;
+}
+
 /// Combine the chunk partials of every query head: one workgroup per head, a thread per channel.
-__global__ __launch_bounds__(128) void AttentionMergeKernel(const int32_t* __restrict__ position, DecodeScratch sc,
-                                                            float* __restrict__ out, uint32_t group, uint32_t headDim,
-                                                            uint32_t policyChunks, uint32_t maxChunks)
+__global__ __launch_bounds__(128) void AttentionMergeKernel(DecodeScratch sc, float* __restrict__ out, uint32_t group,
+                                                            uint32_t headDim, uint32_t gridChunks)
 {
     const uint32_t h = blockIdx.x;
     const uint32_t g = h / group;
     const uint32_t hh = h % group;
-    const uint32_t keys = static_cast<uint32_t>(max(*position, 0)) + 1;
-    const uint32_t chunks = min(AttnChunkCount(keys, headDim, policyChunks), maxChunks);
-    float m[kMaxAttnChunks];
-    float l[kMaxAttnChunks];
-    float a[kMaxAttnChunks];
     for (uint32_t d = threadIdx.x; d < headDim; d += blockDim.x)
     {
-        // Every slot of the grid is requested with the position, not after it: slots past the
-        // step's last chunk hold earlier values and are dropped by selection below.
+        float m[kMaxAttnChunks];
+        float l[kMaxAttnChunks];
+        float a[kMaxAttnChunks];
 #pragma unroll
         for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
         {
-            const uint32_t cc = min(c, maxChunks - 1);
-            const uint64_t slot = (static_cast<uint64_t>(g) * maxChunks + cc) * group + hh;
-            m[c] = sc.attnMax[slot];
+            const uint32_t cc = min(c, gridChunks - 1);
+            const uint64_t slot = (static_cast<uint64_t>(g) * gridChunks + cc) * group + hh;
+            m[c] = c < gridChunks ? sc.attnMax[slot] : -INFINITY;
             l[c] = sc.attnSum[slot];
             a[c] = sc.attnAcc[slot * headDim + d];
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
-        {
-            mx = c < chunks ? fmaxf(mx, m[c]) : mx;
-        }
-        float num = 0.0f;
         float den = 0.0f;
-#pragma unroll
-        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
-        {
-            if (c < chunks)
-            {
-                const float e = expf(m[c] - mx);
-                num = fmaf(e, a[c], num);
-                den = fmaf(e, l[c], den);
-            }
-        }
-        out[static_cast<uint64_t>(h) * headDim + d] = num / den;
+        const float num = MergeChunks(m, l, a, kMaxAttnChunks, &den);
+        out[static_cast<uint64_t>(h) * headDim + d] = den > 0.0f ? num / den : 0.0f;
     }
 }
 
@@ -1511,7 +1594,7 @@ hipError_t LaunchAttentionT(hipStream_t s, const DecodeDims& dims, const float* 
     const uint32_t group = dims.heads / dims.kvHeads;
     const dim3 grid(AttnGridChunks(dims.maxSeq, kHd, dims.attnChunks), dims.kvHeads, group);
     hipLaunchKernelGGL(AttentionChunk<kHd>, grid, dim3(kBlock), 0, s, q, kcache, vcache, position, group, dims.maxSeq,
-                       dims.attnChunks, dims.attnScale, scratch);
+                       dims.attnScale, scratch);
     return hipGetLastError();
 }
 
@@ -1534,21 +1617,20 @@ hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q
     }
 }
 
-hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const int32_t* position,
-                                const DecodeScratch& scratch, float* out)
+hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const DecodeScratch& scratch, float* out)
 {
     hipLaunchKernelGGL(AttentionMergeKernel, dim3(dims.heads), dim3(std::min<uint32_t>(dims.headDim, 128)), 0, s,
-                       position, scratch, out, dims.heads / dims.kvHeads, dims.headDim, dims.attnChunks,
+                       scratch, out, dims.heads / dims.kvHeads, dims.headDim,
                        AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks));
     return hipGetLastError();
 }
 
-hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const int32_t* position,
-                             const DecodeScratch& scratch, const float* residual, float* out)
+hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                             const float* residual, float* out)
 {
     const uint32_t qdim = dims.heads * dims.headDim;
-    MergeStage stage{position,   scratch.attnMax,           scratch.attnSum, scratch.attnAcc,
-                     dims.heads, dims.heads / dims.kvHeads, dims.headDim,    AttnGridChunks(dims.maxSeq, dims.headDim, kMergeAttnChunks)};
+    MergeStage stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads, dims.heads / dims.kvHeads,
+                     dims.headDim,    AttnGridChunks(dims.maxSeq, dims.headDim, kMergeAttnChunks)};
     ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
     return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
 }
@@ -1669,7 +1751,7 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
                                           static_cast<const uint16_t*>(vcache), position, g_attentionScratch.scratch);
     if (launched == hipSuccess)
     {
-        launched = LaunchAttentionMerge(AsStream(stream), dims, position, g_attentionScratch.scratch, out);
+        launched = LaunchAttentionMerge(AsStream(stream), dims, g_attentionScratch.scratch, out);
     }
     return launched == hipSuccess ? MUYO_OK : HipStatus(launched, name);
 }

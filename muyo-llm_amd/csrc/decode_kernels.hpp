@@ -43,7 +43,7 @@ struct DecodeState
 /// Scratch shared by the kernels of one decoder (sized for its model).
 struct DecodeScratch
 {
-    float* attnMax;     // [kvHeads][gridChunks][group]        chunk-local softmax max
+    float* attnMax;     // [kvHeads][gridChunks][group]        chunk-local softmax max (log2 units)
     float* attnSum;     // [kvHeads][gridChunks][group]        chunk-local softmax sum
     float* attnAcc;     // [kvHeads][gridChunks][group][hd]    chunk-local P.V (relative to the max)
     float* argValue;    // [kArgMaxBlocks]                 per-workgroup LM-head max
@@ -62,24 +62,8 @@ constexpr uint32_t kMaxSeq = 32768;
 /// a cache row each (headDim 64 -> 32 keys, 128 -> 16 keys).
 __host__ __device__ inline uint32_t AttnSlices(uint32_t headDim) { return 2048u / headDim; }
 
-/// Keys per attention chunk for a cache of `keys` rows: a multiple of the slices, large enough
-/// that at most maxChunks chunks cover the rows.
-__host__ __device__ inline uint32_t AttnChunkKeys(uint32_t keys, uint32_t headDim, uint32_t maxChunks)
-{
-    const uint32_t slices = AttnSlices(headDim);
-    const uint32_t per = (keys + maxChunks - 1) / maxChunks;
-    const uint32_t rounded = (per + slices - 1) / slices * slices;
-    return rounded > slices ? rounded : slices;
-}
-
-__host__ __device__ inline uint32_t AttnChunkCount(uint32_t keys, uint32_t headDim, uint32_t maxChunks)
-{
-    const uint32_t chunkKeys = AttnChunkKeys(keys, headDim, maxChunks);
-    return (keys + chunkKeys - 1) / chunkKeys;
-}
-
-/// Chunk slots per kv head (the attention grid's x): the most chunks any position up to maxSeq
-/// needs, min(maxChunks, ceil(maxSeq / slices)).
+/// Chunks per kv head (the attention grid's x): min(maxChunks, ceil(maxSeq / slices)). Blocks of
+/// `slices` consecutive keys are dealt to the chunks round-robin.
 inline uint32_t AttnGridChunks(uint32_t maxSeq, uint32_t headDim, uint32_t maxChunks)
 {
     const uint32_t bySlices = (maxSeq + AttnSlices(headDim) - 1) / AttnSlices(headDim);
@@ -114,11 +98,10 @@ hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const floa
 hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
                            const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch);
 
-hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const int32_t* position,
-                                const DecodeScratch& scratch, float* out);
+hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const DecodeScratch& scratch, float* out);
 
-hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const int32_t* position,
-                             const DecodeScratch& scratch, const float* residual, float* out);
+hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                             const float* residual, float* out);
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols);

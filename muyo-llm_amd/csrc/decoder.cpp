@@ -241,7 +241,7 @@ hipError_t EnqueueAttention(MuyoDecoder* d, hipStream_t s, uint32_t l)
                                         d->At<uint16_t>(d->Layer(l, kVCache)), &d->state->position, d->scratch);
     if (status == hipSuccess && !d->mergeInOProj)
     {
-        status = LaunchAttentionMerge(s, d->dims, &d->state->position, d->scratch, d->attnOut);
+        status = LaunchAttentionMerge(s, d->dims, d->scratch, d->attnOut);
     }
     return status;
 }
@@ -251,7 +251,7 @@ hipError_t EnqueueOProj(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* 
     const uint16_t* wo = d->At<uint16_t>(d->Layer(l, kOut));
     if (d->mergeInOProj)
     {
-        return LaunchOProjMerged(s, d->dims, wo, &d->state->position, d->scratch, residual, out);
+        return LaunchOProjMerged(s, d->dims, wo, d->scratch, residual, out);
     }
     return LaunchMatVecResidual(s, wo, d->attnOut, residual, out, d->config.hidden, d->config.heads * d->config.headDim);
 }

@@ -91,10 +91,17 @@ __device__ __forceinline__ void LoadActivation(const float4* __restrict__ lo, co
 /// no workgroup barrier. With kNorm the chunks are scaled in place by rsqrt(mean(x^2) + eps) * w
 /// in rms_norm.comp:122's order (scale * x) * w; the sum of squares is the segment's, which
 /// holds every element of the row once.
-template <int kLpr, int kCpl, bool kNorm>
+struct NoOp
+{
+    __device__ void operator()() const {}
+};
+
+/// `between` runs once the loads are issued and before the norm waits for them (work that
+/// overlaps their latency).
+template <int kLpr, int kCpl, bool kNorm, class Between = NoOp>
 __device__ __forceinline__ void LoadActivationDirect(const float* __restrict__ x, const float* __restrict__ w,
                                                      uint32_t n, float eps, uint32_t lir, float4 (&xlo)[kCpl],
-                                                     float4 (&xhi)[kCpl])
+                                                     float4 (&xhi)[kCpl], Between between = Between{})
 {
     const uint32_t nchunks = n / 8;
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -113,6 +120,7 @@ __device__ __forceinline__ void LoadActivationDirect(const float* __restrict__ x
             ghi[i] = w4[2 * c + 1];
         }
     }
+    between();
     if constexpr (kNorm)
     {
         float ss = 0.0f;

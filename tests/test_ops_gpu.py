@@ -513,10 +513,11 @@ def test_cpy_kv_cache_fill_and_shader_index_math(mh, gpu):
 # fp16 KV cache: rope + append, attention
 
 
-# Positions cover one key, chunk-size steps of the adaptive chunking (32/64 keys per chunk for
-# head_dim 64 around rows 1024..1025), several rounds per lane (long caches) and the last row.
-ATTN_CASES = [("0.5b", 2048, (0, 1, 31, 32, 63, 64, 255, 256, 257, 1000, 1023, 1024, 1025, 2047)),
-              ("7b", 2048, (0, 15, 16, 17, 511, 512, 513, 2040, 2047)),
+# Keys go to the 16 chunks in blocks of 32 (head_dim 64) or 16 (head_dim 128) consecutive rows,
+# round-robin. Positions cover one key, block edges, the edges of a full lap of the chunks (512 or
+# 256 rows), several rounds per lane (caches past one round's 4096 or 2048 rows) and the last row.
+ATTN_CASES = [("0.5b", 2048, (0, 1, 31, 32, 63, 64, 255, 256, 257, 511, 512, 513, 1000, 1023, 1024, 1025, 2047)),
+              ("7b", 2048, (0, 15, 16, 17, 255, 256, 257, 511, 512, 513, 2040, 2047)),
               ("0.5b", 8192, (4095, 8191)),
               ("7b", 8192, (5000, 8191))]
 
@@ -555,6 +556,37 @@ def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape, max_seq, positions
         expect = orc.attention_f16kv(host(qr), kbits, vbits, heads, kv, hd, max_seq, pos, scale)
         assert close(host(out), expect, 1e-3) == 0, f"pos {pos}"
         assert worst(host(out), expect) < 1e-5
+
+
+@pytest.mark.parametrize("shape", ["0.5b", "7b"])
+def test_attention_ignores_rows_past_the_position(mh, gpu, orc, shape):
+    """The first round of K/V rows is requested before the position is read, so it covers rows past
+    the position too; those rows (here NaN and infinity) must not reach the output."""
+    torch = gpu
+    heads, kv, hd = (14, 2, 64) if shape == "0.5b" else (28, 4, 128)
+    max_seq = 2048
+    scale = 1.0 / math.sqrt(hd)
+    lib = mh.load()
+    for pos in (0, 5, 40, 700, 2046):
+        kc = torch.empty(kv * max_seq * hd, dtype=torch.float16, device="cuda")
+        vc = torch.empty_like(kc)
+        mh.check(lib.muyo_fill_normal_f16(kc.data_ptr(), kc.numel(), 41, 0.0, 1.0, stream(torch)))
+        mh.check(lib.muyo_fill_normal_f16(vc.data_ptr(), vc.numel(), 42, 0.0, 1.0, stream(torch)))
+        kc.view(kv, max_seq, hd)[:, pos + 1:] = float("nan")
+        vc.view(kv, max_seq, hd)[:, pos + 1:, ::2] = float("inf")
+        vc.view(kv, max_seq, hd)[:, pos + 1:, 1::2] = float("nan")
+        q = orc.normal_f32(heads * hd, 500 + pos)
+        qd = dev(torch, q)
+        pd = dev(torch, np.array([pos], np.int32))
+        out = torch.empty_like(qd)
+        run(mh, torch, lib.muyo_attention_decode_f16kv(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, stream(torch)))
+        kbits = host(kc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
+        vbits = host(vc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
+        expect = orc.attention_f16kv(q, kbits, vbits, heads, kv, hd, max_seq, pos, scale)
+        got = host(out)
+        assert np.isfinite(got).all(), f"pos {pos}"
+        assert close(got, expect, 1e-3) == 0, f"pos {pos}"
 
 
 # ------------------------------------------------------------------------------------------------
