@@ -136,6 +136,34 @@ __device__ __forceinline__ float GroupSum(float value)
     return value;
 }
 
+/// GroupSum of N independent values, level by level: each lane permute reads a register written
+/// N instructions earlier, so the chain needs no wait states between its steps.
+template <int kWidth, int N>
+__device__ __forceinline__ void GroupSumN(float (&v)[N])
+{
+    static_assert(kWidth >= 1 && kWidth <= kWave && (kWidth & (kWidth - 1)) == 0, "width");
+#define MUYO_GROUP_SUM_LEVEL(step)                   \
+    if constexpr (kWidth >= 2 * (step))              \
+    {                                                \
+        float other[N];                              \
+        _Pragma("unroll") for (int i = 0; i < N; ++i) \
+        {                                            \
+            other[i] = PartnerLane<step>(v[i]);      \
+        }                                            \
+        _Pragma("unroll") for (int i = 0; i < N; ++i) \
+        {                                            \
+            v[i] += other[i];                        \
+        }                                            \
+    }
+    MUYO_GROUP_SUM_LEVEL(1)
+    MUYO_GROUP_SUM_LEVEL(2)
+    MUYO_GROUP_SUM_LEVEL(4)
+    MUYO_GROUP_SUM_LEVEL(8)
+    MUYO_GROUP_SUM_LEVEL(16)
+    MUYO_GROUP_SUM_LEVEL(32)
+#undef MUYO_GROUP_SUM_LEVEL
+}
+
 template <int kWidth>
 __device__ __forceinline__ float GroupMax(float value)
 {

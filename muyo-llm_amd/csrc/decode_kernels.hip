@@ -303,11 +303,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
                 epi.Ready(next);
             }
             // Every lane of the segment ends with the unit's row sums.
-#pragma unroll
-            for (int r = 0; r < kNr; ++r)
-            {
-                sums[r] = GroupSum<kLpr>(sums[r]);
-            }
+            GroupSumN<kLpr>(sums);
             if (unit < units && lir == 0)
             {
                 epi.Finish(unit, sums, pre, bestValue, bestIndex);
@@ -515,16 +511,26 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stag
             xhi[i].w = (scale * xhi[i].w) * ghi[i].w;
         }
     }
+    float d[kUnits * kNr];
 #pragma unroll
     for (int k = 0; k < kUnits; ++k)
     {
 #pragma unroll
         for (int r = 0; r < kNr; ++r)
         {
-            const float d = GroupSum<kWave>(DotRegisters<kWave, kCpl>(w[k][r], xlo, xhi, span, lane));
-            if (lane == 0)
+            d[k * kNr + r] = DotRegisters<kWave, kCpl>(w[k][r], xlo, xhi, span, lane);
+        }
+    }
+    GroupSumN<kWave>(d);
+    if (lane == 0)
+    {
+#pragma unroll
+        for (int k = 0; k < kUnits; ++k)
+        {
+#pragma unroll
+            for (int r = 0; r < kNr; ++r)
             {
-                partial[k][r][waveId] = d;
+                partial[k][r][waveId] = d[k * kNr + r];
             }
         }
     }
@@ -877,12 +883,12 @@ uint32_t ResidentBlocks(Kernel kernel, int threads, size_t lds)
     return CuCount() * static_cast<uint32_t>(perCu) * MUYO_GEMV_ROUNDS;
 }
 
-/// Launches `kernel` over `units`, or with blocksOut only reports its workgroup count. The grid
+/// Launches `kernel` over `units`, or with shapeOut only reports its grid. The grid
 /// holds at most the workgroups resident at once (each stages the activation once and then
 /// strides over the units), so no workgroup waits for a second round.
 template <auto kKernel, class Stage, class Epi, int kThreads = kBlock>
 hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBlock, uint32_t blockCap, size_t lds,
-                            uint32_t cols, const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+                            uint32_t cols, const Stage& stage, const Epi& epi, GemvShape* shapeOut)
 {
     const auto kernel = kKernel;
     // Cached per kernel (the statics belong to this instantiation).
@@ -894,9 +900,9 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
         residentLds = lds;
     }
     const uint32_t blocks = std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, resident}));
-    if (blocksOut != nullptr)
+    if (shapeOut != nullptr)
     {
-        *blocksOut = blocks;
+        *shapeOut = GemvShape{blocks, unitsPerBlock};
         return hipSuccess;
     }
     // Opt in to more than the default 64 KB of dynamic LDS only when a launch needs it.
@@ -920,33 +926,35 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
 /// round; hipErrorNotSupported (nothing launched) when none is.
 template <int kNr, int kUnits, class Stage, class Epi>
 hipError_t LaunchColumnsT(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_t cols, const Stage& stage,
-                          const Epi& epi, uint32_t* blocksOut)
+                          const Epi& epi, GemvShape* shapeOut)
 {
     constexpr auto kKernel = &FusedMatVecColumns<2, kNr, kUnits, Stage, Epi>;
-    uint32_t blocks = 0;
-    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, &blocks);
+    GemvShape probe{};
+    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, &probe);
+    const uint32_t blocks = probe.blocks;
     if (static_cast<uint64_t>(blocks) * kUnits < units)
     {
         if constexpr (kUnits < 6)
         {
-            return LaunchColumnsT<kNr, kUnits + 1, Stage, Epi>(s, units, blockCap, cols, stage, epi, blocksOut);
+            return LaunchColumnsT<kNr, kUnits + 1, Stage, Epi>(s, units, blockCap, cols, stage, epi, shapeOut);
         }
         return hipErrorNotSupported;
     }
-    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, blocksOut);
+    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, kUnits, blockCap, 0, cols, stage, epi, shapeOut);
 }
 
 template <int kLpr, int kCpl, int kNr, bool kSingle, class Stage, class Epi>
 hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
-                        const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+                        const Stage& stage, const Epi& epi, GemvShape* shapeOut)
 {
     constexpr uint32_t kUnitsPerBlock = kWaves * UnitsPerWave<kLpr, kNr, kSingle>();
     if constexpr (kSingle && Stage::kCanDirect)
     {
         // At most one workgroup per CU: latency-bound, so each lane stages its own chunks.
-        uint32_t blocks = 0;
+        GemvShape probe{};
         (void)LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
-            s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, &blocks);
+            s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, &probe);
+        const uint32_t blocks = probe.blocks;
         if (blocks <= CuCount())
         {
             // No LDS, so the workgroups can be small and spread over more CUs.
@@ -954,19 +962,20 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
             constexpr uint32_t kDirectUnits = (kDirectThreads / kWave) * UnitsPerWave<kLpr, kNr, kSingle>();
             return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, DirectStage<Stage>, Epi, kDirectThreads>,
                                     DirectStage<Stage>, Epi, kDirectThreads>(s, units, kDirectUnits, blockCap, 0, cols,
-                                                                             direct, epi, blocksOut);
+                                                                             direct, epi, shapeOut);
         }
         // More workgroups than CUs but few enough single-wave ones that every unit gets its own
         // segment in one round: single-wave workgroups balance the CUs (a 256-thread grid of
         // 1.2 CUs' worth leaves most CUs with one workgroup and some with two).
-        uint32_t small = 0;
+        GemvShape smallProbe{};
         constexpr uint32_t kSmallUnits = UnitsPerWave<kLpr, kNr, kSingle>();
         (void)LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
-            s, units, kSmallUnits, blockCap, lds, cols, stage, epi, &small);
+            s, units, kSmallUnits, blockCap, lds, cols, stage, epi, &smallProbe);
+        const uint32_t small = smallProbe.blocks;
         if (static_cast<uint64_t>(small) * kSmallUnits >= units)
         {
             return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
-                s, units, kSmallUnits, blockCap, lds, cols, stage, epi, blocksOut);
+                s, units, kSmallUnits, blockCap, lds, cols, stage, epi, shapeOut);
         }
 #ifndef MUYO_NO_COLUMNS
         // Units past one round of resident waves: column quarters with several units per
@@ -975,7 +984,7 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
         if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
         {
             const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
-                                                                        blocksOut);
+                                                                        shapeOut);
             if (status != hipErrorNotSupported)
             {
                 return status;
@@ -984,40 +993,46 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
 #endif
     }
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
-        s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, blocksOut);
+        s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, shapeOut);
 }
 
 /// hipErrorNotSupported (nothing launched) when a workgroup's share of the rows would overflow
 /// its partial-sum table.
 template <int kCpl, class Stage, class Epi>
 hipError_t LaunchSplitRowsT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
-                            const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+                            const Stage& stage, const Epi& epi, GemvShape* shapeOut)
 {
     constexpr auto kKernel = &FusedMatVecSplitRows<kCpl, Stage, Epi>;
     const size_t used = Stage::kElementwise ? 0 : lds;
-    uint32_t blocks = 0;
-    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, &blocks);
+    GemvShape probe{};
+    (void)LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, &probe);
+    const uint32_t blocks = probe.blocks;
     if (CeilDiv(units, blocks) > kMaxSplitRows)
     {
         return hipErrorNotSupported;
     }
-    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, blocksOut);
+    if (shapeOut != nullptr)
+    {
+        *shapeOut = GemvShape{blocks, CeilDiv(units, blocks)};  // a run of consecutive rows per workgroup
+        return hipSuccess;
+    }
+    return LaunchGemvKernel<kKernel, Stage, Epi>(s, units, 1, blockCap, used, cols, stage, epi, shapeOut);
 }
 
 template <int kCpl, class Stage, class Epi>
 hipError_t LaunchBlockRowT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t lds, uint32_t cols,
-                           const Stage& stage, const Epi& epi, uint32_t* blocksOut)
+                           const Stage& stage, const Epi& epi, GemvShape* shapeOut)
 {
     return LaunchGemvKernel<&FusedMatVecBlockRow<kCpl, Stage, Epi>, Stage, Epi>(s, units, 1, blockCap, lds, cols,
-                                                                                 stage, epi, blocksOut);
+                                                                                 stage, epi, shapeOut);
 }
 
-/// Launches (or, with blocksOut, only sizes) the fused GEMV for a row of `cols` fp16 weights.
+/// Launches (or, with shapeOut, only sizes) the fused GEMV for a row of `cols` fp16 weights.
 /// Rows of up to 1024 chunks (512 for two-row units) fit one batch of a wave segment; longer
 /// rows use two-row units in RowDot's batch ping-pong, or one workgroup per row.
 template <int kNr, class Stage, class Epi>
 hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_t cols, const Stage& stage,
-                       const Epi& epi, uint32_t* blocksOut = nullptr)
+                       const Epi& epi, GemvShape* shapeOut = nullptr)
 {
     if (cols % 8 != 0 || static_cast<size_t>(cols) * sizeof(float) > kMaxLds)
     {
@@ -1030,13 +1045,13 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     // exact-fit 16 x 7 shape's. 0.5B-shape QKV: 3.62 -> 3.37 us.
     if (nchunks > 64 && nchunks <= 128 && units <= kWideUnits)
     {
-        return LaunchFusedT<64, 2, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        return LaunchFusedT<64, 2, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
     }
     const RowShape shape = PickFusedShape(nchunks, kNr);
 #define MUYO_FUSED_CASE(L, C)                                                                                    \
     if (shape.lpr == L && shape.cpl == C)                                                                        \
     {                                                                                                            \
-        return LaunchFusedT<L, C, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
+        return LaunchFusedT<L, C, kNr, true, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut); \
     }
     MUYO_FUSED_CASE(8, 7)
     MUYO_FUSED_CASE(8, 8)
@@ -1050,7 +1065,7 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
     if constexpr (kNr == 2)
     {
         // Rows past 640 chunks: the two rows of a unit in adjacent 32-lane segments.
-        return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+        return LaunchFusedT<32, 16, kNr, false, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
     }
     else
     {
@@ -1063,19 +1078,19 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
         hipError_t split = hipErrorNotSupported;
         if (qcpl <= 8)
         {
-            split = LaunchSplitRowsT<8, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+            split = LaunchSplitRowsT<8, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
         }
         else if (qcpl <= 10)
         {
-            split = LaunchSplitRowsT<10, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+            split = LaunchSplitRowsT<10, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
         }
         else if (qcpl <= 12)
         {
-            split = LaunchSplitRowsT<12, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+            split = LaunchSplitRowsT<12, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
         }
         else if (qcpl <= 16)
         {
-            split = LaunchSplitRowsT<16, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut);
+            split = LaunchSplitRowsT<16, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut);
         }
         if (split != hipErrorNotSupported)
         {
@@ -1085,7 +1100,7 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
 #define MUYO_BLOCK_ROW_CASE(C)                                                                       \
     if (cpl <= C)                                                                                    \
     {                                                                                                \
-        return LaunchBlockRowT<C, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, blocksOut); \
+        return LaunchBlockRowT<C, Stage, Epi>(s, units, blockCap, lds, cols, stage, epi, shapeOut); \
     }
         MUYO_BLOCK_ROW_CASE(8)
         MUYO_BLOCK_ROW_CASE(10)
@@ -1313,22 +1328,25 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         acc[c] = 0.0f;
     }
     // Online softmax over one round of blocks b0 .. b0 + kR - 1. Keys past the position and
-    // blocks past this chunk's are masked; their rows may hold anything, so their V is selected
-    // out rather than weighted by 0.
+    // blocks past this chunk's are masked; their rows may hold anything, so their V is zeroed as
+    // well as weighted by 0.
     auto consume = [&](uint32_t b0) {
+        // Dot products first, then their lane sums level by level, so the permutes of the
+        // blocks interleave instead of each waiting on its own previous step.
         float s[kR];
         bool valid[kR];
-        float top = m;
 #pragma unroll
         for (int k = 0; k < kR; ++k)
         {
             valid[k] = b0 + k < mine && keyOf(b0 + k) < keys;
-            s[k] = -INFINITY;
-            if (b0 + k < mine)  // uniform over the workgroup
-            {
-                const float d = GroupSum<kRC>(DotChunk(kk[k], q0, q1, 0.0f)) * sl;
-                s[k] = valid[k] ? d : -INFINITY;
-            }
+            s[k] = DotChunk(kk[k], q0, q1, 0.0f);
+        }
+        GroupSumN<kRC>(s);
+        float top = m;
+#pragma unroll
+        for (int k = 0; k < kR; ++k)
+        {
+            s[k] = valid[k] ? s[k] * sl : -INFINITY;
             top = fmaxf(top, s[k]);
         }
         if (top == -INFINITY)
@@ -1344,6 +1362,10 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         {
             p[k] = valid[k] ? exp2f(s[k] - top) : 0.0f;
             psum += p[k];
+            if (!valid[k])
+            {
+                vv[k] = half8{};  // 0 * NaN would be NaN
+            }
         }
         l = fmaf(l, factor, psum);
 #pragma unroll
@@ -1353,7 +1375,7 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
 #pragma unroll
             for (int k = 0; k < kR; ++k)
             {
-                a = valid[k] ? fmaf(p[k], static_cast<float>(vv[k][c]), a) : a;
+                a = fmaf(p[k], static_cast<float>(vv[k][c]), a);
             }
             acc[c] = a;
         }
@@ -1536,12 +1558,12 @@ __global__ __launch_bounds__(kBlock) void RopeAppendKernel(const float* __restri
 
 uint32_t LmHeadBlocks(const DecodeDims& dims)
 {
-    uint32_t blocks = 0;
+    GemvShape shape{};
     LmHeadEpi epi{};
     epi.rows = dims.vocab;
     (void)LaunchFused<1>(nullptr, dims.vocab, kArgMaxBlocks, dims.hidden,
-                         NormStage{nullptr, nullptr, 0.0f}, epi, &blocks);
-    return blocks;
+                         NormStage{nullptr, nullptr, 0.0f}, epi, &shape);
+    return shape.blocks;
 }
 
 bool MergeInOProj(const DecodeDims& dims)

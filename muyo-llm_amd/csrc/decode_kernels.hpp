@@ -70,6 +70,14 @@ inline uint32_t AttnGridChunks(uint32_t maxSeq, uint32_t headDim, uint32_t maxCh
     return bySlices < maxChunks ? bySlices : maxChunks;
 }
 
+/// Grid of a fused GEMV launch: `blocks` workgroups; when blocks * unitsPerBlock covers the
+/// units, workgroup i owns units [i * unitsPerBlock, (i + 1) * unitsPerBlock).
+struct GemvShape
+{
+    uint32_t blocks;
+    uint32_t unitsPerBlock;
+};
+
 /// Workgroups of the LM-head kernel (each leaves one argmax partial).
 uint32_t LmHeadBlocks(const DecodeDims& dims);
 
