@@ -448,9 +448,12 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
 }
 
 // ------------------------------------------------------------------------------------------------
-// Causal flash attention. A workgroup owns one kv head and 32 consecutive queries; its waves are
-// the query heads of that kv head's group and share each 32-key tile of K and V through LDS (V
-// stored transposed, channel-major). Per wave and tile:
+// Causal flash attention. A workgroup owns one kv head, 32 consecutive queries and up to
+// kHeadsPerBlock of the group's query heads, one per wave (a group of 7 takes two workgroups when
+// one per tile would leave CUs idle); the waves share each 32-key tile of K and V through LDS (V
+// stored transposed, channel-major). The next tile's rows are loaded into registers while the
+// current one is multiplied, so a workgroup waits on memory once, not once per tile. Per wave
+// and tile:
 //   S^T (keys x queries) = K . Q^T on the matrix cores (K the A operand from LDS, Q the B operand
 //   held in registers as split planes), so a lane holds 16 keys of one query and the online
 //   softmax needs only one exchange with the lane 32 away;
@@ -461,25 +464,31 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
 constexpr int kAttnKeys = 32;
 constexpr int kVStride = kAttnKeys + 8;  // halves per transposed V row
 
-template <int kHd>
-__global__ __launch_bounds__(512) void PrefillAttentionKernel(
+/// Grid (head splits, query tiles, kv heads): the splits of one tile are dispatched together and
+/// the longest tiles first.
+template <int kHd, int kHeadsPerBlock>
+__global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel(
     const uint16_t* __restrict__ qhi, const uint16_t* __restrict__ qlo, const uint16_t* __restrict__ kcache,
     const uint16_t* __restrict__ vcache, uint16_t* __restrict__ ohi, uint16_t* __restrict__ olo, uint32_t rows,
     int32_t pos0, uint32_t heads, uint32_t kvHeads, uint32_t maxSeq, float scale)
 {
     constexpr int kKStride = kHd + 8;
     constexpr int kChunks = kHd / 8;
+    constexpr int kThreads = kWave * kHeadsPerBlock;
+    constexpr int kLoads = (kAttnKeys * kChunks + kThreads - 1) / kThreads;  // K (and V) chunks per thread per tile
     __shared__ __attribute__((aligned(16))) uint16_t kTile[kAttnKeys * kKStride];
     __shared__ __attribute__((aligned(16))) uint16_t vTile[kHd * kVStride];
 
     const uint32_t group = heads / kvHeads;
-    const uint32_t tiles = gridDim.x;
-    const uint32_t qtile = tiles - 1 - blockIdx.x;  // longest rows first
-    const uint32_t g = blockIdx.y;
+    const uint32_t tiles = gridDim.y;
+    const uint32_t qtile = tiles - 1 - blockIdx.y;  // longest rows first
+    const uint32_t g = blockIdx.z;
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t h = lane / 32;
-    const uint32_t head = g * group + wave;
+    const uint32_t inGroup = blockIdx.x * kHeadsPerBlock + wave;
+    const bool active = inGroup < group;  // a wave past the group only loads tiles
+    const uint32_t head = g * group + (active ? inGroup : group - 1);
     const uint32_t qdim = heads * kHd;
     const uint32_t m0 = qtile * 32;
     const uint32_t mq = m0 + lane % 32 < rows ? m0 + lane % 32 : rows - 1;
@@ -508,24 +517,48 @@ __global__ __launch_bounds__(512) void PrefillAttentionKernel(
     const uint16_t* kBase = kcache + static_cast<uint64_t>(g) * maxSeq * kHd;
     const uint16_t* vBase = vcache + static_cast<uint64_t>(g) * maxSeq * kHd;
 
+    half8 kReg[kLoads], vReg[kLoads];
+    auto loadTile = [&](uint32_t kt) {
+#pragma unroll
+        for (int i = 0; i < kLoads; ++i)
+        {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            const uint32_t r = c % kAttnKeys;               // key within the tile
+            const uint32_t cc = (c / kAttnKeys) % kChunks;  // 8-channel chunk
+            const uint32_t key = kt * kAttnKeys + r < maxSeq ? kt * kAttnKeys + r : maxSeq - 1;
+            kReg[i] = *reinterpret_cast<const half8*>(kBase + static_cast<uint64_t>(key) * kHd + cc * 8);
+            vReg[i] = *reinterpret_cast<const half8*>(vBase + static_cast<uint64_t>(key) * kHd + cc * 8);
+        }
+    };
+    loadTile(0);
     for (uint32_t kt = 0; kt < keyTiles; ++kt)
     {
         __syncthreads();  // every wave is done with the previous tile
-        for (uint32_t c = threadIdx.x; c < kAttnKeys * kChunks; c += blockDim.x)
-        {
-            const uint32_t r = c % kAttnKeys;  // key within the tile
-            const uint32_t cc = c / kAttnKeys;  // 8-channel chunk
-            const uint32_t key = kt * kAttnKeys + r < maxSeq ? kt * kAttnKeys + r : maxSeq - 1;
-            const half8 kv = *reinterpret_cast<const half8*>(kBase + static_cast<uint64_t>(key) * kHd + cc * 8);
-            const half8 vv = *reinterpret_cast<const half8*>(vBase + static_cast<uint64_t>(key) * kHd + cc * 8);
-            *reinterpret_cast<half8*>(kTile + r * kKStride + cc * 8) = kv;
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+        for (int i = 0; i < kLoads; ++i)
+        {
+            const uint32_t c = threadIdx.x + i * kThreads;
+            if (c < kAttnKeys * kChunks)
             {
-                reinterpret_cast<_Float16*>(vTile)[(cc * 8 + i) * kVStride + r] = vv[i];
+                const uint32_t r = c % kAttnKeys;
+                const uint32_t cc = c / kAttnKeys;
+                *reinterpret_cast<half8*>(kTile + r * kKStride + cc * 8) = kReg[i];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                {
+                    reinterpret_cast<_Float16*>(vTile)[(cc * 8 + j) * kVStride + r] = vReg[i][j];
+                }
             }
         }
         __syncthreads();
+        if (kt + 1 < keyTiles)
+        {
+            loadTile(kt + 1);  // in flight while this tile is multiplied
+        }
+        if (!active)
+        {
+            continue;
+        }
 
         floatx16 st = floatx16{};
         const uint16_t* kFrag = kTile + (lane % 32) * kKStride + 8 * h;
@@ -592,7 +625,7 @@ __global__ __launch_bounds__(512) void PrefillAttentionKernel(
 
     const float total = runSum + __shfl_xor(runSum, 32);
     const uint32_t m = m0 + lane % 32;
-    if (m < rows)
+    if (active && m < rows)
     {
         const float inv = 1.0f / total;
         const uint64_t base = static_cast<uint64_t>(m) * qdim + head * kHd;
@@ -689,22 +722,38 @@ hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint
     {
         return hipErrorInvalidValue;
     }
-    const dim3 grid(CeilDiv(rows, 32), kvHeads);
-    const dim3 block(kWave * (heads / kvHeads));
-    switch (headDim)
+    // A workgroup per (kv head, query tile) holding the whole group when that alone fills the chip
+    // (7B shape: 256 workgroups, one K/V staging per tile for all 7 heads); otherwise groups past
+    // four heads take two workgroups (0.5B shape: 128 -> 256).
+    const uint32_t group = heads / kvHeads;
+    int device = 0;
+    int cus = 256;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
     {
-        case 64:
-            hipLaunchKernelGGL(PrefillAttentionKernel<64>, grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, olo,
-                               rows, pos0, heads, kvHeads, maxSeq, scale);
-            break;
-        case 128:
-            hipLaunchKernelGGL(PrefillAttentionKernel<128>, grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, olo,
-                               rows, pos0, heads, kvHeads, maxSeq, scale);
-            break;
-        default:
-            return hipErrorInvalidValue;
+        cus = 256;
     }
-    return hipGetLastError();
+    const bool fills = static_cast<uint64_t>(CeilDiv(rows, 32)) * kvHeads >= static_cast<uint64_t>(cus);
+    const uint32_t perBlock = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 || !fills ? 4 : 8;
+    const dim3 grid(CeilDiv(group, perBlock), CeilDiv(rows, 32), kvHeads);
+    const dim3 block(kWave * perBlock);
+#define MUYO_PREFILL_ATTENTION(HD, P)                                                                        \
+    if (headDim == HD && perBlock == P)                                                                      \
+    {                                                                                                        \
+        hipLaunchKernelGGL((PrefillAttentionKernel<HD, P>), grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, \
+                           olo, rows, pos0, heads, kvHeads, maxSeq, scale);                                  \
+        return hipGetLastError();                                                                            \
+    }
+    MUYO_PREFILL_ATTENTION(64, 1)
+    MUYO_PREFILL_ATTENTION(64, 2)
+    MUYO_PREFILL_ATTENTION(64, 4)
+    MUYO_PREFILL_ATTENTION(64, 8)
+    MUYO_PREFILL_ATTENTION(128, 1)
+    MUYO_PREFILL_ATTENTION(128, 2)
+    MUYO_PREFILL_ATTENTION(128, 4)
+    MUYO_PREFILL_ATTENTION(128, 8)
+#undef MUYO_PREFILL_ATTENTION
+    return hipErrorInvalidValue;
 }
 }  // namespace muyo
 

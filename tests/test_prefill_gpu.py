@@ -233,7 +233,7 @@ def test_rope_split_append_matches_oracle(mh, gpu, orc, heads, kv_heads, head_di
     assert np.all(np.abs(orc.half_to_float(got_k) - want_f) <= np.abs(want_f) * 2.0 ** -10 + 2.0 ** -24)  # 1 ulp
 
 
-def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed):
+def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed, check=None):
     q = orc.normal_f32(rows * heads * head_dim, seed).reshape(rows, heads * head_dim)
     kc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 1).reshape(kv_heads, max_seq, head_dim)
     vc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 2).reshape(kv_heads, max_seq, head_dim)
@@ -245,7 +245,7 @@ def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0
                                                           ohi.data_ptr(), olo.data_ptr(), rows, pos0, heads,
                                                           kv_heads, head_dim, max_seq, scale, stream(torch)))
     got = joined(ohi, olo)
-    for m in range(rows):
+    for m in (range(rows) if check is None else check):
         want = orc.attention_f16kv(q[m], kc, vc, heads, kv_heads, head_dim, max_seq, pos0 + m, scale)
         assert close(got[m], want, 1e-3) == 0, m
         assert worst(got[m], want) < 2e-5, (m, worst(got[m], want))
@@ -261,6 +261,16 @@ def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0
 ])
 def test_prefill_attention_matches_per_token_attention(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq):
     prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, heads + rows + pos0)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim", [(14, 2, 64), (28, 4, 128)])
+def test_prefill_attention_full_prompt(mh, gpu, orc, heads, kv_heads, head_dim):
+    """2048 queries: the 0.5B shape's groups of 7 split over two workgroups per tile, the 7B shape's
+    whole groups (its grid alone fills the chip); rows checked at tile edges and spread over the
+    prompt."""
+    rows = 2048
+    check = [0, 1, 31, 32, 33, 500, 1023, 1024, 1537, 2015, 2016, 2046, 2047]
+    prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, 0, rows, 7 + heads, check)
 
 
 def test_prefill_attention_refusals(mh, gpu):
