@@ -133,6 +133,7 @@ struct MuyoDecoder
     uint16_t* pAttnLo = nullptr;
     uint16_t* pActHi = nullptr;  // [rows][ffn] swiglu output
     uint16_t* pActLo = nullptr;
+    float* pPartial = nullptr;   // [kMaxGemmSplits][rows][max(qkv rows, hidden)] K-split partial sums
 
     template <typename T>
     T* At(const TensorSlot& slot) const
@@ -999,6 +1000,8 @@ int EnsurePrefill(MuyoDecoder* d)
     const size_t attnLo = place(rows * qdim * 2);
     const size_t actHi = place(rows * c.feedForward * 2);
     const size_t actLo = place(rows * c.feedForward * 2);
+    // K-split partial sums of the GEMMs whose tiles alone leave the chip idle (GemmSplits).
+    const size_t partial = place(kMaxGemmSplits * rows * std::max<size_t>(qkvRows, c.hidden) * 4);
     char* arena = nullptr;
     if (hipMalloc(reinterpret_cast<void**>(&arena), cursor) != hipSuccess)
     {
@@ -1019,6 +1022,7 @@ int EnsurePrefill(MuyoDecoder* d)
     d->pAttnLo = reinterpret_cast<uint16_t*>(arena + attnLo);
     d->pActHi = reinterpret_cast<uint16_t*>(arena + actHi);
     d->pActLo = reinterpret_cast<uint16_t*>(arena + actLo);
+    d->pPartial = reinterpret_cast<float*>(arena + partial);
     return MUYO_OK;
 }
 
@@ -1037,23 +1041,29 @@ int EnqueuePrefillPass(MuyoDecoder* d, hipStream_t s, uint32_t rows, int32_t pos
     }
     float* x = d->pxA;
     float* other = d->pxB;
+    uint32_t pending = 0;  // K splits of the previous layer's down GEMM not yet summed into x
     for (uint32_t l = 0; l < c.layers; ++l)
     {
         uint16_t* kcache = d->At<uint16_t>(d->Layer(l, kKCache));
         uint16_t* vcache = d->At<uint16_t>(d->Layer(l, kVCache));
-        if ((status = LaunchRmsNormSplit(s, x, d->At<float>(d->Layer(l, kAttnNorm)), rows, c.hidden, c.rmsEps,
-                                         d->pNormHi, d->pNormLo)) != hipSuccess)
+        const float* attnNorm = d->At<float>(d->Layer(l, kAttnNorm));
+        status = pending > 0 ? LaunchReduceRmsNormSplit(s, d->pxMid, d->pPartial, pending, x, attnNorm, rows,
+                                                        c.hidden, c.rmsEps, d->pNormHi, d->pNormLo)
+                             : LaunchRmsNormSplit(s, x, attnNorm, rows, c.hidden, c.rmsEps, d->pNormHi, d->pNormLo);
+        if (status != hipSuccess)
         {
             return LaunchFailed(status, "prefill attn_norm", l);
         }
-        if ((status = LaunchGemmSplit(s, d->pNormHi, d->pNormLo, d->At<uint16_t>(d->Layer(l, kQkv)),
-                                      d->At<float>(d->Layer(l, kQkvBias)), nullptr, d->pQkv, rows, qkvRows,
-                                      c.hidden)) != hipSuccess)
+        const float* qkvBias = d->At<float>(d->Layer(l, kQkvBias));
+        const uint32_t qkvSplits = GemmSplits(rows, qkvRows, c.hidden);
+        if ((status = LaunchGemmSplit(s, d->pNormHi, d->pNormLo, d->At<uint16_t>(d->Layer(l, kQkv)), qkvBias, nullptr,
+                                      d->pQkv, rows, qkvRows, c.hidden, d->pPartial, qkvSplits)) != hipSuccess)
         {
             return LaunchFailed(status, "prefill qkv", l);
         }
-        if ((status = LaunchRopeSplitAppend(s, d->pQkv, rows, pos0, c.heads, c.kvHeads, c.headDim, c.maxSeq,
-                                            d->dims.ropePow, d->pQHi, d->pQLo, kcache, vcache)) != hipSuccess)
+        if ((status = LaunchRopeSplitAppend(s, qkvSplits > 1 ? d->pPartial : d->pQkv, rows, pos0, c.heads, c.kvHeads,
+                                            c.headDim, c.maxSeq, d->dims.ropePow, d->pQHi, d->pQLo, kcache, vcache,
+                                            qkvSplits, qkvBias)) != hipSuccess)
         {
             return LaunchFailed(status, "prefill rope", l);
         }
@@ -1063,13 +1073,18 @@ int EnqueuePrefillPass(MuyoDecoder* d, hipStream_t s, uint32_t rows, int32_t pos
         {
             return LaunchFailed(status, "prefill attention", l);
         }
+        const uint32_t oSplits = GemmSplits(rows, c.hidden, qdim);
         if ((status = LaunchGemmSplit(s, d->pAttnHi, d->pAttnLo, d->At<uint16_t>(d->Layer(l, kOut)), nullptr, x,
-                                      d->pxMid, rows, c.hidden, qdim)) != hipSuccess)
+                                      d->pxMid, rows, c.hidden, qdim, d->pPartial, oSplits)) != hipSuccess)
         {
             return LaunchFailed(status, "prefill o_proj", l);
         }
-        if ((status = LaunchRmsNormSplit(s, d->pxMid, d->At<float>(d->Layer(l, kFfnNorm)), rows, c.hidden, c.rmsEps,
-                                         d->pNormHi, d->pNormLo)) != hipSuccess)
+        const float* ffnNorm = d->At<float>(d->Layer(l, kFfnNorm));
+        status = oSplits > 1 ? LaunchReduceRmsNormSplit(s, x, d->pPartial, oSplits, d->pxMid, ffnNorm, rows, c.hidden,
+                                                        c.rmsEps, d->pNormHi, d->pNormLo)
+                             : LaunchRmsNormSplit(s, d->pxMid, ffnNorm, rows, c.hidden, c.rmsEps, d->pNormHi,
+                                                  d->pNormLo);
+        if (status != hipSuccess)
         {
             return LaunchFailed(status, "prefill ffn_norm", l);
         }
@@ -1079,12 +1094,24 @@ int EnqueuePrefillPass(MuyoDecoder* d, hipStream_t s, uint32_t rows, int32_t pos
         {
             return LaunchFailed(status, "prefill gate_up", l);
         }
+        const uint32_t downSplits = GemmSplits(rows, c.hidden, c.feedForward);
         if ((status = LaunchGemmSplit(s, d->pActHi, d->pActLo, d->At<uint16_t>(d->Layer(l, kDown)), nullptr,
-                                      d->pxMid, other, rows, c.hidden, c.feedForward)) != hipSuccess)
+                                      d->pxMid, other, rows, c.hidden, c.feedForward, d->pPartial, downSplits)) !=
+            hipSuccess)
         {
             return LaunchFailed(status, "prefill down", l);
         }
+        pending = downSplits > 1 ? downSplits : 0;
         std::swap(x, other);
+    }
+    if (pending > 0)
+    {
+        status = LaunchReduceRmsNormSplit(s, d->pxMid, d->pPartial, pending, x, nullptr, rows, c.hidden, c.rmsEps,
+                                          nullptr, nullptr);
+        if (status != hipSuccess)
+        {
+            return LaunchFailed(status, "prefill down", c.layers - 1);
+        }
     }
     *result = x;
     return MUYO_OK;

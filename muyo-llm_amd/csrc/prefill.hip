@@ -5,6 +5,7 @@
 // Matrix-core lane layout of v_mfma_f32_32x32x16_f16 (D = A.B, A 32x16, B 16x32), as used below:
 // lane l supplies A[l % 32][8 * (l / 32) .. +8] and B[8 * (l / 32) .. +8][l % 32], and receives
 // D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32] in accumulator r (0..15).
+#include <algorithm>
 #include <cmath>
 #include <initializer_list>
 
@@ -67,10 +68,42 @@ __global__ __launch_bounds__(256) void EmbedRowsKernel(const uint16_t* __restric
     }
 }
 
-/// One wave per row: sum of squares across the wave, then (scale * x) * w split into planes.
-__global__ __launch_bounds__(256) void RmsNormSplitKernel(const float* __restrict__ x, const float* __restrict__ w,
+/// The K splits of a split GEMM folded into its consumer: x = residual + (P_0 + P_1 + ...) in
+/// split order, the unsplit epilogue's residual + sum.
+struct SplitSum
+{
+    const float* residual;  // may be null
+    const float* partial;   // [splits][rows][cols]
+    uint32_t splits;
+    uint64_t stride;        // rows * cols
+
+    __device__ float4 At(uint64_t i) const
+    {
+        float4 a = *reinterpret_cast<const float4*>(partial + i);
+        for (uint32_t z = 1; z < splits; ++z)
+        {
+            const float4 b = *reinterpret_cast<const float4*>(partial + z * stride + i);
+            a.x += b.x;
+            a.y += b.y;
+            a.z += b.z;
+            a.w += b.w;
+        }
+        if (residual != nullptr)
+        {
+            const float4 r = *reinterpret_cast<const float4*>(residual + i);
+            a = make_float4(r.x + a.x, r.y + a.y, r.z + a.z, r.w + a.w);
+        }
+        return a;
+    }
+};
+
+/// One wave per row: sum of squares across the wave, then (scale * x) * w split into planes. With
+/// a split sum (splits > 0) the row is first reduced from its parts and stored to x; without w
+/// only that.
+__global__ __launch_bounds__(256) void RmsNormSplitKernel(float* __restrict__ x, const float* __restrict__ w,
                                                           uint32_t rows, uint32_t cols, float eps,
-                                                          uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
+                                                          uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                          SplitSum sum)
 {
     const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
     if (row >= rows)
@@ -78,12 +111,25 @@ __global__ __launch_bounds__(256) void RmsNormSplitKernel(const float* __restric
         return;
     }
     const uint32_t lane = threadIdx.x % kWave;
-    const float* xr = x + static_cast<uint64_t>(row) * cols;
+    float* xr = x + static_cast<uint64_t>(row) * cols;
     float ss = 0.0f;
     for (uint32_t i = lane * 4; i < cols; i += 4 * kWave)
     {
-        const float4 v = *reinterpret_cast<const float4*>(xr + i);
+        float4 v;
+        if (sum.splits > 0)
+        {
+            v = sum.At(static_cast<uint64_t>(row) * cols + i);
+            *reinterpret_cast<float4*>(xr + i) = v;  // read back below by this lane only
+        }
+        else
+        {
+            v = *reinterpret_cast<const float4*>(xr + i);
+        }
         ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    if (w == nullptr)
+    {
+        return;
     }
     ss = GroupSum<kWave>(ss);
     const float scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
@@ -109,13 +155,16 @@ __global__ __launch_bounds__(256) void SplitF32Kernel(const float* __restrict__ 
 /// The decode step's rope and cache append (rope_funcs.glsl:76-114; the fp16 cache rows of
 /// src/FullModel.cpp:771-784) for many positions: one thread per (row, unit), units as in the
 /// decode QKV epilogue: rope pairs (j, j + hd/2) of each q and k head, then pairs of v channels.
+/// With splits > 1, qkv holds the K splits' raw sums ([splits][rows][width]) and each value is
+/// their sum plus bias, the unsplit epilogue's acc + bias.
 __global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __restrict__ qkv, uint32_t rows,
                                                              int32_t pos0, uint32_t heads, uint32_t kvHeads,
                                                              uint32_t headDim, uint32_t maxSeq,
                                                              const float* __restrict__ ropePow,
                                                              uint16_t* __restrict__ qhi, uint16_t* __restrict__ qlo,
                                                              uint16_t* __restrict__ kcache,
-                                                             uint16_t* __restrict__ vcache)
+                                                             uint16_t* __restrict__ vcache, uint32_t splits,
+                                                             const float* __restrict__ bias)
 {
     const uint32_t half = headDim / 2;
     const uint32_t ropeUnits = (heads + kvHeads) * half;
@@ -130,12 +179,25 @@ __global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __rest
     const int32_t pos = pos0 + static_cast<int32_t>(m);
     const uint32_t width = (heads + 2 * kvHeads) * headDim;
     const float* row = qkv + static_cast<uint64_t>(m) * width;
+    const uint64_t stride = static_cast<uint64_t>(rows) * width;
+    auto value = [&](uint32_t col) {
+        if (splits <= 1)
+        {
+            return row[col];
+        }
+        float a = row[col];
+        for (uint32_t z = 1; z < splits; ++z)
+        {
+            a += row[z * stride + col];
+        }
+        return a + bias[col];
+    };
     if (unit < ropeUnits)
     {
         const uint32_t head = unit / half;
         const uint32_t j = unit % half;
-        const float s0 = row[head * headDim + j];
-        const float s1 = row[head * headDim + j + half];
+        const float s0 = value(head * headDim + j);
+        const float s1 = value(head * headDim + j + half);
         const float theta = static_cast<float>(pos) * ropePow[j];
         const float c = cosf(theta);
         const float sn = sinf(theta);
@@ -163,9 +225,9 @@ __global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __rest
         const uint32_t channel = 2 * (unit - ropeUnits);  // within kvHeads * headDim
         const uint32_t g = channel / headDim;
         const uint64_t base = (static_cast<uint64_t>(g) * maxSeq + pos) * headDim + channel % headDim;
-        const float* v = row + (heads + kvHeads) * headDim + channel;
-        vcache[base] = FloatToHalfBits(v[0]);
-        vcache[base + 1] = FloatToHalfBits(v[1]);
+        const uint32_t v = (heads + kvHeads) * headDim + channel;
+        vcache[base] = FloatToHalfBits(value(v));
+        vcache[base + 1] = FloatToHalfBits(value(v + 1));
     }
 }
 
@@ -182,6 +244,8 @@ constexpr int kGemmBK = 64;
 constexpr int kGemmStride = kGemmBK + 8;
 
 /// out = acc + bias[n] + residual[m][n] (either may be null); virtual rows are the weight rows.
+/// With `partial` the grid splits K (blockIdx.z) and each split stores its raw sums to plane z of
+/// `partial` ([splits][rows][n]); bias and residual are then the consumer's to add.
 struct PlainEpi
 {
     const uint16_t* w;
@@ -189,6 +253,7 @@ struct PlainEpi
     const float* residual;
     float* out;
     uint32_t n, k;
+    float* partial = nullptr;
 
     __device__ const uint16_t* WRow(uint32_t row) const
     {
@@ -221,6 +286,11 @@ struct PlainEpi
                     float4 v = make_float4(acc[nb][mb][4 * g], acc[nb][mb][4 * g + 1], acc[nb][mb][4 * g + 2],
                                            acc[nb][mb][4 * g + 3]);
                     const uint64_t at = static_cast<uint64_t>(m) * n + nn;
+                    if (partial != nullptr)
+                    {
+                        *reinterpret_cast<float4*>(partial + static_cast<uint64_t>(blockIdx.z) * rows * n + at) = v;
+                        continue;
+                    }
                     if (bias != nullptr)
                     {
                         const float4 b = *reinterpret_cast<const float4*>(bias + nn);
@@ -295,10 +365,11 @@ struct SwiGluEpi
     }
 };
 
+/// The grid's z splits K into runs of kPerSplit (a multiple of kGemmBK) columns.
 template <int kWm, int kWn, typename Epi>
 __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
                                                                      const uint16_t* __restrict__ alo, Epi epi,
-                                                                     uint32_t rows, uint32_t k)
+                                                                     uint32_t rows, uint32_t k, uint32_t kPerSplit)
 {
     constexpr int kThreads = kWave * kWm * kWn;
     constexpr int kBM = 64 * kWm;
@@ -342,6 +413,8 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
         wCol[i] = cc * 8;
     }
 
+    const uint32_t kBegin = blockIdx.z * kPerSplit;
+    const uint32_t kEnd = min(k, kBegin + kPerSplit);
     half8 aReg[kALoads];
     half8 wReg[kWLoads];
     auto load = [&](uint32_t k0)
@@ -349,12 +422,12 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
         {
-            aReg[i] = k0 + aCol[i] < k ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
+            aReg[i] = k0 + aCol[i] < kEnd ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
         }
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
         {
-            wReg[i] = k0 + wCol[i] < k ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
+            wReg[i] = k0 + wCol[i] < kEnd ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
         }
     };
 
@@ -379,8 +452,8 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
         }
     }
 
-    load(0);
-    for (uint32_t k0 = 0; k0 < k; k0 += kGemmBK)
+    load(kBegin);
+    for (uint32_t k0 = kBegin; k0 < kEnd; k0 += kGemmBK)
     {
         __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
@@ -394,7 +467,7 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
             *reinterpret_cast<half8*>(lds + wDst[i]) = wReg[i];
         }
         __syncthreads();
-        if (k0 + kGemmBK < k)
+        if (k0 + kGemmBK < kEnd)
         {
             load(k0 + kGemmBK);
         }
@@ -424,25 +497,30 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
     epi.Finish(acc, n0 + wn * 64, m0 + wm * 64, rows);
 }
 
+/// 128 x 128 tiles when they alone give two workgroups per CU; 64-token tiles otherwise.
+bool BigTiles(uint32_t rows, uint32_t virtualRows)
+{
+    return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128) >= 512;
+}
+
 template <typename Epi>
 hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const Epi& epi, uint32_t rows,
-                      uint32_t virtualRows, uint32_t k)
+                      uint32_t virtualRows, uint32_t k, uint32_t splits = 1)
 {
-    if (rows == 0 || virtualRows == 0 || k == 0)
+    if (rows == 0 || virtualRows == 0 || k == 0 || splits == 0)
     {
         return hipErrorInvalidValue;
     }
-    // 128 x 128 tiles when they alone give two workgroups per CU; 64-token tiles otherwise.
-    const uint64_t big = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128);
-    if (big >= 512)
+    const uint32_t kPerSplit = CeilDiv(CeilDiv(k, kGemmBK), splits) * kGemmBK;
+    if (BigTiles(rows, virtualRows))
     {
-        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128)),
-                           dim3(256), 0, s, ahi, alo, epi, rows, k);
+        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128), splits),
+                           dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
     else
     {
-        hipLaunchKernelGGL((GemmSplitKernel<1, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 64)),
-                           dim3(128), 0, s, ahi, alo, epi, rows, k);
+        hipLaunchKernelGGL((GemmSplitKernel<1, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 64), splits),
+                           dim3(128), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
     return hipGetLastError();
 }
@@ -655,11 +733,26 @@ hipError_t LaunchEmbedRows(hipStream_t s, const uint16_t* table, const int32_t* 
 hipError_t LaunchRmsNormSplit(hipStream_t s, const float* x, const float* w, uint32_t rows, uint32_t cols, float eps,
                               uint16_t* hi, uint16_t* lo)
 {
-    if (rows == 0 || cols == 0 || cols % 4 != 0)
+    if (rows == 0 || cols == 0 || cols % 4 != 0 || w == nullptr)
     {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo);
+    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, const_cast<float*>(x), w, rows,
+                       cols, eps, hi, lo, SplitSum{});
+    return hipGetLastError();
+}
+
+hipError_t LaunchReduceRmsNormSplit(hipStream_t s, const float* residual, const float* partial, uint32_t splits,
+                                    float* x, const float* w, uint32_t rows, uint32_t cols, float eps, uint16_t* hi,
+                                    uint16_t* lo)
+{
+    if (rows == 0 || cols == 0 || cols % 4 != 0 || splits == 0 || splits > kMaxGemmSplits || partial == nullptr)
+    {
+        return hipErrorInvalidValue;
+    }
+    const SplitSum sum{residual, partial, splits, static_cast<uint64_t>(rows) * cols};
+    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo,
+                       sum);
     return hipGetLastError();
 }
 
@@ -675,15 +768,35 @@ hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_
     return hipGetLastError();
 }
 
+uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k)
+{
+    // Waves of the unsplit grid (64 x 64 outputs each); short of ~1024 (a wave per SIMD), K is
+    // split so the grid reaches it, keeping at least two K tiles per split.
+    if (rows == 0 || n == 0 || BigTiles(rows, n))
+    {
+        return 1;
+    }
+    const uint64_t waves = static_cast<uint64_t>(CeilDiv(rows, 64)) * CeilDiv(n, 128) * 2;
+    const uint32_t tiles = CeilDiv(k, kGemmBK);
+    uint32_t splits = static_cast<uint32_t>(std::min<uint64_t>(kMaxGemmSplits, CeilDiv(1024, waves)));
+    while (splits > 1 && tiles / splits < 2)
+    {
+        --splits;
+    }
+    return std::max(splits, 1u);
+}
+
 hipError_t LaunchGemmSplit(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* w,
                            const float* bias, const float* residual, float* out, uint32_t rows, uint32_t n,
-                           uint32_t k)
+                           uint32_t k, float* partial, uint32_t splits)
 {
-    if (n % 4 != 0 || k % 8 != 0)
+    if (n % 4 != 0 || k % 8 != 0 || splits == 0 || splits > kMaxGemmSplits || (splits > 1 && partial == nullptr))
     {
         return hipErrorInvalidValue;
     }
-    return LaunchGemm(s, ahi, alo, PlainEpi{w, bias, residual, out, n, k}, rows, n, k);
+    PlainEpi epi{w, bias, residual, out, n, k};
+    epi.partial = splits > 1 ? partial : nullptr;
+    return LaunchGemm(s, ahi, alo, epi, rows, n, k, splits);
 }
 
 hipError_t LaunchGemmSwiGlu(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* wgate,
@@ -701,15 +814,17 @@ hipError_t LaunchGemmSwiGlu(hipStream_t s, const uint16_t* ahi, const uint16_t* 
 
 hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads,
                                  uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, const float* ropePow,
-                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache)
+                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache, uint32_t splits,
+                                 const float* bias)
 {
     const uint64_t total = static_cast<uint64_t>(rows) * (heads + 2 * kvHeads) * (headDim / 2);
-    if (total == 0 || pos0 < 0 || static_cast<uint64_t>(pos0) + rows > maxSeq)
+    if (total == 0 || pos0 < 0 || static_cast<uint64_t>(pos0) + rows > maxSeq || splits == 0 ||
+        splits > kMaxGemmSplits || (splits > 1 && bias == nullptr))
     {
         return hipErrorInvalidValue;
     }
     hipLaunchKernelGGL(RopeSplitAppendKernel, dim3(CeilDiv(total, 256)), dim3(256), 0, s, qkv, rows, pos0, heads,
-                       kvHeads, headDim, maxSeq, ropePow, qhi, qlo, kcache, vcache);
+                       kvHeads, headDim, maxSeq, ropePow, qhi, qlo, kcache, vcache, splits, bias);
     return hipGetLastError();
 }
 

@@ -27,11 +27,27 @@ hipError_t LaunchRmsNormSplit(hipStream_t s, const float* x, const float* w, uin
 /// hi/lo planes of a plain f32 matrix (no norm): count values, count % 4 == 0.
 hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_t* hi, uint16_t* lo);
 
+/// Most K splits of a prefill GEMM.
+constexpr uint32_t kMaxGemmSplits = 4;
+
+/// K splits for a GEMM of this shape: more than one when its output tiles alone leave most SIMDs
+/// without a wave (the 0.5B shape's q|k|v, o_proj and down at 2048 rows).
+uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k);
+
 /// out[m][n] = sum_k (ahi + alo)[m][k] * w[n][k] + bias[n] (bias may be null) + residual[m][n]
 /// (residual may be null). A is [rows][k] (two planes), W is [n][k] f16, out is [rows][n] f32.
+/// With splits > 1 the K range is split and each split's raw sums go to plane z of `partial`
+/// ([splits][rows][n]); out, bias and residual are then left to the consumer
+/// (LaunchReduceRmsNormSplit, LaunchRopeSplitAppend).
 hipError_t LaunchGemmSplit(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, const uint16_t* w,
                            const float* bias, const float* residual, float* out, uint32_t rows, uint32_t n,
-                           uint32_t k);
+                           uint32_t k, float* partial = nullptr, uint32_t splits = 1);
+
+/// x = residual + the sum of a split GEMM's planes (split order), stored; then, with w, its rows'
+/// rms_norm as f16 hi/lo planes as LaunchRmsNormSplit.
+hipError_t LaunchReduceRmsNormSplit(hipStream_t s, const float* residual, const float* partial, uint32_t splits,
+                                    float* x, const float* w, uint32_t rows, uint32_t cols, float eps, uint16_t* hi,
+                                    uint16_t* lo);
 
 /// h[m][f] = silu(g) * u with g = A.gate[f], u = A.up[f] (same split product), written as f16
 /// hi/lo planes [rows][ffn].
@@ -42,9 +58,11 @@ hipError_t LaunchGemmSwiGlu(hipStream_t s, const uint16_t* ahi, const uint16_t* 
 /// From the QKV projection rows [rows][(heads + 2 kvHeads) * headDim] (bias included): rope_neox
 /// on q and k at positions pos0 + m, q as hi/lo planes [rows][heads * headDim], k and v appended
 /// to the fp16 caches [kvHeads][maxSeq][headDim] at rows pos0 + m.
+/// With splits > 1, qkv is a split GEMM's partial planes and bias its bias.
 hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows, int32_t pos0, uint32_t heads,
                                  uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, const float* ropePow,
-                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache);
+                                 uint16_t* qhi, uint16_t* qlo, uint16_t* kcache, uint16_t* vcache,
+                                 uint32_t splits = 1, const float* bias = nullptr);
 
 /// Causal attention of the queries at positions pos0 + m (m < rows) over cache rows 0..pos0 + m:
 /// out[m][h * headDim + c] as hi/lo planes [rows][heads * headDim].
