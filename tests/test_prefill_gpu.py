@@ -367,7 +367,7 @@ def test_decoder_prefill_05b_prompt_then_greedy(mh, gpu, orc, capsys):
     margins = []
     for i, t in enumerate(tokens):
         want, _, (top1, top2) = model.step(int(t), i)
-    margins.append(top1 - top2)
+        margins.append(top1 - top2)
     rest, more = model.greedy(want, 96, 16)
     with capsys.disabled():
         print(f"\n[0.5b prefill 96] next {nxt} ids {ids[:6]}... min margin {min(margins + more):.3g}")
