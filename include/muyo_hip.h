@@ -342,6 +342,37 @@ int muyo_gguf_qwen2_config(const MuyoGguf* gguf, uint32_t max_seq, MuyoQwen2Conf
 int muyo_decoder_load_gguf(MuyoDecoder* decoder, const MuyoGguf* gguf);
 
 /* ---------------------------------------------------------------------------------------------
+ * Tokenizer. Replaces the reference's muyo_llm::Tokenizer (src/Tokenizer.h:22-88,
+ * src/Tokenizer.cpp:89-345): GPT-2/Qwen2 byte-level BPE built from a GGUF file's
+ * tokenizer.ggml.tokens, .merges, .token_type and .pre. Host code; no device is needed.
+ *
+ * muyo_tokenizer_create is Tokenizer(const GgufReader&) (MUYO_E_CONTRACT when the file has no
+ * tokens array); the tokenizer keeps no reference to the file. muyo_tokenizer_encode is
+ * Encode(text, parse_special): CONTROL/USER_DEFINED tokens are matched as units first when
+ * parse_special is nonzero, the text between them is split by Qwen2's pattern (pre "qwen2",
+ * "stablelm2", "hunyuan", "solar-open") or GPT-2's (any other) and merged by rank. It sets *count to
+ * the number of ids and writes them when they fit in `capacity` (else MUYO_E_RANGE; 3 ids per
+ * byte of text always fit); a code point above U+10FFFF in the text is MUYO_E_RANGE, as the
+ * reference throws on one. muyo_tokenizer_decode is Decode (ids out of range are skipped),
+ * muyo_tokenizer_token_bytes is TokenBytes, both reporting the byte length in *length and
+ * copying when it fits. muyo_tokenizer_token_text is TokenFor ("" out of range, valid until
+ * destroy), muyo_tokenizer_is_special IsSpecial, muyo_tokenizer_vocab_size VocabSize.
+ * ------------------------------------------------------------------------------------------- */
+typedef struct MuyoTokenizer MuyoTokenizer;
+
+int muyo_tokenizer_create(const MuyoGguf* gguf, MuyoTokenizer** out);
+void muyo_tokenizer_destroy(MuyoTokenizer* tokenizer);
+uint64_t muyo_tokenizer_vocab_size(const MuyoTokenizer* tokenizer);
+const char* muyo_tokenizer_token_text(const MuyoTokenizer* tokenizer, uint64_t id);
+int muyo_tokenizer_is_special(const MuyoTokenizer* tokenizer, int32_t id);
+int muyo_tokenizer_encode(const MuyoTokenizer* tokenizer, const char* text, uint64_t length, int parse_special,
+                          int32_t* ids, uint64_t capacity, uint64_t* count);
+int muyo_tokenizer_decode(const MuyoTokenizer* tokenizer, const int32_t* ids, uint64_t n, char* text,
+                          uint64_t capacity, uint64_t* length);
+int muyo_tokenizer_token_bytes(const MuyoTokenizer* tokenizer, int32_t id, char* bytes, uint64_t capacity,
+                               uint64_t* length);
+
+/* ---------------------------------------------------------------------------------------------
  * Batched prefill. The reference feeds a prompt one token at a time, a full decode step per
  * token (feedToken inside runTurn, src/FullModel.cpp:1096-1108,1162-1170), and names batched
  * prefill with mul_mm and flash_attn as deferred work (docs/Plan.md:277, README.md:120-121,

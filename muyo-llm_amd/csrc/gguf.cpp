@@ -487,6 +487,43 @@ extern "C" const char* muyo_gguf_string_array_at(MuyoGguf* g, const char* key, u
     return c.ok ? g->scratch.c_str() : nullptr;
 }
 
+namespace muyo
+{
+bool GgufStringArray(const MuyoGguf* g, const char* key, std::vector<std::string>& out)
+{
+    const ValueRef* v = g != nullptr && key != nullptr ? g->Find(key) : nullptr;
+    out.clear();
+    if (v == nullptr || v->type != kArray || v->elementType != kString)
+    {
+        return false;
+    }
+    // One walk over the elements (the parse already checked that they fit the file).
+    Cursor c{g->map, g->size, v->at};
+    out.reserve(static_cast<size_t>(v->count));
+    for (uint64_t i = 0; i < v->count && c.ok; ++i)
+    {
+        out.push_back(c.String());
+    }
+    return c.ok;
+}
+
+bool GgufInt32Array(const MuyoGguf* g, const char* key, std::vector<int32_t>& out)
+{
+    const ValueRef* v = g != nullptr && key != nullptr ? g->Find(key) : nullptr;
+    out.clear();
+    if (v == nullptr || v->type != kArray || v->elementType != kI32)
+    {
+        return false;
+    }
+    out.resize(static_cast<size_t>(v->count));
+    if (!out.empty())
+    {
+        std::memcpy(out.data(), g->map + v->at, out.size() * sizeof(int32_t));
+    }
+    return true;
+}
+}  // namespace muyo
+
 extern "C" int muyo_gguf_tensor_data(const MuyoGguf* g, const char* name, const void** data, uint64_t* bytes)
 {
     if (g == nullptr || name == nullptr || data == nullptr || bytes == nullptr)

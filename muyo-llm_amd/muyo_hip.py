@@ -197,6 +197,16 @@ _SIGNATURES = {
     "muyo_gemm_swiglu_split_f16": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, u32, vp]),
     "muyo_rope_split_append_f16kv": (ctypes.c_int, [vp, u32, i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp]),
     "muyo_prefill_attention_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, i32, u32, u32, u32, u32, f32, vp]),
+    "muyo_tokenizer_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
+    "muyo_tokenizer_destroy": (None, [vp]),
+    "muyo_tokenizer_vocab_size": (ctypes.c_uint64, [vp]),
+    "muyo_tokenizer_token_text": (ctypes.c_char_p, [vp, ctypes.c_uint64]),
+    "muyo_tokenizer_is_special": (ctypes.c_int, [vp, i32]),
+    "muyo_tokenizer_encode": (ctypes.c_int, [vp, ctypes.c_char_p, ctypes.c_uint64, ctypes.c_int, vp, ctypes.c_uint64,
+                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "muyo_tokenizer_decode": (ctypes.c_int, [vp, vp, ctypes.c_uint64, vp, ctypes.c_uint64,
+                                             ctypes.POINTER(ctypes.c_uint64)]),
+    "muyo_tokenizer_token_bytes": (ctypes.c_int, [vp, i32, vp, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]),
     "muyo_fill_normal_f16": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_normal_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, vp]),
     "muyo_fill_uniform_f32": (ctypes.c_int, [vp, ctypes.c_uint64, ctypes.c_uint64, vp]),
@@ -499,6 +509,86 @@ class Gguf:
         c = MuyoQwen2Config()
         check(self.lib.muyo_gguf_qwen2_config(self.handle, max_seq, ref(c)))
         return c
+
+
+class Tokenizer:
+    """Owner of a MuyoTokenizer (muyo_tokenizer_* in include/muyo_hip.h), with the reference's
+    Tokenizer methods (src/Tokenizer.h:22-88). Host code: no device is needed."""
+
+    def __init__(self, gguf: Gguf):
+        self.lib = load()
+        handle = vp()
+        check(self.lib.muyo_tokenizer_create(gguf.handle, ctypes.byref(handle)))
+        self.handle = handle
+
+    def close(self):
+        if self.handle:
+            self.lib.muyo_tokenizer_destroy(self.handle)
+            self.handle = vp()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def vocab_size(self) -> int:
+        return int(self.lib.muyo_tokenizer_vocab_size(self.handle))
+
+    def token_for(self, id: int) -> str:
+        """The vocabulary string of `id` ("" out of range), as UTF-8 text."""
+        return self.lib.muyo_tokenizer_token_text(self.handle, id).decode("utf-8", "surrogateescape")
+
+    def is_special(self, id: int) -> bool:
+        return bool(self.lib.muyo_tokenizer_is_special(self.handle, id))
+
+    def encode(self, text: str | bytes, parse_special: bool = True) -> list[int]:
+        data = text.encode("utf-8", "surrogateescape") if isinstance(text, str) else bytes(text)
+        cap = 3 * len(data) + 1
+        ids, n = (i32 * cap)(), ctypes.c_uint64()
+        check(self.lib.muyo_tokenizer_encode(self.handle, data, len(data), int(parse_special), ids, cap,
+                                             ctypes.byref(n)))
+        return list(ids[:n.value])
+
+    def _text(self, call) -> bytes:
+        """Bytes from a call(buffer, capacity, &length) entry point, growing the buffer once when
+        the first one is too small."""
+        n = ctypes.c_uint64()
+        cap = 256
+        while True:
+            buf = ctypes.create_string_buffer(cap)
+            status = call(buf, cap, ctypes.byref(n))
+            if status == MUYO_OK:
+                return buf.raw[:n.value]
+            if n.value <= cap:
+                check(status)
+            cap = int(n.value)
+
+    def decode_bytes(self, ids) -> bytes:
+        arr = (i32 * max(1, len(ids)))(*ids)
+        return self._text(lambda buf, cap, n: self.lib.muyo_tokenizer_decode(self.handle, arr, len(ids), buf, cap, n))
+
+    def decode(self, ids) -> str:
+        return self.decode_bytes(ids).decode("utf-8", "replace")
+
+    def token_bytes(self, id: int) -> bytes:
+        return self._text(lambda buf, cap, n: self.lib.muyo_tokenizer_token_bytes(self.handle, id, buf, cap, n))
+
+
+# Qwen2.5's ChatML framing (the reference's src/ChatTemplate.h:9-29, src/ChatTemplate.cpp).
+QWEN2_DEFAULT_SYSTEM = "You are Qwen, created by Alibaba Cloud. You are a helpful assistant."
+
+
+def qwen2_system_start(system: str) -> str:
+    return "<|im_start|>system\n" + system + "<|im_end|>\n"
+
+
+def qwen2_user_turn(user: str) -> str:
+    return "<|im_start|>user\n" + user + "<|im_end|>\n<|im_start|>assistant\n"
+
+
+def qwen2_chat_start(system: str, user: str) -> str:
+    return qwen2_system_start(system) + qwen2_user_turn(user)
 
 
 class Decoder:

@@ -58,9 +58,31 @@ def write(path, metadata, tensors, version: int = 3, alignment: int = 32) -> int
     return start
 
 
-def qwen2_file(path, model, alignment: int = 32, order: str = "reference") -> None:
+def tokenizer_metadata(vocab: dict, pre: str = "qwen2", bos: int | None = None, eos: int | None = None) -> list:
+    """tokenizer.ggml.* entries for a vocabulary dict with "tokens", "merges" and "token_type" (as in
+    tests/golden/bpe_vocab.json)."""
+    meta = [("tokenizer.ggml.model", STRING, "gpt2"),
+            ("tokenizer.ggml.pre", STRING, pre),
+            ("tokenizer.ggml.tokens", ARRAY, (STRING, vocab["tokens"])),
+            ("tokenizer.ggml.token_type", ARRAY, (I32, vocab["token_type"])),
+            ("tokenizer.ggml.merges", ARRAY, (STRING, vocab["merges"]))]
+    if bos is not None:
+        meta.append(("tokenizer.ggml.bos_token_id", U32, bos))
+    if eos is not None:
+        meta.append(("tokenizer.ggml.eos_token_id", U32, eos))
+    return meta
+
+
+def tokenizer_file(path, vocab: dict, pre: str = "qwen2") -> None:
+    """A GGUF holding only a tokenizer's metadata."""
+    write(path, tokenizer_metadata(vocab, pre), [])
+
+
+def qwen2_file(path, model, alignment: int = 32, order: str = "reference", vocab: dict | None = None) -> None:
     """An oracle.Model's weights as a Qwen2 GGUF (the names of src/FullModel.cpp:582-600): q, k and
-    v split back out of the stacked QKV tensor, output.weight when the model is untied."""
+    v split back out of the stacked QKV tensor, output.weight when the model is untied. With
+    `vocab` (len(vocab["tokens"]) == the model's vocab) the file carries that tokenizer, with
+    <|endoftext|> as BOS and <|im_end|> as EOS, instead of placeholder token strings."""
     m = model
     qdim, kvdim = m.heads * m.head_dim, m.kv_heads * m.head_dim
     meta = [
@@ -72,10 +94,15 @@ def qwen2_file(path, model, alignment: int = 32, order: str = "reference") -> No
         ("qwen2.attention.head_count_kv", U32, m.kv_heads),
         ("qwen2.attention.layer_norm_rms_epsilon", F32, m.eps),
         ("qwen2.rope.freq_base", F32, m.rope_base),
-        ("tokenizer.ggml.tokens", ARRAY, (STRING, [f"t{i}" for i in range(m.vocab)])),
-        ("tokenizer.ggml.bos_token_id", U32, 1),
-        ("tokenizer.ggml.eos_token_id", U32, 2),
     ]
+    if vocab is None:
+        meta += [("tokenizer.ggml.tokens", ARRAY, (STRING, [f"t{i}" for i in range(m.vocab)])),
+                 ("tokenizer.ggml.bos_token_id", U32, 1),
+                 ("tokenizer.ggml.eos_token_id", U32, 2)]
+    else:
+        assert len(vocab["tokens"]) == m.vocab, (len(vocab["tokens"]), m.vocab)
+        meta += tokenizer_metadata(vocab, "qwen2", bos=vocab["tokens"].index("<|endoftext|>"),
+                                   eos=vocab["tokens"].index("<|im_end|>"))
     if alignment != 32:
         meta.append(("general.alignment", U32, alignment))
     t = m.t

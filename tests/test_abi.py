@@ -176,3 +176,43 @@ int Use(float* logits) {
 ''')
     subprocess.run(["/opt/rocm/bin/hipcc", "-std=c++17", "-Wall", "-Werror", "-Wno-unused-command-line-argument",
                     "-fsyntax-only", "-I", str(ROOT / "include"), str(probe)], check=True)
+
+
+def test_tokenizer_and_chat_headers_work_as_the_reference_classes(tmp_path, mh):
+    """include/muyo/Tokenizer.h and include/muyo/ChatTemplate.h (mirrors of src/Tokenizer.h and
+    src/ChatTemplate.h) compile as C++ and, linked to the library, encode the ChatML prompt as the
+    Python binding does and decode it back (the tokenizer is host code: no device)."""
+    import json
+
+    import gguf_writer as gw
+
+    vocab = json.loads((ROOT / "tests" / "golden" / "bpe_vocab.json").read_text(encoding="utf-8"))
+    gguf = tmp_path / "tok.gguf"
+    gw.tokenizer_file(gguf, vocab, "qwen2")
+    probe = tmp_path / "tok.cpp"
+    probe.write_text(r'''
+#include <cstdio>
+#include "muyo/ChatTemplate.h"
+#include "muyo/Tokenizer.h"
+int main(int argc, char** argv) {
+    MuyoGguf* g = nullptr;
+    if (muyo_gguf_open(argv[1], &g) != MUYO_OK) return 3;
+    muyo_llm::hip::Tokenizer tok(g);
+    muyo_gguf_close(g);
+    namespace ct = muyo_llm::hip::chat_template;
+    const std::string text = ct::Qwen2ChatStart(ct::QWEN2_DEFAULT_SYSTEM, "Hi there");
+    const std::vector<int32_t> ids = tok.Encode(text);
+    for (int32_t id : ids) std::printf("%d ", id);
+    std::printf("\n%d %d %zu\n", tok.Decode(ids) == text ? 1 : 0, tok.IsSpecial(ids[0]) ? 1 : 0, tok.VocabSize());
+    try { tok.Encode("\xf4\x90\x80\x80"); } catch (const std::invalid_argument&) { std::printf("threw\n"); }
+    return 0;
+}
+''')
+    exe = tmp_path / "tok"
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Werror", "-I", str(ROOT / "include"), str(probe), "-o", str(exe),
+                    "-L", str(mh.LIB_PATH.parent), "-lmuyo_hip", f"-Wl,-rpath,{mh.LIB_PATH.parent}"], check=True)
+    out = subprocess.run([str(exe), str(gguf)], capture_output=True, text=True, check=True).stdout.splitlines()
+    with mh.Gguf(gguf) as g, mh.Tokenizer(g) as tok:
+        want = tok.encode(mh.qwen2_chat_start(mh.QWEN2_DEFAULT_SYSTEM, "Hi there"))
+    assert [int(x) for x in out[0].split()] == want
+    assert out[1] == f"1 1 {len(vocab['tokens'])}" and out[2] == "threw"
