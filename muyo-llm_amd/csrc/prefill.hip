@@ -260,7 +260,8 @@ struct PlainEpi
         return w + static_cast<uint64_t>(row < n ? row : n - 1) * k;
     }
 
-    __device__ void Finish(const floatx16 (&acc)[2][2], uint32_t n0, uint32_t m0, uint32_t rows) const
+    template <int kNb>
+    __device__ void Finish(const floatx16 (&acc)[kNb][2], uint32_t n0, uint32_t m0, uint32_t rows) const
     {
         const uint32_t lane = threadIdx.x % kWave;
         const uint32_t h = lane / 32;
@@ -273,7 +274,7 @@ struct PlainEpi
                 continue;
             }
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
+            for (int nb = 0; nb < kNb; ++nb)
             {
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
@@ -332,7 +333,9 @@ struct SwiGluEpi
         return (row % 64 < 32 ? gate : up) + offset;
     }
 
-    __device__ void Finish(const floatx16 (&acc)[2][2], uint32_t n0, uint32_t m0, uint32_t rows) const
+    /// Blocks 2p and 2p + 1 of a wave's kNb are the gate and up rows of the same 32 f.
+    template <int kNb>
+    __device__ void Finish(const floatx16 (&acc)[kNb][2], uint32_t n0, uint32_t m0, uint32_t rows) const
     {
         const uint32_t lane = threadIdx.x % kWave;
         const uint32_t h = lane / 32;
@@ -345,35 +348,40 @@ struct SwiGluEpi
                 continue;
             }
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
+            for (int p = 0; p < kNb / 2; ++p)
             {
-                const uint32_t f = n0 / 2 + 8 * g + 4 * h;
-                if (f >= ffn)
-                {
-                    continue;
-                }
-                float a[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
+                for (int g = 0; g < 4; ++g)
                 {
-                    const float gv = acc[0][mb][4 * g + t];
-                    a[t] = gv / (1.0f + expf(-gv)) * acc[1][mb][4 * g + t];
+                    const uint32_t f = (n0 + 64 * p) / 2 + 8 * g + 4 * h;
+                    if (f >= ffn)
+                    {
+                        continue;
+                    }
+                    float a[4];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+                    {
+                        const float gv = acc[2 * p][mb][4 * g + t];
+                        a[t] = gv / (1.0f + expf(-gv)) * acc[2 * p + 1][mb][4 * g + t];
+                    }
+                    StoreSplit4(hhi, hlo, static_cast<uint64_t>(m) * ffn + f, a[0], a[1], a[2], a[3]);
                 }
-                StoreSplit4(hhi, hlo, static_cast<uint64_t>(m) * ffn + f, a[0], a[1], a[2], a[3]);
             }
         }
     }
 };
 
-/// The grid's z splits K into runs of kPerSplit (a multiple of kGemmBK) columns.
-template <int kWm, int kWn, typename Epi>
-__global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
+/// The grid's z splits K into runs of kPerSplit (a multiple of kGemmBK) columns. A wave owns 64
+/// tokens and kNb blocks of 32 weight rows.
+template <int kWm, int kWn, typename Epi, int kNb = 2>
+__global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 ? 2 : 1) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
                                                                      const uint16_t* __restrict__ alo, Epi epi,
                                                                      uint32_t rows, uint32_t k, uint32_t kPerSplit)
 {
     constexpr int kThreads = kWave * kWm * kWn;
     constexpr int kBM = 64 * kWm;
-    constexpr int kBN = 64 * kWn;
+    constexpr int kBN = 32 * kNb * kWn;
     constexpr int kChunks = kGemmBK / 8;  // 16-byte chunks per tile row
     constexpr int kALoads = 2 * kBM * kChunks / kThreads;
     constexpr int kWLoads = kBN * kChunks / kThreads;
@@ -437,13 +445,13 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
     const uint32_t wn = wave % kWn;
     const uint32_t lrow = lane % 32;
     const uint32_t lk = (lane / 32) * 8;
-    const uint16_t* wFrag = lds + (2 * kBM + wn * 64 + lrow) * kGemmStride + lk;
+    const uint16_t* wFrag = lds + (2 * kBM + wn * 32 * kNb + lrow) * kGemmStride + lk;
     const uint16_t* hiFrag = lds + (wm * 64 + lrow) * kGemmStride + lk;
     const uint16_t* loFrag = lds + (kBM + wm * 64 + lrow) * kGemmStride + lk;
 
-    floatx16 acc[2][2];
+    floatx16 acc[kNb][2];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < kNb; ++a)
     {
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -474,33 +482,55 @@ __global__ __launch_bounds__(kWave * kWm * kWn) void GemmSplitKernel(const uint1
 #pragma unroll
         for (int s = 0; s < kGemmBK / 16; ++s)
         {
-            half8 wf[2], xh[2], xl[2];
+            half8 wf[kNb], xh[2], xl[2];
+#pragma unroll
+            for (int b = 0; b < kNb; ++b)
+            {
+                wf[b] = *reinterpret_cast<const half8*>(wFrag + b * 32 * kGemmStride + s * 16);
+            }
 #pragma unroll
             for (int b = 0; b < 2; ++b)
             {
-                wf[b] = *reinterpret_cast<const half8*>(wFrag + b * 32 * kGemmStride + s * 16);
                 xh[b] = *reinterpret_cast<const half8*>(hiFrag + b * 32 * kGemmStride + s * 16);
                 xl[b] = *reinterpret_cast<const half8*>(loFrag + b * 32 * kGemmStride + s * 16);
             }
+            // The hi products of every block, then the lo products, so that independent
+            // matrix-core operations separate two that accumulate into the same block.
 #pragma unroll
-            for (int nb = 0; nb < 2; ++nb)
+            for (int nb = 0; nb < kNb; ++nb)
             {
 #pragma unroll
                 for (int mb = 0; mb < 2; ++mb)
                 {
                     acc[nb][mb] = Mfma(wf[nb], xh[mb], acc[nb][mb]);
+                }
+            }
+#pragma unroll
+            for (int nb = 0; nb < kNb; ++nb)
+            {
+#pragma unroll
+                for (int mb = 0; mb < 2; ++mb)
+                {
                     acc[nb][mb] = Mfma(wf[nb], xl[mb], acc[nb][mb]);
                 }
             }
         }
     }
-    epi.Finish(acc, n0 + wn * 64, m0 + wm * 64, rows);
+    epi.Finish(acc, n0 + wn * 32 * kNb, m0 + wm * 64, rows);
 }
 
 /// 128 x 128 tiles when they alone give two workgroups per CU; 64-token tiles otherwise.
 bool BigTiles(uint32_t rows, uint32_t virtualRows)
 {
     return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128) >= 512;
+}
+
+/// 128-token x 256-row tiles (a wave 64 tokens x 128 rows, two workgroups per CU) when they give
+/// four workgroups per CU or more: an activation fragment read from LDS feeds twice the
+/// matrix-core work. With fewer tiles the last round's imbalance costs more than that gains.
+bool WideTiles(uint32_t rows, uint32_t virtualRows)
+{
+    return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 256) >= 1024;
 }
 
 template <typename Epi>
@@ -512,7 +542,12 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
         return hipErrorInvalidValue;
     }
     const uint32_t kPerSplit = CeilDiv(CeilDiv(k, kGemmBK), splits) * kGemmBK;
-    if (BigTiles(rows, virtualRows))
+    if (WideTiles(rows, virtualRows))
+    {
+        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 4>), dim3(CeilDiv(virtualRows, 256), CeilDiv(rows, 128), splits),
+                           dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
+    }
+    else if (BigTiles(rows, virtualRows))
     {
         hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
