@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <initializer_list>
+#include <type_traits>
 
 #include "common.hpp"
 #include "prefill.hpp"
@@ -374,8 +375,8 @@ struct SwiGluEpi
 
 /// The grid's z splits K into runs of kPerSplit (a multiple of kGemmBK) columns. A wave owns 64
 /// tokens and kNb blocks of 32 weight rows.
-template <int kWm, int kWn, typename Epi, int kNb = 2>
-__global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 ? 2 : 1) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
+template <int kWm, int kWn, typename Epi, int kNb = 2, int kStages = 1>
+__global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1) void GemmSplitKernel(const uint16_t* __restrict__ ahi,
                                                                      const uint16_t* __restrict__ alo, Epi epi,
                                                                      uint32_t rows, uint32_t k, uint32_t kPerSplit)
 {
@@ -423,19 +424,22 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 ? 2 : 1) void GemmSplit
 
     const uint32_t kBegin = blockIdx.z * kPerSplit;
     const uint32_t kEnd = min(k, kBegin + kPerSplit);
-    half8 aReg[kALoads];
-    half8 wReg[kWLoads];
-    auto load = [&](uint32_t k0)
+    // kStages register buffers: the loads of tile t + kStages are issued as tile t's registers
+    // reach LDS, so each load has kStages tiles of matrix-core work to arrive in.
+    half8 aReg[kStages][kALoads];
+    half8 wReg[kStages][kWLoads];
+    auto load = [&](auto buf, uint32_t k0)
     {
+        constexpr int b = decltype(buf)::value;
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
         {
-            aReg[i] = k0 + aCol[i] < kEnd ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
+            aReg[b][i] = k0 + aCol[i] < kEnd ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
         }
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
         {
-            wReg[i] = k0 + wCol[i] < kEnd ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
+            wReg[b][i] = k0 + wCol[i] < kEnd ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
         }
     };
 
@@ -460,24 +464,26 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 ? 2 : 1) void GemmSplit
         }
     }
 
-    load(kBegin);
-    for (uint32_t k0 = kBegin; k0 < kEnd; k0 += kGemmBK)
+    // One tile: its registers to LDS, the refill of the same registers kStages tiles ahead, then
+    // the tile's products.
+    auto tile = [&](auto buf, uint32_t k0)
     {
+        constexpr int b = decltype(buf)::value;
         __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
         {
-            *reinterpret_cast<half8*>(lds + aDst[i]) = aReg[i];
+            *reinterpret_cast<half8*>(lds + aDst[i]) = aReg[b][i];
         }
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
         {
-            *reinterpret_cast<half8*>(lds + wDst[i]) = wReg[i];
+            *reinterpret_cast<half8*>(lds + wDst[i]) = wReg[b][i];
         }
         __syncthreads();
-        if (k0 + kGemmBK < kEnd)
+        if (k0 + kStages * kGemmBK < kEnd)
         {
-            load(k0 + kGemmBK);
+            load(buf, k0 + kStages * kGemmBK);
         }
 #pragma unroll
         for (int s = 0; s < kGemmBK / 16; ++s)
@@ -515,6 +521,22 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 ? 2 : 1) void GemmSplit
                 }
             }
         }
+    };
+
+    using First = std::integral_constant<int, 0>;
+    using Second = std::integral_constant<int, kStages - 1>;
+    load(First{}, kBegin);
+    if (kStages == 2 && kBegin + kGemmBK < kEnd)
+    {
+        load(Second{}, kBegin + kGemmBK);
+    }
+    for (uint32_t k0 = kBegin; k0 < kEnd; k0 += kStages * kGemmBK)
+    {
+        tile(First{}, k0);
+        if (kStages == 2 && k0 + kGemmBK < kEnd)
+        {
+            tile(Second{}, k0 + kGemmBK);
+        }
     }
     epi.Finish(acc, n0 + wn * 32 * kNb, m0 + wm * 64, rows);
 }
@@ -544,17 +566,17 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
     const uint32_t kPerSplit = CeilDiv(CeilDiv(k, kGemmBK), splits) * kGemmBK;
     if (WideTiles(rows, virtualRows))
     {
-        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 4>), dim3(CeilDiv(virtualRows, 256), CeilDiv(rows, 128), splits),
+        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 4, 1>), dim3(CeilDiv(virtualRows, 256), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
     else if (BigTiles(rows, virtualRows))
     {
-        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128), splits),
+        hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 2, 2>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
     else
     {
-        hipLaunchKernelGGL((GemmSplitKernel<1, 2, Epi>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 64), splits),
+        hipLaunchKernelGGL((GemmSplitKernel<1, 2, Epi, 2, 2>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 64), splits),
                            dim3(128), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
     return hipGetLastError();
