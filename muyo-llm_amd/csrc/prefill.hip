@@ -541,10 +541,11 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1
     epi.Finish(acc, n0 + wn * 32 * kNb, m0 + wm * 64, rows);
 }
 
-/// 128 x 128 tiles when they alone give two workgroups per CU; 64-token tiles otherwise.
-bool BigTiles(uint32_t rows, uint32_t virtualRows)
+/// 128 x 128 tiles when they, with the K splits, give two workgroups per CU; 64-token tiles
+/// otherwise.
+bool BigTiles(uint32_t rows, uint32_t virtualRows, uint32_t splits = 1)
 {
-    return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128) >= 512;
+    return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128) * splits >= 512;
 }
 
 /// 128-token x 256-row tiles (a wave 64 tokens x 128 rows, two workgroups per CU) when they give
@@ -569,7 +570,7 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
         hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 4, 1>), dim3(CeilDiv(virtualRows, 256), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
     }
-    else if (BigTiles(rows, virtualRows))
+    else if (BigTiles(rows, virtualRows, splits))
     {
         hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 2, 2>), dim3(CeilDiv(virtualRows, 128), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit);
@@ -832,6 +833,11 @@ uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k)
     if (rows == 0 || n == 0 || BigTiles(rows, n))
     {
         return 1;
+    }
+    // 128 x 128 tiles over two K halves, where that grid fills two workgroups per CU.
+    if (BigTiles(rows, n, 2) && CeilDiv(k, kGemmBK) >= 8)
+    {
+        return 2;
     }
     const uint64_t waves = static_cast<uint64_t>(CeilDiv(rows, 64)) * CeilDiv(n, 128) * 2;
     const uint32_t tiles = CeilDiv(k, kGemmBK);

@@ -400,6 +400,28 @@ def test_decoder_prefill_equals_steps_on_gpu(mh, gpu, orc):
     assert ids_p == ids_s
 
 
+def test_decoder_prefill_7b_width_full_prompt_equals_steps(mh, gpu, orc):
+    """The 7B widths over a full 2048-token prompt, where o_proj and down take 128 x 128 tiles over
+    two K halves and the gate+up 128 x 256 tiles: the same logits, cache rows and next token as
+    2048 of the decoder's own steps."""
+    shape = dict(mh.QWEN25_7B, layers=2)
+    tokens = prompt(orc, 2048, shape["vocab"], 63)
+    with mh.Decoder(mh.qwen2_config(**shape)) as dec:
+        dec.fill_random(64)
+        nxt = dec.prefill(tokens, 0)
+        logits_p = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+        cache_p = download(dec, "VCACHE", 1, np.empty((4, 2048, 128), np.uint16))
+        dec.fill_kv_random(0, 0)
+        for i, t in enumerate(tokens):
+            stepped = dec.step(int(t), i)
+        logits_s = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+        cache_s = download(dec, "VCACHE", 1, np.empty((4, 2048, 128), np.uint16))
+    assert close(logits_p, logits_s, 1e-3) == 0
+    assert nxt == stepped
+    assert np.abs(orc.half_to_float(cache_p) - orc.half_to_float(cache_s)).max() <= 2e-3 * (
+        1 + np.abs(orc.half_to_float(cache_s)).max())
+
+
 def test_decoder_prefill_in_passes(mh, gpu, orc):
     """A prompt longer than one pass (2048 rows) runs in two; the second pass attends to the first
     through the cache."""
