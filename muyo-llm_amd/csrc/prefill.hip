@@ -828,17 +828,24 @@ hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_
 
 uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k)
 {
-    // Waves of the unsplit grid (64 x 64 outputs each); short of ~1024 (a wave per SIMD), K is
-    // split so the grid reaches it, keeping at least two K tiles per split.
-    if (rows == 0 || n == 0 || BigTiles(rows, n))
+    if (rows == 0 || n == 0)
     {
         return 1;
     }
+    const uint64_t bigTiles = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(n, 128);
+    const bool halves = CeilDiv(k, kGemmBK) >= 8;
+    // 128 x 128 tiles alone fill two workgroups per CU: K halves when under four per CU.
+    if (bigTiles >= 512)
+    {
+        return bigTiles < 1024 && halves ? 2 : 1;
+    }
     // 128 x 128 tiles over two K halves, where that grid fills two workgroups per CU.
-    if (BigTiles(rows, n, 2) && CeilDiv(k, kGemmBK) >= 8)
+    if (bigTiles * 2 >= 512 && halves)
     {
         return 2;
     }
+    // 64-token tiles: waves of the unsplit grid (64 x 64 outputs each); short of ~1024 (a wave
+    // per SIMD), K is split so the grid reaches it, keeping at least two K tiles per split.
     const uint64_t waves = static_cast<uint64_t>(CeilDiv(rows, 64)) * CeilDiv(n, 128) * 2;
     const uint32_t tiles = CeilDiv(k, kGemmBK);
     uint32_t splits = static_cast<uint32_t>(std::min<uint64_t>(kMaxGemmSplits, CeilDiv(1024, waves)));
