@@ -159,10 +159,17 @@ int muyo_cpy_f32_f32(const LlamaCopyPushConstants* pc, const float* a, float* d,
  * `position` is a device int32 (the cache row of the current token; keys 0..pos are read).
  * The caller appends k/v of the current token before this call (muyo_rope_append_f16kv).
  * max_seq <= 32768; q and the caches 16-byte aligned.
+ * `workspace` is caller-owned device memory (16-byte aligned) of at least
+ * muyo_attention_decode_f16kv_workspace_bytes(heads, kv_heads, head_dim, max_seq) bytes for the
+ * chunk partials; it needs no clearing. Calls that overlap in time (other streams) need their
+ * own workspaces. The call allocates nothing, so it may be captured into a graph.
  * ------------------------------------------------------------------------------------------- */
+size_t muyo_attention_decode_f16kv_workspace_bytes(uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                                   uint32_t max_seq); /* 0: unsupported shape */
 int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* vcache, float* out,
                                 const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
-                                uint32_t max_seq, float scale, void* stream);
+                                uint32_t max_seq, float scale, void* workspace, uint64_t workspace_bytes,
+                                void* stream);
 
 /* Rope k (NeoX, theta = pos * theta_scale^j) and append k and v of the current token, as fp16,
  * at row `*position` of the [kv_heads][max_seq][head_dim] caches; q is roped into q_out. This

@@ -36,13 +36,7 @@ constexpr int kWaves = kBlock / kWave;
 constexpr uint32_t kMaxLds = 160 * 1024;
 constexpr int kStageVec = 8;           // float4 per thread per staging round at most (rows <= 8192 floats)
 constexpr int kMaxGroup = 8;           // query heads per kv head
-#ifndef MUYO_GEMV_ROUNDS
-#define MUYO_GEMV_ROUNDS 1  // GEMV grid = this many rounds of the workgroups resident on the chip
-#endif
-#ifndef MUYO_DIRECT_THREADS
-#define MUYO_DIRECT_THREADS 64  // workgroup size of the register-direct GEMVs
-#endif
-constexpr int kDirectThreads = MUYO_DIRECT_THREADS;
+constexpr int kDirectThreads = 64;  // workgroup size of the register-direct GEMVs
 constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
 constexpr uint32_t kWideUnits = 2048;  // most units of a short-row GEMV launched a wave per unit
 constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
@@ -880,7 +874,7 @@ uint32_t ResidentBlocks(Kernel kernel, int threads, size_t lds)
     {
         perCu = 1;
     }
-    return CuCount() * static_cast<uint32_t>(perCu) * MUYO_GEMV_ROUNDS;
+    return CuCount() * static_cast<uint32_t>(perCu);
 }
 
 /// Launches `kernel` over `units`, or with shapeOut only reports its grid. The grid
@@ -977,7 +971,6 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
             return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
                 s, units, kSmallUnits, blockCap, lds, cols, stage, epi, shapeOut);
         }
-#ifndef MUYO_NO_COLUMNS
         // Units past one round of resident waves: column quarters with several units per
         // workgroup put the whole matrix in flight at once (rows of 257..512 chunks, where a
         // quarter is two chunks per lane).
@@ -990,7 +983,6 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
                 return status;
             }
         }
-#endif
     }
     return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi>, Stage, Epi>(
         s, units, kUnitsPerBlock, blockCap, lds, cols, stage, epi, shapeOut);
@@ -1697,57 +1689,24 @@ using namespace muyo;
 
 namespace
 {
-struct AttentionScratchOwner
+/// Floats of chunk partials one attention call needs: (max, sum) and head_dim accumulators per
+/// (kv head, chunk, query head of the group).
+size_t AttentionScratchFloats(uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq)
 {
-    DecodeScratch scratch{};
-    size_t floats = 0;
-    int device = -1;
-};
-
-thread_local AttentionScratchOwner g_attentionScratch;
-
-int EnsureAttentionScratch(uint32_t kvHeads, uint32_t chunks, uint32_t group, uint32_t headDim)
-{
-    int device = 0;
-    MUYO_HIP_CHECK(hipGetDevice(&device));
-    AttentionScratchOwner& o = g_attentionScratch;
-    const size_t small = static_cast<size_t>(kvHeads) * chunks * group;
-    const size_t floats = 2 * small + small * headDim;
-    if (o.device == device && o.floats >= floats)
-    {
-        return MUYO_OK;
-    }
-    if (o.scratch.attnMax != nullptr)
-    {
-        (void)hipFree(o.scratch.attnMax);
-        o.scratch = DecodeScratch{};
-        o.floats = 0;
-    }
-    float* base = nullptr;
-    if (hipMalloc(reinterpret_cast<void**>(&base), floats * sizeof(float)) != hipSuccess)
-    {
-        return Fail(MUYO_E_NOMEM, "attention scratch: hipMalloc(%zu) failed", floats * sizeof(float));
-    }
-    o.scratch.attnMax = base;
-    o.scratch.attnSum = base + small;
-    o.scratch.attnAcc = base + 2 * small;
-    o.floats = floats;
-    o.device = device;
-    return MUYO_OK;
+    const size_t slots = static_cast<size_t>(kvHeads) * AttnGridChunks(maxSeq, headDim, kMaxAttnChunks) *
+                         (heads / kvHeads);
+    return slots * (2 + headDim);
 }
-}  // namespace
 
-extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* vcache, float* out,
-                                           const int32_t* position, uint32_t heads, uint32_t kv_heads,
-                                           uint32_t head_dim, uint32_t max_seq, float scale, void* stream)
+int CheckAttentionArgs(const char* name, const float* q, const void* kcache, const void* vcache, const float* out,
+                       const int32_t* position, uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq)
 {
-    const char* name = "attention_decode_f16kv";
     if (q == nullptr || kcache == nullptr || vcache == nullptr || out == nullptr || position == nullptr)
     {
         return Fail(MUYO_E_NULL, "%s: q, caches, out and position are required", name);
     }
-    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > 8 || (head_dim != 64 && head_dim != 128) ||
-        max_seq == 0 || max_seq > kMaxSeq)
+    if (kvHeads == 0 || heads % kvHeads != 0 || heads / kvHeads > kMaxGroup || (headDim != 64 && headDim != 128) ||
+        maxSeq == 0 || maxSeq > kMaxSeq)
     {
         return Fail(MUYO_E_UNSUPPORTED,
                     "%s: needs heads %% kv_heads == 0, group <= 8, head_dim 64 or 128, max_seq <= %u", name,
@@ -1757,25 +1716,68 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
     {
         return Fail(MUYO_E_CONTRACT, "%s: q and the caches must be 16-byte aligned", name);
     }
-    const int status = EnsureAttentionScratch(kv_heads, AttnGridChunks(max_seq, head_dim, kMaxAttnChunks), heads / kv_heads, head_dim);
-    if (status != MUYO_OK)
-    {
-        return status;
-    }
+    return MUYO_OK;
+}
+
+/// Attention chunks + merge with the partials in `base` (AttentionScratchFloats floats). Every
+/// slot is written before it is read (a chunk without keys writes the neutral partial), so the
+/// buffer needs no clearing between calls.
+int RunAttentionDecode(const char* name, const float* q, const void* kcache, const void* vcache, float* out,
+                       const int32_t* position, uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq,
+                       float scale, float* base, void* stream)
+{
+    const size_t slots = AttentionScratchFloats(heads, kvHeads, headDim, maxSeq) / (2 + headDim);
+    DecodeScratch scratch{};
+    scratch.attnMax = base;
+    scratch.attnSum = base + slots;
+    scratch.attnAcc = base + 2 * slots;
     DecodeDims dims{};
     dims.heads = heads;
-    dims.kvHeads = kv_heads;
-    dims.headDim = head_dim;
-    dims.maxSeq = max_seq;
+    dims.kvHeads = kvHeads;
+    dims.headDim = headDim;
+    dims.maxSeq = maxSeq;
     dims.attnScale = scale;
     dims.attnChunks = kMaxAttnChunks;
     hipError_t launched = LaunchAttention(AsStream(stream), dims, q, static_cast<const uint16_t*>(kcache),
-                                          static_cast<const uint16_t*>(vcache), position, g_attentionScratch.scratch);
+                                          static_cast<const uint16_t*>(vcache), position, scratch);
     if (launched == hipSuccess)
     {
-        launched = LaunchAttentionMerge(AsStream(stream), dims, g_attentionScratch.scratch, out);
+        launched = LaunchAttentionMerge(AsStream(stream), dims, scratch, out);
     }
     return launched == hipSuccess ? MUYO_OK : HipStatus(launched, name);
+}
+}  // namespace
+
+extern "C" size_t muyo_attention_decode_f16kv_workspace_bytes(uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                                              uint32_t max_seq)
+{
+    if (kv_heads == 0 || heads % kv_heads != 0 || heads / kv_heads > kMaxGroup || (head_dim != 64 && head_dim != 128) ||
+        max_seq == 0 || max_seq > kMaxSeq)
+    {
+        return 0;
+    }
+    return AttentionScratchFloats(heads, kv_heads, head_dim, max_seq) * sizeof(float);
+}
+
+extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* vcache, float* out,
+                                           const int32_t* position, uint32_t heads, uint32_t kv_heads,
+                                           uint32_t head_dim, uint32_t max_seq, float scale, void* workspace,
+                                           uint64_t workspace_bytes, void* stream)
+{
+    const char* name = "attention_decode_f16kv";
+    const int args = CheckAttentionArgs(name, q, kcache, vcache, out, position, heads, kv_heads, head_dim, max_seq);
+    if (args != MUYO_OK)
+    {
+        return args;
+    }
+    const size_t need = AttentionScratchFloats(heads, kv_heads, head_dim, max_seq) * sizeof(float);
+    if (workspace == nullptr || !Aligned16(workspace) || workspace_bytes < need)
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: needs a 16-byte aligned workspace of %zu bytes (got %llu)", name, need,
+                    static_cast<unsigned long long>(workspace_bytes));
+    }
+    return RunAttentionDecode(name, q, kcache, vcache, out, position, heads, kv_heads, head_dim, max_seq, scale,
+                              static_cast<float*>(workspace), stream);
 }
 
 extern "C" int muyo_rope_append_f16kv(const float* q, const float* k, const float* v, float* q_out, void* kcache,

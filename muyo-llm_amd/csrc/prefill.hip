@@ -679,10 +679,15 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
                 const uint32_t r = c % kAttnKeys;
                 const uint32_t cc = c / kAttnKeys;
                 *reinterpret_cast<half8*>(kTile + r * kKStride + cc * 8) = kReg[i];
+                // Rows past the tile's last query position may hold anything (NaN, inf): their
+                // weight is 0, and 0 * NaN would poison every query of the tile, so they enter
+                // the V tile as zeros. Their scores are masked to -inf by position.
+                const bool live = static_cast<int32_t>(kt * kAttnKeys + r) <= lastPos;
+                const half8 v = live ? vReg[i] : half8{};
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                 {
-                    reinterpret_cast<_Float16*>(vTile)[(cc * 8 + j) * kVStride + r] = vReg[i][j];
+                    reinterpret_cast<_Float16*>(vTile)[(cc * 8 + j) * kVStride + r] = v[j];
                 }
             }
         }

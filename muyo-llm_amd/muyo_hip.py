@@ -23,6 +23,7 @@ u32 = ctypes.c_uint32
 i32 = ctypes.c_int32
 f32 = ctypes.c_float
 vp = ctypes.c_void_p
+u64 = ctypes.c_uint64
 
 
 class LlamaAddPushConstants(ctypes.Structure):
@@ -148,7 +149,8 @@ _SIGNATURES = {
     "muyo_get_rows_f16_f32": (ctypes.c_int, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "muyo_get_rows_f32": (ctypes.c_int, [vp, vp, vp, vp, u32, u32, u32, vp]),
     "muyo_cpy_f32_f32": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, vp]),
-    "muyo_attention_decode_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp]),
+    "muyo_attention_decode_f16kv_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32, u32]),
+    "muyo_attention_decode_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp, u64, vp]),
     "muyo_rope_append_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp]),
     "muyo_decoder_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
     "muyo_decoder_destroy": (None, [vp]),

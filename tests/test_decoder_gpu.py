@@ -153,6 +153,28 @@ def test_decoder_7b_shape_two_layers(mh, gpu, orc):
     assert close(gpu_logits, logits, 1e-3) == 0  # the last step, at cache row 2047
 
 
+@pytest.mark.timeout(900)
+def test_decoder_7b_shape_full_depth(mh, gpu, orc, capsys):
+    """Every layer of the Qwen2.5-7B shape (28 layers, a ~14.3 GB arena with tensors past 4 GiB),
+    two greedy steps at cache rows 2046 and 2047 (the last of a 2048-row cache): ids equal and each
+    step's logits within 1e-3 of the oracle's."""
+    orc.set_threads(16)
+    shape = mh.QWEN25_7B
+    dec, model = make_pair(mh, orc, shape, seed=77, kv_positions=2046, kv_seed=78)
+    token = 4242
+    with dec:
+        for pos in (2046, 2047):
+            got = dec.step(token, pos)
+            gpu_logits = download(dec, "LOGITS", 0, np.empty(shape["vocab"], np.float32))
+            want, logits, (top1, top2) = model.step(token, pos)
+            with capsys.disabled():
+                print(f"\n[7b full depth p={pos}] token {token} -> gpu {got} oracle {want} "
+                      f"worst {worst(gpu_logits, logits):.2e} margin {top1 - top2:.3g}", flush=True)
+            assert close(gpu_logits, logits, 1e-3) == 0, f"p={pos}"
+            assert got == want, f"p={pos}"
+            token = got
+
+
 def test_decoder_rejects_out_of_range(mh, gpu):
     cfg = mh.qwen2_config(**SMALL)
     with mh.Decoder(cfg) as dec:

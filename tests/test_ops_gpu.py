@@ -522,6 +522,13 @@ ATTN_CASES = [("0.5b", 2048, (0, 1, 31, 32, 63, 64, 255, 256, 257, 511, 512, 513
               ("7b", 8192, (5000, 8191))]
 
 
+def attention_workspace(mh, torch, heads, kv, hd, max_seq):
+    """A byte tensor of the size muyo_attention_decode_f16kv asks for (caller-owned partials)."""
+    nbytes = mh.load().muyo_attention_decode_f16kv_workspace_bytes(heads, kv, hd, max_seq)
+    assert nbytes > 0
+    return torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+
+
 @pytest.mark.parametrize("shape,max_seq,positions", ATTN_CASES)
 def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape, max_seq, positions):
     torch = gpu
@@ -543,8 +550,10 @@ def test_rope_append_and_attention_f16kv(mh, gpu, orc, shape, max_seq, positions
         lib = mh.load()
         mh.check(lib.muyo_rope_append_f16kv(qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), qr.data_ptr(), kc.data_ptr(),
                                             vc.data_ptr(), pd.data_ptr(), heads, kv, hd, max_seq, ts, stream(torch)))
+        ws = attention_workspace(mh, torch, heads, kv, hd, max_seq)
         run(mh, torch, lib.muyo_attention_decode_f16kv(qr.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
-                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, stream(torch)))
+                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, ws.data_ptr(),
+                                                       ws.numel(), stream(torch)))
         kbits = host(kc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
         vbits = host(vc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
         # Appended rows: k roped, v as is, rounded to fp16 (bit-exact slots).
@@ -579,14 +588,55 @@ def test_attention_ignores_rows_past_the_position(mh, gpu, orc, shape):
         qd = dev(torch, q)
         pd = dev(torch, np.array([pos], np.int32))
         out = torch.empty_like(qd)
+        ws = attention_workspace(mh, torch, heads, kv, hd, max_seq)
         run(mh, torch, lib.muyo_attention_decode_f16kv(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
-                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, stream(torch)))
+                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, ws.data_ptr(),
+                                                       ws.numel(), stream(torch)))
         kbits = host(kc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
         vbits = host(vc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
         expect = orc.attention_f16kv(q, kbits, vbits, heads, kv, hd, max_seq, pos, scale)
         got = host(out)
         assert np.isfinite(got).all(), f"pos {pos}"
         assert close(got, expect, 1e-3) == 0, f"pos {pos}"
+
+
+def test_attention_workspace_sizes_and_refusals(mh, gpu, orc):
+    """The workspace grows with the cache's chunk count and the group; a short workspace, a null one
+    and unsupported shapes are refused before anything is launched. A small cache and then a
+    larger one through workspaces of their own sizes both match the oracle."""
+    torch = gpu
+    lib = mh.load()
+    small = lib.muyo_attention_decode_f16kv_workspace_bytes(14, 2, 64, 64)
+    large = lib.muyo_attention_decode_f16kv_workspace_bytes(14, 2, 64, 4096)
+    assert 0 < small < large == 2 * 16 * 7 * (2 + 64) * 4
+    assert lib.muyo_attention_decode_f16kv_workspace_bytes(14, 3, 64, 64) == 0
+    assert lib.muyo_attention_decode_f16kv_workspace_bytes(14, 2, 96, 64) == 0
+    heads, kv, hd = 14, 2, 64
+    scale = 1.0 / math.sqrt(hd)
+    for max_seq, pos in ((64, 40), (4096, 3000)):
+        kc = torch.empty(kv * max_seq * hd, dtype=torch.float16, device="cuda")
+        vc = torch.empty_like(kc)
+        mh.check(lib.muyo_fill_normal_f16(kc.data_ptr(), kc.numel(), 61, 0.0, 1.0, stream(torch)))
+        mh.check(lib.muyo_fill_normal_f16(vc.data_ptr(), vc.numel(), 62, 0.0, 1.0, stream(torch)))
+        q = orc.normal_f32(heads * hd, 600 + pos)
+        qd = dev(torch, q)
+        pd = dev(torch, np.array([pos], np.int32))
+        out = torch.empty_like(qd)
+        ws = attention_workspace(mh, torch, heads, kv, hd, max_seq)
+        short = lib.muyo_attention_decode_f16kv(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                                                pd.data_ptr(), heads, kv, hd, max_seq, scale, ws.data_ptr(),
+                                                ws.numel() - 4, stream(torch))
+        assert short == mh.MUYO_E_CONTRACT
+        assert lib.muyo_attention_decode_f16kv(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                                               pd.data_ptr(), heads, kv, hd, max_seq, scale, None, 0,
+                                               stream(torch)) == mh.MUYO_E_CONTRACT
+        run(mh, torch, lib.muyo_attention_decode_f16kv(qd.data_ptr(), kc.data_ptr(), vc.data_ptr(), out.data_ptr(),
+                                                       pd.data_ptr(), heads, kv, hd, max_seq, scale, ws.data_ptr(),
+                                                       ws.numel(), stream(torch)))
+        kbits = host(kc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
+        vbits = host(vc.view(torch.int16)).view(np.uint16).reshape(kv, max_seq, hd)
+        expect = orc.attention_f16kv(q, kbits, vbits, heads, kv, hd, max_seq, pos, scale)
+        assert close(host(out), expect, 1e-3) == 0, f"max_seq {max_seq}"
 
 
 # ------------------------------------------------------------------------------------------------

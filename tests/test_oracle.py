@@ -445,3 +445,72 @@ def test_decode_step_tied_head_and_greedy(orc):
     assert np.linalg.matrix_rank(emb[:10]) == 10
     ids, margins = m.greedy(3, 1, 4)
     assert len(ids) == 4 and all(0 <= i < SMALL["vocab"] for i in ids) and all(g >= 0 for g in margins)
+
+
+def _torch_step(m, token, pos, final_norm=True, head="model"):
+    """Independent float64 whole step for the oracle's decode step: embed, every layer through
+    _torch_layer, output_norm, then the LM head (tools/reference_qwen2.py:160-166;
+    src/FullModel.cpp:955-993: output.weight when the model has one, else the tied embedding).
+
+    `final_norm=False` and `head="embedding"|"output"` plant the mistakes the pin must catch."""
+    emb = m.t[("TOKEN_EMBD", 0)].view(np.float16).astype(np.float64)
+    h = emb[token].copy()
+    for layer in range(m.layers):
+        h = _torch_layer(m, layer, h, pos)
+    ht = torch.from_numpy(np.asarray(h, np.float64))
+    if final_norm:
+        w = torch.from_numpy(m.t[("OUTPUT_NORM", 0)].astype(np.float64))
+        ht = torch.nn.functional.rms_norm(ht, (m.hidden,), w, eps=m.eps)
+    if head == "model":
+        head = "output" if m.untied_output else "embedding"
+    table = m.t[("OUTPUT", 0)] if head == "output" else m.t[("TOKEN_EMBD", 0)]
+    table = torch.from_numpy(table.view(np.float16).astype(np.float64))
+    return torch.nn.functional.linear(ht, table).numpy()
+
+
+def _scaled_model(orc, seed, untied):
+    m = orc.Model(**SMALL, untied_output=untied)
+    m.fill_random(seed)
+    m.fill_kv_random(12, seed + 1)
+    # Larger projections so every layer term, the final norm and the head all move the logits
+    # well past the tolerance.
+    for key, arr in m.t.items():
+        if key[0] in ("ATTN_QKV", "ATTN_OUTPUT", "FFN_GATE", "FFN_UP", "FFN_DOWN", "TOKEN_EMBD", "OUTPUT"):
+            arr[...] = (arr.view(np.float16).astype(np.float32) * 10).astype(np.float16).view(np.uint16)
+    return m
+
+
+@pytest.mark.parametrize("untied", [False, True])
+def test_decode_step_logits_match_torch_float64(orc, untied):
+    """oracle_decode_step's logits against the float64 composition, tied and untied heads; the
+    same comparison must fail with the final norm dropped and with the other head table."""
+    m = _scaled_model(orc, 51 + int(untied), untied)
+    token, pos = 7, 12
+    expect = _torch_step(m, token, pos)
+    no_norm = _torch_step(m, token, pos, final_norm=False)
+    other_head = _torch_step(m, token, pos, head="embedding") if untied else None
+    best, logits, (top1, _) = m.step(token, pos)
+    tol = 1e-4
+    assert worst(logits, expect) < tol
+    assert best == int(np.argmax(expect)) or expect[best] == expect.max()
+    # Teeth: the planted mistakes each move the logits far past the tolerance.
+    assert worst(logits, no_norm) > 100 * tol
+    if other_head is not None:
+        assert worst(logits, other_head) > 100 * tol
+    # The tied model's head is the embedding; a layer norm weight in place of output_norm fails.
+    if not untied:
+        saved = m.t[("OUTPUT_NORM", 0)].copy()
+        m.t[("OUTPUT_NORM", 0)][...] = m.t[("ATTN_NORM", 0)]
+        wrong = _torch_step(m, token, pos)
+        m.t[("OUTPUT_NORM", 0)][...] = saved
+        assert worst(logits, wrong) > 100 * tol
+
+
+def test_decode_step_two_positions_carry_the_cache(orc):
+    """Two consecutive oracle steps: the second attends over the row the first appended, as the
+    float64 composition does when fed the same cache."""
+    m = _scaled_model(orc, 61, False)
+    m.step(5, 12)  # appends row 12 in every layer
+    expect = _torch_step(m, 9, 13)
+    _, logits, _ = m.step(9, 13)
+    assert worst(logits, expect) < 1e-4

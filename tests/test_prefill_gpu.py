@@ -233,10 +233,17 @@ def test_rope_split_append_matches_oracle(mh, gpu, orc, heads, kv_heads, head_di
     assert np.all(np.abs(orc.half_to_float(got_k) - want_f) <= np.abs(want_f) * 2.0 ** -10 + 2.0 ** -24)  # 1 ulp
 
 
-def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed, check=None):
+def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed, check=None,
+                           poison=False):
     q = orc.normal_f32(rows * heads * head_dim, seed).reshape(rows, heads * head_dim)
     kc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 1).reshape(kv_heads, max_seq, head_dim)
     vc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 2).reshape(kv_heads, max_seq, head_dim)
+    if poison:
+        # Cache rows past the last query's position hold NaN and infinity (fp16 bit patterns).
+        last = pos0 + rows - 1
+        kc[:, last + 1:] = 0x7E00
+        vc[:, last + 1:, ::2] = 0x7C00
+        vc[:, last + 1:, 1::2] = 0x7E00
     qhi, qlo = split_np(q)
     ohi, olo = planes(torch, (rows, heads * head_dim))
     scale = 1.0 / math.sqrt(head_dim)
@@ -245,6 +252,7 @@ def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0
                                                           ohi.data_ptr(), olo.data_ptr(), rows, pos0, heads,
                                                           kv_heads, head_dim, max_seq, scale, stream(torch)))
     got = joined(ohi, olo)
+    assert np.isfinite(got).all()
     for m in (range(rows) if check is None else check):
         want = orc.attention_f16kv(q[m], kc, vc, heads, kv_heads, head_dim, max_seq, pos0 + m, scale)
         assert close(got[m], want, 1e-3) == 0, m
@@ -271,6 +279,18 @@ def test_prefill_attention_full_prompt(mh, gpu, orc, heads, kv_heads, head_dim):
     rows = 2048
     check = [0, 1, 31, 32, 33, 500, 1023, 1024, 1537, 2015, 2016, 2046, 2047]
     prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, 0, rows, 7 + heads, check)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rows,pos0,max_seq", [
+    (14, 2, 64, 5, 0, 64),        # one tile, keys 5..31 of it past the last query
+    (14, 2, 64, 33, 30, 128),     # tiles 0..1, the last one mostly past the prompt
+    (28, 4, 128, 40, 1000, 2048), # 7B heads after an earlier prompt
+])
+def test_prefill_attention_ignores_rows_past_the_prompt(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0,
+                                                        max_seq):
+    """The last key tile covers cache rows past the prompt's last position; NaN and infinity there
+    must not reach any query's output (a weight of 0 times NaN is NaN)."""
+    prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, 3 + rows, poison=True)
 
 
 def test_prefill_attention_refusals(mh, gpu):
