@@ -171,6 +171,17 @@ int muyo_attention_decode_f16kv(const float* q, const void* kcache, const void* 
                                 uint32_t max_seq, float scale, void* workspace, uint64_t workspace_bytes,
                                 void* stream);
 
+/* muyo_attention_decode_f16kv without a workspace and without any allocation. It has no
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * graph capture, serving loops that forbid hipMalloc). The chunk partials live in a fixed
+ * 512 KiB device array per GPU, held until the process ends; shapes whose partials
+ * (kv_heads * chunks * (heads / kv_heads) * (head_dim + 2) floats, chunks = min(16,
+ * ceil(max_seq * head_dim / 2048))) exceed it are MUYO_E_UNSUPPORTED. Every call on one GPU
+ * shares that array: calls that overlap in time on one GPU (other streams, other threads) race. */
+int muyo_attention_decode_f16kv_static(const float* q, const void* kcache, const void* vcache, float* out,
+                                       const int32_t* position, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                       uint32_t max_seq, float scale, void* stream);
+
 /* Rope k (NeoX, theta = pos * theta_scale^j) and append k and v of the current token, as fp16,
  * at row `*position` of the [kv_heads][max_seq][head_dim] caches; q is roped into q_out. This
  * is the q rope + k rope + v copy node trio of src/FullModel.cpp:756-795 for an fp16 cache. */

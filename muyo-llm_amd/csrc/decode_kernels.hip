@@ -22,6 +22,7 @@
 // and the next row's batch before the current row's reduction. Work that does not depend on the
 // dot products (the rope angle's cosine and sine) runs while the loads are in flight.
 #include <algorithm>
+#include <mutex>
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
@@ -1778,6 +1779,80 @@ extern "C" int muyo_attention_decode_f16kv(const float* q, const void* kcache, c
     }
     return RunAttentionDecode(name, q, kcache, vcache, out, position, heads, kv_heads, head_dim, max_seq, scale,
                               static_cast<float*>(workspace), stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// The same attention with no allocation and no workspace argument, for callers that cannot
+// allocate (code under graph capture, serving loops that forbid hipMalloc): the chunk partials
+// live in a fixed device array. The array's name is a host-side stand-in; its device address is
+// looked up once per device with hipGetSymbolAddress and only that address reaches the kernels.
+
+constexpr size_t kStaticScratchFloats = 131072;  // 512 KiB per device, held until the process ends
+static __device__ __align__(256) float scratch[kStaticScratchFloats];
+
+namespace
+{
+constexpr int kMaxDevices = 64;
+std::mutex g_scratchMutex;
+float* g_scratchAddress[kMaxDevices] = {};
+
+/// This device's copy of `scratch` (looked up on the first call on the device, with it current).
+int StaticScratch(const char* name, float** out)
+{
+    int device = 0;
+    const hipError_t got = hipGetDevice(&device);
+    if (got != hipSuccess)
+    {
+        return HipStatus(got, name);
+    }
+    if (device < 0 || device >= kMaxDevices)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "%s: device %d is past the %d devices this entry point serves", name, device,
+                    kMaxDevices);
+    }
+    std::lock_guard<std::mutex> lock(g_scratchMutex);
+    if (g_scratchAddress[device] == nullptr)
+    {
+        void* address = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (status != hipSuccess || address == nullptr)
+        {
+            return Fail(status != hipSuccess ? static_cast<int>(status) : MUYO_E_NOMEM,
+                        "%s: hipGetSymbolAddress(scratch) failed: %s", name, hipGetErrorString(status));
+        }
+        g_scratchAddress[device] = static_cast<float*>(address);
+    }
+    *out = g_scratchAddress[device];
+    return MUYO_OK;
+}
+}  // namespace
+
+extern "C" int muyo_attention_decode_f16kv_static(const float* q, const void* kcache, const void* vcache, float* out,
+                                                  const int32_t* position, uint32_t heads, uint32_t kv_heads,
+                                                  uint32_t head_dim, uint32_t max_seq, float scale, void* stream)
+{
+    const char* name = "attention_decode_f16kv_static";
+    const int args = CheckAttentionArgs(name, q, kcache, vcache, out, position, heads, kv_heads, head_dim, max_seq);
+    if (args != MUYO_OK)
+    {
+        return args;
+    }
+    const size_t need = AttentionScratchFloats(heads, kv_heads, head_dim, max_seq);
+    if (need > kStaticScratchFloats)
+    {
+        return Fail(MUYO_E_UNSUPPORTED,
+                    "%s: this shape needs %zu bytes of partials, past the fixed %zu-byte device array "
+                    "(use muyo_attention_decode_f16kv with a workspace)",
+                    name, need * sizeof(float), kStaticScratchFloats * sizeof(float));
+    }
+    float* base = nullptr;
+    const int status = StaticScratch(name, &base);
+    if (status != MUYO_OK)
+    {
+        return status;
+    }
+    return RunAttentionDecode(name, q, kcache, vcache, out, position, heads, kv_heads, head_dim, max_seq, scale, base,
+                              stream);
 }
 
 extern "C" int muyo_rope_append_f16kv(const float* q, const float* k, const float* v, float* q_out, void* kcache,

@@ -151,6 +151,7 @@ _SIGNATURES = {
     "muyo_cpy_f32_f32": (ctypes.c_int, [vp, vp, vp, u32, u32, u32, vp]),
     "muyo_attention_decode_f16kv_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32, u32]),
     "muyo_attention_decode_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp, u64, vp]),
+    "muyo_attention_decode_f16kv_static": (ctypes.c_int, [vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp]),
     "muyo_rope_append_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, u32, u32, u32, u32, f32, vp]),
     "muyo_decoder_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
     "muyo_decoder_destroy": (None, [vp]),
