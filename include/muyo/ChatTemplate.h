@@ -12,22 +12,22 @@ namespace hip
 {
 namespace chat_template
 {
-/// The system prompt Qwen2.5's template falls back to when none is given.
+/// Default system text (Qwen2.5's own template uses it whenever a chat names no system turn).
 inline constexpr char QWEN2_DEFAULT_SYSTEM[] = "You are Qwen, created by Alibaba Cloud. You are a helpful assistant.";
 
-/// "<|im_start|>system\n{system}<|im_end|>\n"
+/// Frames `system` as ChatML's system block, ending on a newline.
 inline std::string Qwen2SystemStart(const std::string& system)
 {
     return "<|im_start|>system\n" + system + "<|im_end|>\n";
 }
 
-/// "<|im_start|>user\n{user}<|im_end|>\n<|im_start|>assistant\n"
+/// Frames `user` as a user block, then opens the assistant block the model continues.
 inline std::string Qwen2UserTurn(const std::string& user)
 {
     return "<|im_start|>user\n" + user + "<|im_end|>\n<|im_start|>assistant\n";
 }
 
-/// The single-turn prompt: the system turn, then the user turn.
+/// A whole first exchange: the system block followed by the user block and the open assistant block.
 inline std::string Qwen2ChatStart(const std::string& system, const std::string& user)
 {
     return Qwen2SystemStart(system) + Qwen2UserTurn(user);

@@ -24,7 +24,7 @@ struct SamplerParams
     int32_t topK = 40;
     float topP = 0.95F;
     float repeatPenalty = 1.0F;
-    int32_t repeatLastN = 64;  ///< History window the penalty looks at; negative means all of it.
+    int32_t repeatLastN = 64;  ///< How many of the latest tokens are penalised (< 0: every token so far).
     uint64_t seed = 0;
 };
 
@@ -65,10 +65,10 @@ public:
         (void)hipFree(m_history);
     }
 
-    /// @param logits  The model's logits for the current position, in device memory. Modified in
-    ///                place by the penalty and the temperature, as the reference's are.
+    /// @param logits  Device pointer to this position's logits; the penalty and the division by
+    ///                the temperature are applied to them in place.
     /// @param vocab   Number of logits (the constructor's).
-    /// @param history Tokens fed and generated so far, newest last; used by the repetition penalty.
+    /// @param history Every token so far (prompt and output), oldest first; the penalty window reads its tail.
     /// @return The sampled token id. Waits for the stream.
     int32_t Sample(float* logits, int32_t vocab, const std::vector<int32_t>& history)
     {
