@@ -8,6 +8,10 @@
 // that changes per token (token id, position, step counter) lives in device memory: the first
 // kernel of a step reduces the previous step's argmax partials into its token and advances the
 // position. Greedy generation therefore needs no host round trip between tokens.
+//
+// Shapes the persistent step supports (persistent.hpp) run instead as one cooperative launch per
+// token that covers every layer and the LM head when muyo_decoder_set_persistent selects it (the
+// graph path stays the default: it is the faster of the two); both compute the same step.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -15,6 +19,7 @@
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
+#include "persistent.hpp"
 #include "prefill.hpp"
 #include "sampler.hpp"
 
@@ -115,6 +120,16 @@ struct MuyoDecoder
     bool warm = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+
+    // The persistent step (persistent.hpp): its plan, the transposed FFN_DOWN of every layer
+    // (rebuilt before a step whenever the weights may have changed), the per-layer pointer table,
+    // the hand-off arena and the control words.
+    const char* stepUnsupported = "not set up";
+    bool persistent = false;
+    bool downTDirty = true;
+    StepPlan plan{};
+    std::vector<TensorSlot> downT;
+    uint32_t* stepControl = nullptr;
 
     // Batched prefill (muyo_decoder_prefill): row-major activations of up to prefillRows prompt
     // tokens, allocated on first use. Split planes (hi, lo) feed the matrix cores.
@@ -435,6 +450,45 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
                 place(LayerTensorBytes(c, static_cast<LayerTensor>(t)));
         }
     }
+    int cus = 0;
+    int current = 0;
+    if (hipGetDevice(&current) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, current) != hipSuccess || cus <= 0)
+    {
+        cus = 0;
+    }
+    d->stepUnsupported = StepUnsupported(c.hidden, c.feedForward, c.heads, c.kvHeads, c.headDim,
+                                         static_cast<uint32_t>(cus));
+    if (d->stepUnsupported == nullptr && c.layers > kStepMaxLayers)
+    {
+        d->stepUnsupported = "more than 64 layers";
+    }
+    if (d->stepUnsupported == nullptr && StepResidentPerCu() < 1)
+    {
+        d->stepUnsupported = "the step kernel does not fit a CU";
+    }
+    TensorSlot stepLayers, packets, control;
+    size_t packetCount = 0;
+    if (d->stepUnsupported == nullptr)
+    {
+        // Attention blocks may read a block of rows past the last value cache; then the
+        // transposed down tensors (three rows of slack each), the pointer table, the arena.
+        (void)place(static_cast<size_t>(kStepCacheSlackRows) * c.headDim * 2);
+        d->downT.resize(c.layers);
+        for (uint32_t l = 0; l < c.layers; ++l)
+        {
+            d->downT[l] = place((static_cast<size_t>(c.feedForward) + 3) * c.hidden * 2);
+        }
+        stepLayers = place(static_cast<size_t>(c.layers) * sizeof(StepLayer));
+        d->plan.hidden = c.hidden;
+        d->plan.ffn = c.feedForward;
+        d->plan.heads = c.heads;
+        d->plan.kvHeads = c.kvHeads;
+        d->plan.headDim = c.headDim;
+        packetCount = StepPlanLayout(d->plan, static_cast<uint32_t>(cus));
+        packets = place(packetCount * sizeof(uint64_t));
+        control = place(kStepControlWords * sizeof(uint32_t));
+    }
     const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
     const size_t group = c.heads / c.kvHeads;
     const size_t chunks = AttnGridChunks(c.maxSeq, c.headDim, d->dims.attnChunks);
@@ -524,6 +578,62 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->rng = d->At<Mt64State>(rng);
     d->sampleWorkspace = d->arena + sampleWorkspace.offset;
     d->argBlocks = LmHeadBlocks(d->dims);
+    if (d->stepUnsupported == nullptr)
+    {
+        StepPlan& p = d->plan;
+        p.layers = c.layers;
+        p.vocab = c.vocab;
+        p.maxSeq = c.maxSeq;
+        p.eps = c.rmsEps;
+        p.attnScale = d->dims.attnScale;
+        p.ropePow = d->dims.ropePow;
+        p.layer = d->At<StepLayer>(stepLayers);
+        p.embedding = d->At<uint16_t>(d->tokenEmbd);
+        p.head = d->At<uint16_t>(c.untiedOutput != 0 ? d->output : d->tokenEmbd);
+        p.outputNorm = d->At<float>(d->outputNorm);
+        p.logits = d->At<float>(d->logits);
+        p.state = d->state;
+        p.argValue = d->scratch.argValue;
+        p.argIndex = d->scratch.argIndex;
+        p.sampled = nullptr;
+        p.history = d->scratch.history;
+        p.historyCap = d->scratch.historyCap;
+        p.ids = d->ids;
+        p.idsCap = kIdsCapacity;
+        p.packets = d->At<uint64_t>(packets);
+        p.control = d->At<uint32_t>(control);
+        p.spinLimit = 1u << 20;
+        d->stepControl = p.control;
+        std::vector<StepLayer> table(c.layers);
+        for (uint32_t l = 0; l < c.layers; ++l)
+        {
+            StepLayer& t = table[l];
+            t.attnNorm = d->At<float>(d->Layer(l, kAttnNorm));
+            t.qkv = d->At<uint16_t>(d->Layer(l, kQkv));
+            t.qkvBias = d->At<float>(d->Layer(l, kQkvBias));
+            t.wo = d->At<uint16_t>(d->Layer(l, kOut));
+            t.ffnNorm = d->At<float>(d->Layer(l, kFfnNorm));
+            t.gate = d->At<uint16_t>(d->Layer(l, kGate));
+            t.up = d->At<uint16_t>(d->Layer(l, kUp));
+            t.downT = d->At<uint16_t>(d->downT[l]);
+            t.kcache = d->At<uint16_t>(d->Layer(l, kKCache));
+            t.vcache = d->At<uint16_t>(d->Layer(l, kVCache));
+        }
+        // Hand-off epochs start at 1 (the zeroed arena's packets carry epoch 0).
+        const uint32_t words[kStepControlWords] = {0, 0, 1, 0};
+        hipError_t st = hipMemcpy(d->arena + stepLayers.offset, table.data(), table.size() * sizeof(StepLayer),
+                                  hipMemcpyHostToDevice);
+        if (st == hipSuccess)
+        {
+            st = hipMemcpy(p.control, words, sizeof(words), hipMemcpyHostToDevice);
+        }
+        if (st != hipSuccess)
+        {
+            const int code = HipStatus(st, "decoder_create: persistent step tables");
+            muyo_decoder_destroy(d);
+            return code;
+        }
+    }
     *out = d;
     return MUYO_OK;
 }
@@ -623,6 +733,7 @@ extern "C" int muyo_decoder_tensor(MuyoDecoder* d, uint32_t kind, uint32_t layer
     if (device_ptr != nullptr)
     {
         *device_ptr = d->arena + slot.offset;
+        d->downTDirty = true;  // the caller may write the weights through the pointer
     }
     if (bytes != nullptr)
     {
@@ -646,6 +757,7 @@ extern "C" int muyo_decoder_upload(MuyoDecoder* d, uint32_t kind, uint32_t layer
     }
     MUYO_HIP_CHECK(hipMemcpyAsync(d->arena + slot.offset, host, bytes, hipMemcpyHostToDevice, d->stream));
     MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->downTDirty = true;
     return MUYO_OK;
 }
 
@@ -673,6 +785,7 @@ extern "C" int muyo_decoder_fill_random(MuyoDecoder* d, uint64_t seed)
     {
         return Fail(MUYO_E_NULL, "decoder is NULL");
     }
+    d->downTDirty = true;
     int status = FillTensor(d, d->tokenEmbd, true, muyo_tensor_seed(seed, MUYO_TENSOR_TOKEN_EMBD, 0), 0.0, 0.02);
     if (status == MUYO_OK)
     {
@@ -762,6 +875,77 @@ extern "C" int muyo_decoder_fill_kv_random(MuyoDecoder* d, uint32_t positions, u
     return MUYO_OK;
 }
 
+namespace
+{
+/// The transposed FFN_DOWN copies, rebuilt when the weights may have changed since the last step.
+hipError_t EnsureDownT(MuyoDecoder* d, hipStream_t s)
+{
+    if (!d->downTDirty)
+    {
+        return hipSuccess;
+    }
+    for (uint32_t l = 0; l < d->config.layers; ++l)
+    {
+        const hipError_t st = LaunchTranspose16(s, d->At<uint16_t>(d->Layer(l, kDown)), d->At<uint16_t>(d->downT[l]),
+                                                d->config.hidden, d->config.feedForward);
+        if (st != hipSuccess)
+        {
+            return st;
+        }
+    }
+    d->downTDirty = false;
+    return hipSuccess;
+}
+
+/// `count` persistent steps: one cooperative launch per token (plus the sampler's kernels when
+/// sampling), the argmax partials one per workgroup.
+int GeneratePersistent(MuyoDecoder* d, hipStream_t s, int32_t token, int32_t position, uint32_t count)
+{
+    MUYO_HIP_CHECK(EnsureDownT(d, s));
+    const uint32_t grid = d->plan.grid;
+    d->plan.sampled = d->sampling ? d->sampledToken : nullptr;
+    DecodeScratch scratch = d->scratch;
+    scratch.sampled = d->sampling ? d->sampledToken : nullptr;
+    MUYO_HIP_CHECK(LaunchSetState(s, d->state, scratch, token, position, grid));
+    const MuyoQwen2Config& c = d->config;
+    for (uint32_t i = 0; i < count; ++i)
+    {
+        MUYO_HIP_CHECK(LaunchStep(s, d->plan));
+        if (d->sampling)
+        {
+            MUYO_HIP_CHECK(LaunchSample(s, d->At<float>(d->logits), d->sampleLogits, c.vocab, d->scratch.history,
+                                        &d->state->position, c.maxSeq, d->sample, d->rng,
+                                        SampleWorkspaceAt(d->sampleWorkspace, c.vocab, d->sample), d->sampledToken));
+        }
+    }
+    MUYO_HIP_CHECK(LaunchFinalize(s, d->state, scratch, grid, d->ids, kIdsCapacity));
+    return MUYO_OK;
+}
+
+/// After the stream has drained: a persistent step whose wait gave up reports it (and the
+/// control words are reset so the next call starts clean).
+int StepOutcome(MuyoDecoder* d)
+{
+    if (!d->persistent || d->stepControl == nullptr)
+    {
+        return MUYO_OK;
+    }
+    uint32_t words[2] = {0, 0};
+    MUYO_HIP_CHECK(hipMemcpy(words, d->stepControl, sizeof(words), hipMemcpyDeviceToHost));
+    if (words[kStepError] == 0 && words[kStepAbort] == 0)
+    {
+        return MUYO_OK;
+    }
+    static const uint32_t kClear[2] = {0, 0};
+    MUYO_HIP_CHECK(hipMemcpy(d->stepControl, kClear, sizeof(kClear), hipMemcpyHostToDevice));
+    static const char* const kWaits[] = {"q|k|v", "attention partials", "o_proj output", "down partials",
+                                         "layer output"};
+    const uint32_t which = words[kStepError];
+    return Fail(MUYO_E_STATE, "decoder: a persistent step gave up waiting for the %s hand-off; its output is void",
+                which >= 1 && which <= 5 ? kWaits[which - 1] : "(abandoned)");
+}
+}  // namespace
+
 extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_t position, uint32_t count,
                                            void* stream)
 {
@@ -784,6 +968,10 @@ extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_
         return Fail(MUYO_E_RANGE, "decoder: at most %u steps per call", kIdsCapacity);
     }
     hipStream_t s = AsStream(stream);
+    if (d->persistent)
+    {
+        return GeneratePersistent(d, s, token, position, count);
+    }
     MUYO_HIP_CHECK(LaunchSetState(s, d->state, d->scratch, token, position, d->argBlocks));
     for (uint32_t i = 0; i < count; ++i)
     {
@@ -822,6 +1010,11 @@ extern "C" int muyo_decoder_generate(MuyoDecoder* d, int32_t token, int32_t posi
         return status;
     }
     MUYO_HIP_CHECK(hipStreamSynchronize(AsStream(stream)));
+    const int outcome = StepOutcome(d);
+    if (outcome != MUYO_OK)
+    {
+        return outcome;
+    }
     return ids != nullptr ? muyo_decoder_generated_ids(d, ids, count) : MUYO_OK;
 }
 
@@ -842,7 +1035,7 @@ extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
     {
         return 0;
     }
-    const uint32_t greedy = 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
+    const uint32_t greedy = d->persistent ? 1u : 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
     return greedy + (d->sampling ? SampleLaunches(d->config.vocab, d->sample, true) : 0u);
 }
 
@@ -1192,4 +1385,24 @@ extern "C" int muyo_decoder_prefill(MuyoDecoder* d, const int32_t* tokens, uint3
         *next_token = next;
     }
     return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_set_persistent(MuyoDecoder* d, int on)
+{
+    if (d == nullptr)
+    {
+        return Fail(MUYO_E_NULL, "decoder is NULL");
+    }
+    if (on != 0 && d->stepUnsupported != nullptr)
+    {
+        return Fail(MUYO_E_UNSUPPORTED, "decoder: no persistent step for this shape: %s", d->stepUnsupported);
+    }
+    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    d->persistent = on != 0;
+    return MUYO_OK;
+}
+
+extern "C" int muyo_decoder_persistent(const MuyoDecoder* d)
+{
+    return d != nullptr && d->persistent ? 1 : 0;
 }
