@@ -12,12 +12,16 @@ value = algorithmic HBM bytes of the timed steps / time (GB/s): every weight onc
 rows 0..p read once as fp16, the appended rows written, activations as f32 once per kernel that
 reads or writes them. tok/s is reported beside it.
 
-roofline: the LM-head kernel (rms_norm prologue + 151936 x 896 fp16 GEMV + argmax; the largest
-single launch, 272 MB, bigger than the 256 MB MALL), timed alone with HIP events on its stream.
+roofline: the kernel with the largest share of the step's time, the fused gate/up (rms_norm
+prologue + 2 x 4864 x 896 fp16 GEMV + swiglu; 25.9 % of the step by rocprofv3's kernel trace),
+timed with HIP events on its stream while it rotates over the 24 layers' weights (420 MB, more
+than the 256 MB MALL); its HBM traffic and L2 hit rate come from the counter runs of the same
+kernel inside whole steps.
 
-cpu_baseline: the CPU oracle's decode step (oracle/, a C restatement of the reference's CPU
-path) on one host core, over a bounded sample of steps of the same workload; the same on all
-the process's cores (OpenMP over GEMV rows, at most 16) is reported beside it.
+cpu_baseline: the reference's CPU path for the same workload (oracle/'s f32 step: HostMatVec-
+order f32 sums, gcc -O3) on one host core, the median of 10 single-step timings; the same with
+its row loops over every core the process may use (OpenMP) is reported beside it, with the CPU
+model.
 
 kernels: per-launch figures of the per-op launchers at the batched element-wise/reduction shapes
 and the decode GEMV suite (inputs under 256 MB rotated over >= 512 MB of copies; the launches
@@ -38,11 +42,12 @@ sys.path.insert(0, str(ROOT / "muyo-llm_amd"))
 METRIC = "F16 GEMV+norm HBM GB/s (% of MI355X peak); Qwen2.5-0.5B-shape decode tok/s"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core flop/s of MI355X
-# HBM bytes per LM-head launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by what the
-# counter reads for a 256 MiB device copy (profiles/lm_head_0.5b_pmc.md), and the L2 hit rate
-# (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)) of the same runs.
-LM_HEAD_TRAFFIC_BYTES = 273_033_388
-LM_HEAD_L2_HIT_RATE = 0.031
+# HBM bytes per gate/up launch (0.5B shape) from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by
+# what the counter reads for a 256 MiB device copy, and its L2 hit rate (TCC_HIT_sum /
+# (TCC_HIT_sum + TCC_MISS_sum)), over whole steps launched kernel by kernel
+# (profiles/decode_step_counters_0.5b.md: `--kernel-only step_05b`, `--summarize-counters`).
+GATE_UP_TRAFFIC_BYTES = 17_608_160
+GATE_UP_L2_HIT_RATE = 0.154
 
 
 def step_bytes(c: dict, position: int) -> int:
@@ -68,15 +73,53 @@ def gate_up_bytes(c: dict) -> int:
     return 2 * 2 * c["ffn"] * c["hidden"] + 4 * c["hidden"] * 2 + 4 * c["ffn"]
 
 
-def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
+STEP_KINDS = ("QKV", "ATTENTION", "O_PROJ", "GATE_UP", "DOWN")
+
+
+def kernel_bytes(c: dict, kind: str, position: int) -> int:
+    """Algorithmic HBM bytes of one launch of a decode-step kernel at cache row `position`: weights
+    once as fp16, K/V rows 0..position once as fp16, f32 activations once per kernel touching them.
+    Attention writes per-chunk partials (head_dim + 2 floats per chunk and query head) that the
+    o_proj prologue (q dim <= 1024, 8 chunks) or the merge kernel (16 chunks) reads."""
+    h, f, hd, v = c["hidden"], c["ffn"], c["head_dim"], c["vocab"]
+    q, kv = c["heads"] * hd, c["kv_heads"] * hd
+    merged = q <= 1024
+    chunks = min(8 if merged else 16, -(-c["max_seq"] // (2048 // hd)))
+    partials = 4 * chunks * c["heads"] * (hd + 2)
+    table = {
+        "embed": 8 * 1024 + 2 * h + 4 * h,
+        "qkv": 2 * (q + 2 * kv) * h + 4 * (q + 2 * kv) + 8 * h + 4 * q + 4 * kv,
+        "attention": 4 * kv * (position + 1) + 4 * q + partials,
+        "merge": partials + 4 * q,
+        "o_proj": 2 * h * q + (partials if merged else 4 * q) + 8 * h,
+        "gate_up": 4 * f * h + 8 * h + 4 * f,
+        "down": 2 * h * f + 4 * f + 8 * h,
+        "lm_head": lm_head_bytes(c),
+    }
+    return table[kind]
+
+
+def enqueue_step(dec, shape, stream) -> None:
+    """One decode step launched kernel by kernel (the graph's sequence, enqueued eagerly)."""
+    dec.enqueue_kernel("EMBED", 0, stream)
+    for layer in range(shape["layers"]):
+        for kind in STEP_KINDS:
+            dec.enqueue_kernel(kind, layer, stream)
+    dec.enqueue_kernel("LM_HEAD", 0, stream)
+
+
+def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None, persistent=False):
     """Returns (ms per step, positions timed, decoder launches per step). `sampler`: keyword
-    parameters of the device sampler (greedy when None), with a synthetic prompt as history."""
+    parameters of the device sampler (greedy when None), with a synthetic prompt as history;
+    `persistent`: the one-launch-per-token step instead of the graph-replayed kernels."""
     stream = torch.cuda.current_stream()
     start = max(1, position - steps // 2 - warmup)
     dec = mh.Decoder(mh.qwen2_config(**shape))
     try:
         dec.fill_random(seed)
         dec.fill_kv_random(start, seed + 1)
+        if persistent:
+            dec.set_persistent(True)
         if sampler is not None:
             dec.set_history([(7919 * i) % shape["vocab"] for i in range(start)])
             dec.set_sampler(**sampler)
@@ -322,44 +365,68 @@ def time_ops(mh, torch, reps: int = 10) -> dict:
     return out
 
 
-def cpu_baseline(shape, position, seconds, seed):
-    """The CPU oracle's decode step on one core over a bounded sample (TEST INFRASTRUCTURE path)."""
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(shape, position, samples, seed):
+    """The reference's CPU path for the same workload, timed on this host (TEST INFRASTRUCTURE:
+    oracle/'s oracle_decode_step_f32, built -O3: every projection and the LM head an f32 running
+    sum in column order as src/MatVec.cpp:52-60 HostMatVec writes it, the reference's softmax,
+    rms_norm, swiglu, rope and greedy loops, composed into tools/reference_qwen2.py:100-166's
+    step). (a) one thread, the reference's own configuration; (b) its row loops split over every
+    core sched_getaffinity grants (OpenMP). Each variant: one untimed step, then the median of
+    `samples` single-step timings at consecutive cache rows from `position`."""
+    import statistics
+
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
 
-    cores = min(16, len(os.sched_getaffinity(0)))
-    oracle.set_threads(cores)
+    granted = len(os.sched_getaffinity(0))
+    # The host's share of cores for this process: OMP_NUM_THREADS when the environment sets it.
+    cores = min(granted, int(os.environ.get("OMP_NUM_THREADS", granted) or granted))
     model = oracle.Model(**shape)
     model.fill_random(seed)
     model.fill_kv_random(position, seed + 1)
 
-    def sample(threads):
+    def run(threads, first):
         oracle.set_threads(threads)
-        token, done, t0 = 9707, 0, time.perf_counter()
-        positions = []
-        while True:
-            token, _, _ = model.step(token, position + done)
-            positions.append(position + done)
-            done += 1
-            if time.perf_counter() - t0 >= seconds or position + done >= shape["max_seq"]:
-                break
-        elapsed = time.perf_counter() - t0
-        total = sum(step_bytes(shape, p) for p in positions)
-        return total / elapsed / 1e9, done, elapsed, positions
+        token = 9707 % shape["vocab"]
+        model.step_f32(token, first)
+        times = []
+        for i in range(samples):
+            t0 = time.perf_counter()
+            model.step_f32(token, first + 1 + i)
+            times.append(time.perf_counter() - t0)
+        rows = list(range(first + 1, first + 1 + samples))
+        sec = statistics.median(times)
+        nbytes = statistics.median(step_bytes(shape, r) for r in rows)
+        return sec, nbytes / sec / 1e9, rows
 
-    gbs, done, elapsed, positions = sample(1)
-    omp_gbs, omp_done, omp_elapsed, _ = sample(cores)
+    sec1, gbs1, rows1 = run(1, position)
+    secn, gbsn, rowsn = run(cores, rows1[-1] + 1)
+    model_name = cpu_model()
     return {
-        "value": round(gbs, 3),
+        "value": round(gbs1, 3),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"{done} decode steps of the same 0.5B-shape workload at cache rows {positions[0]}..{positions[-1]} "
-                  f"({elapsed:.1f} s, {done / elapsed:.3f} tok/s, double-accumulating C oracle, -O2, 1 thread)",
-        "tok_per_s": round(done / elapsed, 4),
-        "openmp": {"value": round(omp_gbs, 3), "unit": "GB/s", "cores": cores,
-                   "tok_per_s": round(omp_done / omp_elapsed, 4),
-                   "sample": f"{omp_done} steps from the same rows, GEMV rows split over {cores} OpenMP threads"},
+        "sample": f"median of {samples} single decode steps of the same 0.5B-shape workload at cache rows "
+                  f"{rows1[0]}..{rows1[-1]} ({sec1 * 1e3:.1f} ms a step, {1.0 / sec1:.3f} tok/s): the reference's "
+                  f"CPU path (f32 HostMatVec-order sums), gcc -O3, 1 thread, on {model_name}",
+        "tok_per_s": round(1.0 / sec1, 4),
+        "cpu_model": model_name,
+        "openmp": {"value": round(gbsn, 3), "unit": "GB/s", "cores": cores, "tok_per_s": round(1.0 / secn, 4),
+                   "sample": f"median of {samples} steps at rows {rowsn[0]}..{rowsn[-1]} "
+                             f"({secn * 1e3:.1f} ms a step), row loops over {cores} threads ({granted} cores in the "
+                             f"affinity mask, OMP_NUM_THREADS {os.environ.get('OMP_NUM_THREADS', 'unset')})"},
     }
 
 
@@ -402,11 +469,147 @@ def kernel_only(mh, torch, which: str, launches: int) -> dict:
         e.record(stream)
         torch.cuda.synchronize()
         nbytes = 2 * 4 * n
+    elif which == "persistent_05b":
+        shape = dict(mh.QWEN25_05B)
+        launches = min(launches, 512)
+        dec = mh.Decoder(mh.qwen2_config(**shape))
+        try:
+            dec.fill_random(20261201)
+            dec.fill_kv_random(1024, 20261202)
+            dec.set_persistent(True)
+            dec.generate_async(9707, 1024, 4, stream.cuda_stream)
+            torch.cuda.synchronize()
+            b.record(stream)
+            dec.generate_async(9707, 1028, launches, stream.cuda_stream)
+            e.record(stream)
+            torch.cuda.synchronize()
+        finally:
+            dec.close()
+        nbytes = sum(step_bytes(shape, 1028 + i) for i in range(launches)) // launches
+    elif which in ("step_05b", "step_7b"):
+        shape = dict(mh.QWEN25_05B if which == "step_05b" else mh.QWEN25_7B)
+        position = 1024 if which == "step_05b" else 2040
+        launches = min(launches, shape["max_seq"] - position)
+        dec = mh.Decoder(mh.qwen2_config(**shape))
+        try:
+            dec.fill_random(20261201)
+            dec.fill_kv_random(position, 20261202)
+            dec.set_state(9707, position, stream.cuda_stream)
+            torch.cuda.synchronize()
+            b.record(stream)
+            for _ in range(launches):
+                enqueue_step(dec, shape, stream.cuda_stream)
+            e.record(stream)
+            torch.cuda.synchronize()
+        finally:
+            dec.close()
+        nbytes = sum(step_bytes(shape, position + i) for i in range(launches)) // launches
     else:
         raise ValueError(which)
     ms = b.elapsed_time(e) / launches
     return {"kernel": which, "launches": launches, "avg_ms": round(ms, 5), "bytes_per_launch": nbytes,
             "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
+def step_kind(name: str, previous: str | None) -> str | None:
+    """The decode-step kernel a rocprofv3 kernel name belongs to (None for anything else)."""
+    if "BeginStep" in name:
+        return "embed"
+    if "QkvEpi" in name:
+        return "qkv"
+    if "AttentionChunk" in name:
+        return "attention"
+    if "AttentionMerge" in name:
+        return "merge"
+    if "GateUpEpi" in name:
+        return "gate_up"
+    if "LmHeadEpi" in name:
+        return "lm_head"
+    if "ResidualEpi" in name:
+        return "down" if previous == "gate_up" else "o_proj"
+    return None
+
+
+def summarize_counters(root: pathlib.Path, which: str) -> str:
+    """Per-kernel figures of one decode step from rocprofv3 CSVs: kernel-trace durations,
+    FETCH_SIZE and WRITE_SIZE scaled by what they read for a 256 MiB copy, the L2 hit rate."""
+    import csv
+    from collections import defaultdict
+
+    sys.path.insert(0, str(ROOT / "muyo-llm_amd"))
+    import muyo_hip as mh
+
+    shape = dict(mh.QWEN25_05B if which == "05b" else mh.QWEN25_7B)
+    position = 1024 if which == "05b" else 2040
+
+    def rows(sub: str, suffix: str):
+        files = sorted((root / sub).rglob(f"*{suffix}"))
+        if not files:
+            raise SystemExit(f"no *{suffix} under {root / sub}")
+        with open(files[0], newline="") as fh:
+            return sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
+
+    def classify(records):
+        kinds, previous = {}, None
+        for r in records:
+            k = step_kind(r["Kernel_Name"], previous)
+            if k is not None:
+                kinds[int(r["Dispatch_Id"])] = k
+                previous = k
+        return kinds
+
+    def counter_means(sub: str, names):
+        recs = rows(sub, "counter_collection.csv")
+        kinds = classify(recs)
+        acc = defaultdict(lambda: defaultdict(list))
+        for r in recs:
+            k = kinds.get(int(r["Dispatch_Id"]))
+            if k is not None and r["Counter_Name"] in names:
+                acc[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        return {k: {n: sum(v) / len(v) for n, v in d.items()} for k, d in acc.items()}
+
+    def copy_mean(sub: str, name: str) -> float:
+        vals = [float(r["Counter_Value"]) for r in rows(sub, "counter_collection.csv")
+                if "copyBuffer" in r["Kernel_Name"] and r["Counter_Name"] == name]
+        return sum(vals) / len(vals)
+
+    copy_kib = 2 * 4 * 64 * 1024 * 1024 / 2 / 1024  # 256 MiB read, 256 MiB written
+    fetch_scale = copy_kib / copy_mean("copy_fetch", "FETCH_SIZE")
+    write_scale = copy_kib / copy_mean("copy_write", "WRITE_SIZE")
+
+    trace = rows("trace", "kernel_trace.csv")
+    kinds = classify(trace)
+    durations = defaultdict(list)
+    for r in trace:
+        k = kinds.get(int(r["Dispatch_Id"]))
+        if k is not None:
+            durations[k].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    fetch = counter_means("fetch", {"FETCH_SIZE"})
+    write = counter_means("write", {"WRITE_SIZE"})
+    hits = counter_means("hit", {"TCC_HIT_sum", "TCC_MISS_sum"})
+    steps = len(durations["lm_head"])
+    per_step = {"embed": 1, "qkv": shape["layers"], "attention": shape["layers"], "merge": shape["layers"],
+                "o_proj": shape["layers"], "gate_up": shape["layers"], "down": shape["layers"], "lm_head": 1}
+    lines = [f"fetch scale {fetch_scale:.4f}, write scale {write_scale:.4f} (256 MiB copy); {steps} steps",
+             "",
+             "| kernel | launches/step | avg µs | µs/step | share | algorithmic bytes | counter bytes | "
+             "counter/alg | GB/s (alg) | % of 8 TB/s | L2 hit rate |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    total = sum(per_step[k] * sum(v) / len(v) for k, v in durations.items())
+    for k in ("embed", "qkv", "attention", "merge", "o_proj", "gate_up", "down", "lm_head"):
+        if k not in durations:
+            continue
+        us = sum(durations[k]) / len(durations[k])
+        alg = kernel_bytes(shape, k, position) if k != "embed" else kernel_bytes(shape, k, 0)
+        got = (fetch.get(k, {}).get("FETCH_SIZE", 0.0) * fetch_scale + write.get(k, {}).get("WRITE_SIZE", 0.0)
+               * write_scale) * 1024
+        hit = hits.get(k, {})
+        rate = hit.get("TCC_HIT_sum", 0.0) / max(1.0, hit.get("TCC_HIT_sum", 0.0) + hit.get("TCC_MISS_sum", 0.0))
+        gbs = alg / (us * 1e-6) / 1e9
+        lines.append(f"| {k} | {per_step[k]} | {us:.2f} | {per_step[k] * us:.1f} | {100 * per_step[k] * us / total:.1f} % "
+                     f"| {alg:,} | {got:,.0f} | {got / alg:.3f} | {gbs:,.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} | {rate:.3f} |")
+    lines.append(f"| step (sum of kernels) | | | {total:.1f} | | | | | | | |")
+    return "\n".join(lines)
 
 
 def main() -> int:
@@ -415,17 +618,27 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--position", type=int, default=1024)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-samples", type=int, default=10, help="timed CPU-baseline steps per variant (median)")
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op launcher suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape secondary figure")
-    ap.add_argument("--kernel-only", choices=["lm_head", "copy"],
-                    help="only launch one kernel back to back (for rocprofv3 traces and counters)")
+    ap.add_argument("--no-persistent", action="store_true",
+                    help="skip the persistent-step figure (rocprofv3 does not survive its cooperative launch)")
+    ap.add_argument("--kernel-only", choices=["lm_head", "copy", "step_05b", "step_7b", "persistent_05b"],
+                    help="only launch one kernel back to back, or whole decode steps kernel by kernel "
+                         "(0.5B shape from cache row 1024, 7B shape from row 2040), for rocprofv3")
+    ap.add_argument("--summarize-counters", metavar="DIR",
+                    help="print the per-kernel table of a step's rocprofv3 runs kept under DIR "
+                         "(trace/, fetch/, write/, hit/, copy_fetch/, copy_write/) and exit")
+    ap.add_argument("--shape", choices=["05b", "7b"], default="05b", help="shape for --summarize-counters")
     ap.add_argument("--launches", type=int, default=20, help="launches for --kernel-only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched-prefill figures (2048-token prompts, 0.5B and 7B shapes)")
     args = ap.parse_args()
 
+    if args.summarize_counters:
+        print(summarize_counters(pathlib.Path(args.summarize_counters), args.shape), flush=True)
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); the decode "
@@ -468,6 +681,14 @@ def main() -> int:
         "sampler": sampling, "tok_per_s": round(1000.0 / ms_s, 1), "ms_per_step": round(ms_s, 5),
         "sampler_ms_per_token": round(ms_s - ms, 5), "launches_per_step": launches_s,
     }
+    # The same greedy decode as one cooperative launch per token (the opt-in persistent step).
+    if not args.no_persistent:
+        ms_p, _, launches_p, ids_p = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed,
+                                                 persistent=True)
+        secondary["qwen2.5-0.5b-shape-persistent"] = {
+            "tok_per_s": round(1000.0 / ms_p, 1), "ms_per_step": round(ms_p, 5), "launches_per_step": launches_p,
+            "same_ids_as_graph_path": ids_p == ids,
+        }
     # Batched prefill of a 2048-token prompt, against feeding it one decode step per token (the
     # reference's feedToken loop) at this run's decode rate.
     secondary["qwen2.5-0.5b-shape-prefill"] = prefill_line(mh, torch, shape, 2048, 5, seed, ms)
@@ -508,28 +729,29 @@ def main() -> int:
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "bytes_per_step": total_bytes // args.steps,
         "roofline": {
-            "kernel": "FusedMatVec<16,7,1,true,NormStage,LmHeadEpi,256> (final norm + tied LM head 151936x896 + argmax)",
+            "kernel": "FusedMatVec<16,7,2,true,NormStage,GateUpEpi,64> (ffn_norm + gate/up 2x4864x896 + swiglu)",
             "bound": "hbm",
-            "achieved": round(lm_gbs, 1),
+            "achieved": round(gu_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-            "traffic": LM_HEAD_TRAFFIC_BYTES,
-            "l2_hit_rate": LM_HEAD_L2_HIT_RATE,
-            "launch_ms": round(kern["lm_head_ms"], 5),
-            "bytes_per_launch": lm_head_bytes(shape),
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": GATE_UP_TRAFFIC_BYTES,
+            "l2_hit_rate": GATE_UP_L2_HIT_RATE,
+            "launch_ms": round(kern["gate_up_ms"], 5),
+            "bytes_per_launch": gate_up_bytes(shape),
+            "share_of_step": 0.259,
+            "note": "rotated over the 24 layers' weights (420 MB > MALL)",
         },
         "kernels": {
-            "gate_up_swiglu": {"GB/s": round(gu_gbs, 1), "launch_ms": round(kern["gate_up_ms"], 5),
-                               "bytes_per_launch": gate_up_bytes(shape),
-                               "note": "rotated over the 24 layers' weights (420 MB > MALL)"},
+            "lm_head": {"GB/s": round(lm_gbs, 1), "launch_ms": round(kern["lm_head_ms"], 5),
+                        "bytes_per_launch": lm_head_bytes(shape), "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
             **ops,
         },
         "secondary": secondary,
         "greedy_ids_head": ids[:8],
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(shape, args.position, args.cpu_seconds, seed)
+        line["cpu_baseline"] = cpu_baseline(shape, args.position, max(10, args.cpu_samples), seed)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

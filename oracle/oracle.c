@@ -295,28 +295,31 @@ void oracle_rms_norm_f16w(const float* x, const uint16_t* w, float* y, uint32_t 
     }
 }
 
+static void soft_max_row(const float* in, float* out, uint32_t cols, float scale)
+{
+    float max_scaled = -1e30f;
+    for (uint32_t c = 0; c < cols; ++c)
+    {
+        const float v = in[c] * scale;
+        max_scaled = v > max_scaled ? v : max_scaled;
+    }
+    double sum_exp = 0.0;
+    for (uint32_t c = 0; c < cols; ++c)
+    {
+        sum_exp += expf(in[c] * scale - max_scaled);
+    }
+    for (uint32_t c = 0; c < cols; ++c)
+    {
+        out[c] = (float)(expf(in[c] * scale - max_scaled) / sum_exp);
+    }
+}
+
 void oracle_soft_max(const float* x, float* y, uint32_t rows, uint32_t cols, float scale)
 {
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < (int64_t)rows; ++r)
     {
-        const float* in = x + (uint64_t)r * cols;
-        float* out = y + (uint64_t)r * cols;
-        float max_scaled = -1e30f;
-        for (uint32_t c = 0; c < cols; ++c)
-        {
-            const float v = in[c] * scale;
-            max_scaled = v > max_scaled ? v : max_scaled;
-        }
-        double sum_exp = 0.0;
-        for (uint32_t c = 0; c < cols; ++c)
-        {
-            sum_exp += expf(in[c] * scale - max_scaled);
-        }
-        for (uint32_t c = 0; c < cols; ++c)
-        {
-            out[c] = (float)(expf(in[c] * scale - max_scaled) / sum_exp);
-        }
+        soft_max_row(x + (uint64_t)r * cols, y + (uint64_t)r * cols, cols, scale);
     }
 }
 
@@ -553,5 +556,124 @@ int32_t oracle_decode_step(const OracleQwen2* m, int32_t token, int32_t pos, flo
     free(h);
     free(next);
     free(hn);
+    return best;
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* The reference's CPU path as written: every sum an f32 running sum in index order, as the
+ * host references compute them (src/MatVec.cpp:52-60 HostMatVec for every projection and the LM
+ * head, src/RmsNorm.cpp:194-216, src/SoftMax.cpp:164-191, src/Swiglu.cpp:56, src/Rope.cpp:48-51,
+ * src/Sampler.cpp:32-43), composed into tools/reference_qwen2.py:100-166's step. This is the
+ * timed CPU baseline; the double-accumulating oracle_decode_step above stays the checker. */
+
+static void attention_f32(const float* q, const uint16_t* kcache, const uint16_t* vcache, float* out, uint32_t heads,
+                          uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq, int32_t pos, float scale)
+{
+    const uint32_t group = heads / kv_heads;
+    const uint32_t keys = (uint32_t)pos + 1u;
+#pragma omp parallel for schedule(static)
+    for (int64_t hh = 0; hh < (int64_t)heads; ++hh)
+    {
+        const uint32_t h = (uint32_t)hh;
+        const uint32_t g = h / group;
+        const float* qh = q + (uint64_t)h * head_dim;
+        const uint16_t* kbase = kcache + (uint64_t)g * max_seq * head_dim;
+        const uint16_t* vbase = vcache + (uint64_t)g * max_seq * head_dim;
+        float* scores = (float*)malloc(sizeof(float) * keys);
+        float* probs = (float*)malloc(sizeof(float) * keys);
+        for (uint32_t j = 0; j < keys; ++j)
+        {
+            float dot = 0.0f;
+            for (uint32_t c = 0; c < head_dim; ++c)
+            {
+                dot += qh[c] * g_half_table[kbase[(uint64_t)j * head_dim + c]];
+            }
+            scores[j] = dot;
+        }
+        soft_max_row(scores, probs, keys, scale);
+        for (uint32_t c = 0; c < head_dim; ++c)
+        {
+            float acc = 0.0f;
+            for (uint32_t j = 0; j < keys; ++j)
+            {
+                acc += probs[j] * g_half_table[vbase[(uint64_t)j * head_dim + c]];
+            }
+            out[(uint64_t)h * head_dim + c] = acc;
+        }
+        free(scores);
+        free(probs);
+    }
+}
+
+int32_t oracle_decode_step_f32(const OracleQwen2* m, int32_t token, int32_t pos, float* logits)
+{
+    if (m == NULL || logits == NULL || token < 0 || (uint32_t)token >= m->vocab || pos < 0 ||
+        (uint32_t)pos >= m->max_seq || m->heads % m->kv_heads != 0)
+    {
+        return -1;
+    }
+    ensure_half_table();
+    const uint32_t hd = m->head_dim;
+    const uint32_t qdim = m->heads * hd;
+    const uint32_t kvdim = m->kv_heads * hd;
+    const uint32_t qkv_rows = qdim + 2u * kvdim;
+    const float theta_scale = powf(m->rope_base, -2.0f / (float)hd);
+    const float attn_scale = 1.0f / sqrtf((float)hd);
+    const uint32_t widest = m->ffn > qkv_rows ? m->ffn : qkv_rows;
+    float* h = (float*)malloc(sizeof(float) * m->hidden);
+    float* xn = (float*)malloc(sizeof(float) * m->hidden);
+    float* x1 = (float*)malloc(sizeof(float) * m->hidden);
+    float* o = (float*)malloc(sizeof(float) * m->hidden);
+    float* qkv = (float*)malloc(sizeof(float) * widest);
+    float* qr = (float*)malloc(sizeof(float) * qdim);
+    float* kr = (float*)malloc(sizeof(float) * kvdim);
+    float* attn = (float*)malloc(sizeof(float) * qdim);
+    float* gate = (float*)malloc(sizeof(float) * m->ffn);
+    float* up = (float*)malloc(sizeof(float) * m->ffn);
+
+    oracle_get_rows_f16(m->token_embd, token, h, m->hidden);
+    for (uint32_t l = 0; l < m->layers; ++l)
+    {
+        oracle_rms_norm(h, m->attn_norm[l], xn, 1, m->hidden, m->rms_eps);
+        oracle_mat_vec_f16(m->attn_qkv[l], xn, qkv, qkv_rows, m->hidden, m->hidden);
+        for (uint32_t r = 0; r < qkv_rows; ++r)
+        {
+            qkv[r] += m->attn_qkv_b[l][r];
+        }
+        oracle_rope_neox(qkv, qr, m->heads, hd, hd, pos, theta_scale);
+        oracle_rope_neox(qkv + qdim, kr, m->kv_heads, hd, hd, pos, theta_scale);
+        for (uint32_t g = 0; g < m->kv_heads; ++g)
+        {
+            for (uint32_t c = 0; c < hd; ++c)
+            {
+                const uint64_t slot = ((uint64_t)g * m->max_seq + (uint64_t)pos) * hd + c;
+                m->kcache[l][slot] = oracle_float_to_half(kr[g * hd + c]);
+                m->vcache[l][slot] = oracle_float_to_half(qkv[qdim + kvdim + g * hd + c]);
+            }
+        }
+        attention_f32(qr, m->kcache[l], m->vcache[l], attn, m->heads, m->kv_heads, hd, m->max_seq, pos, attn_scale);
+        oracle_mat_vec_f16(m->attn_out[l], attn, o, m->hidden, qdim, qdim);
+        oracle_add(h, o, x1, m->hidden);
+        oracle_rms_norm(x1, m->ffn_norm[l], xn, 1, m->hidden, m->rms_eps);
+        oracle_mat_vec_f16(m->ffn_gate[l], xn, gate, m->ffn, m->hidden, m->hidden);
+        oracle_mat_vec_f16(m->ffn_up[l], xn, up, m->ffn, m->hidden, m->hidden);
+        oracle_swiglu(gate, up, qkv, m->ffn);
+        oracle_mat_vec_f16(m->ffn_down[l], qkv, o, m->hidden, m->ffn, m->ffn);
+        oracle_add(x1, o, h, m->hidden);
+    }
+    oracle_rms_norm(h, m->output_norm, xn, 1, m->hidden, m->rms_eps);
+    const uint16_t* head = m->output != NULL ? m->output : m->token_embd;
+    oracle_mat_vec_f16(head, xn, logits, m->vocab, m->hidden, m->hidden);
+    const int32_t best = oracle_argmax(logits, m->vocab);
+    free(h);
+    free(xn);
+    free(x1);
+    free(o);
+    free(qkv);
+    free(qr);
+    free(kr);
+    free(attn);
+    free(gate);
+    free(up);
     return best;
 }

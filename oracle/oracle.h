@@ -113,6 +113,11 @@ typedef struct OracleQwen2
  * final norm, LM head (output, or the tied token_embd). Writes `logits` [vocab]; returns the greedy id; top2 (optional)
  * receives the largest two logits. Returns -1 on bad arguments. */
 int32_t oracle_decode_step(const OracleQwen2* m, int32_t token, int32_t pos, float* logits, float* top2);
+/* The same step as the reference's CPU path computes it: every sum an f32 running sum in index
+ * order (HostMatVec for each projection and the LM head, src/MatVec.cpp:52-60), softmax and
+ * rms_norm as src/SoftMax.cpp:164-191 and src/RmsNorm.cpp:194-216. Appends the cache row like
+ * oracle_decode_step. The CPU baseline that bench.py times; not a checker. */
+int32_t oracle_decode_step_f32(const OracleQwen2* m, int32_t token, int32_t pos, float* logits);
 
 /* One transformer layer on an f32 hidden vector (used to check the composition at small
  * shapes): out = layer(x) at cache row pos. Same arithmetic as inside oracle_decode_step. */

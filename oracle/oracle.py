@@ -45,6 +45,7 @@ _SIGNATURES = {
     "oracle_get_rows_f16": (None, [vp, i32, vp, u32]),
     "oracle_attention_f16kv": (None, [vp, vp, vp, vp, u32, u32, u32, u32, i32, f32]),
     "oracle_decode_step": (i32, [vp, i32, i32, vp, vp]),
+    "oracle_decode_step_f32": (i32, [vp, i32, i32, vp]),
     "oracle_decode_layer": (None, [vp, u32, vp, i32, vp]),
     "oracle_sampler_new": (vp, [f32, i32, f32, f32, i32, u64]),
     "oracle_sampler_free": (None, [vp]),
@@ -373,6 +374,15 @@ class Model:
         if best < 0:
             raise ValueError("oracle_decode_step rejected its arguments")
         return best, logits, (float(top2[0]), float(top2[1]))
+
+    def step_f32(self, token: int, pos: int) -> tuple[int, np.ndarray]:
+        """The reference's CPU path (f32 running sums in index order): the timed CPU baseline."""
+        m = self._struct[0] if self._struct else self._build_struct()
+        logits = np.empty(self.vocab, np.float32)
+        best = load().oracle_decode_step_f32(ctypes.byref(m), token, pos, _p(logits))
+        if best < 0:
+            raise ValueError("oracle_decode_step_f32 rejected its arguments")
+        return best, logits
 
     def layer(self, layer: int, x: np.ndarray, pos: int) -> np.ndarray:
         m = self._struct[0] if self._struct else self._build_struct()

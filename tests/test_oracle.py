@@ -514,3 +514,32 @@ def test_decode_step_two_positions_carry_the_cache(orc):
     expect = _torch_step(m, 9, 13)
     _, logits, _ = m.step(9, 13)
     assert worst(logits, expect) < 1e-4
+
+
+@pytest.mark.parametrize("untied", [False, True])
+def test_f32_reference_path_step_matches_float64(orc, untied):
+    """oracle_decode_step_f32 (the reference's CPU path: f32 running sums in index order, the
+    timed CPU baseline) against the float64 composition: logits within f32 summation error, the
+    same greedy id, the same cache rows as the checker's step, and no dependence on the thread
+    count (each sum is one thread's loop). Dropping the final norm moves it far outside."""
+    m = _scaled_model(orc, 71 + int(untied), untied)
+    twin = _scaled_model(orc, 71 + int(untied), untied)
+    token, pos = 11, 12
+    expect = _torch_step(m, token, pos)
+    orc.set_threads(1)
+    best, logits = m.step_f32(token, pos)
+    tol = 1e-3
+    assert worst(logits, expect) < tol
+    assert best == int(np.argmax(logits)) and expect[best] >= np.sort(expect)[-2]
+    assert worst(logits, _torch_step(m, token, pos, final_norm=False)) > 100 * tol
+    twin.step(token, pos)
+    for layer in range(SMALL["layers"]):
+        for kind in ("KCACHE", "VCACHE"):
+            got = orc.half_to_float(m.t[(kind, layer)][:, pos])
+            ref = orc.half_to_float(twin.t[(kind, layer)][:, pos])
+            assert np.max(np.abs(got - ref)) <= 2e-3 * (1 + np.abs(ref).max())
+    orc.set_threads(4)
+    again = _scaled_model(orc, 71 + int(untied), untied)
+    best4, logits4 = again.step_f32(token, pos)
+    orc.set_threads(1)
+    assert best4 == best and np.array_equal(logits4, logits)
