@@ -98,14 +98,18 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
     const bool wrap = p.ncols > p.ne10;
     if (vec && p.ncols <= kRmsCachedFloat4 * 4 * kWave)
     {
-        // The whole row in registers: one batch of loads, the sum, then the scaled row.
+        // The whole row in registers: one batch of loads, the sum, then the scaled row. The row is
+        // read once and written once, so both stream past L2 (non-temporal); chunks past the row
+        // are not requested.
         const uint32_t n4 = p.ncols / 4;
-        const float4* x4 = reinterpret_cast<const float4*>(x);
-        float4 v[kRmsCachedFloat4];
+        const float4v* x4 = reinterpret_cast<const float4v*>(x);
+        const bool weights4 = p.multiply && p.wAligned && !wrap && (bOff & 3u) == 0;
+        float4v v[kRmsCachedFloat4];
 #pragma unroll
         for (int k = 0; k < kRmsCachedFloat4; ++k)
         {
-            v[k] = x4[min(static_cast<uint32_t>(lane + k * kWave), n4 - 1)];
+            const uint32_t i = lane + k * kWave;
+            v[k] = i < n4 ? __builtin_nontemporal_load(x4 + i) : float4v{};
         }
         float sum = 0.0f;
 #pragma unroll
@@ -121,18 +125,17 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
         }
         sum = GroupSum<kWave>(sum);
         const float scale = 1.0f / sqrtf(sum / static_cast<float>(p.ncols) + p.eps);
-        const bool weights4 = p.multiply && p.wAligned && !wrap && (bOff & 3u) == 0;
 #pragma unroll
         for (int k = 0; k < kRmsCachedFloat4; ++k)
         {
             const uint32_t i = lane + k * kWave;
             if (i < n4)
             {
-                float4 o = make_float4(scale * v[k].x, scale * v[k].y, scale * v[k].z, scale * v[k].w);
+                float4v o = {scale * v[k].x, scale * v[k].y, scale * v[k].z, scale * v[k].w};
                 if (weights4)
                 {
                     const float4 g = LoadWeight4<WT>(w, bOff + 4ull * i);
-                    o = make_float4(o.x * g.x, o.y * g.y, o.z * g.z, o.w * g.w);
+                    o = float4v{o.x * g.x, o.y * g.y, o.z * g.z, o.w * g.w};
                 }
                 else if (p.multiply)
                 {
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
                     o.z *= WeightAt<WT>(w, bOff + (4 * i + 2) % p.ne10);
                     o.w *= WeightAt<WT>(w, bOff + (4 * i + 3) % p.ne10);
                 }
-                reinterpret_cast<float4*>(y)[i] = o;
+                __builtin_nontemporal_store(o, reinterpret_cast<float4v*>(y) + i);
             }
         }
         return;
@@ -197,6 +200,75 @@ __global__ __launch_bounds__(kBlock) void RmsNormRows(const float* __restrict__ 
     }
 }
 
+/// The common case, dense rows: flat row f at a + aoff + f * ncols and d + doff + f * ncols, one
+/// weight row (or none), everything 16-byte aligned, ncols % 4 == 0 and ncols <= 4 * 64 * kChunks.
+/// One wave per row, the row held in kChunks 16-byte chunks per lane: the same sums in the same
+/// order as RmsNormRows's cached path, without its per-row index arithmetic and fallbacks.
+template <typename WT, int kChunks, bool kMultiply>
+__global__ __launch_bounds__(kBlock) void RmsNormDense(const float* __restrict__ a, const WT* __restrict__ w,
+                                                       float* __restrict__ d, uint32_t rows, uint32_t ncols,
+                                                       float eps)
+{
+    const uint32_t flat = blockIdx.x * kWaves + threadIdx.x / kWave;
+    if (flat >= rows)
+    {
+        return;  // whole wave exits together
+    }
+    const uint32_t lane = threadIdx.x & (kWave - 1);
+    const uint32_t n4 = ncols / 4;
+    const float4v* x4 = reinterpret_cast<const float4v*>(a + static_cast<uint64_t>(flat) * ncols);
+    float4v* y4 = reinterpret_cast<float4v*>(d + static_cast<uint64_t>(flat) * ncols);
+    float4v v[kChunks];
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k)
+    {
+        const uint32_t i = lane + k * kWave;
+        v[k] = i < n4 ? __builtin_nontemporal_load(x4 + i) : float4v{};
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k)
+    {
+        sum = fmaf(v[k].x, v[k].x, sum);
+        sum = fmaf(v[k].y, v[k].y, sum);
+        sum = fmaf(v[k].z, v[k].z, sum);
+        sum = fmaf(v[k].w, v[k].w, sum);
+    }
+    sum = GroupSum<kWave>(sum);
+    const float scale = 1.0f / sqrtf(sum / static_cast<float>(ncols) + eps);
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k)
+    {
+        const uint32_t i = lane + k * kWave;
+        if (i < n4)
+        {
+            float4v o = {scale * v[k].x, scale * v[k].y, scale * v[k].z, scale * v[k].w};
+            if constexpr (kMultiply)
+            {
+                const float4 g = LoadWeight4<WT>(w, 4ull * i);
+                o = float4v{o.x * g.x, o.y * g.y, o.z * g.z, o.w * g.w};
+            }
+            __builtin_nontemporal_store(o, y4 + i);
+        }
+    }
+}
+
+template <typename WT, int kChunks>
+void LaunchRmsNormDense(bool multiply, const float* a, const WT* w, float* d, uint32_t rows, uint32_t ncols, float eps,
+                        hipStream_t s)
+{
+    if (multiply)
+    {
+        hipLaunchKernelGGL((RmsNormDense<WT, kChunks, true>), dim3(CeilDiv(rows, kWaves)), dim3(kBlock), 0, s, a, w,
+                           d, rows, ncols, eps);
+    }
+    else
+    {
+        hipLaunchKernelGGL((RmsNormDense<WT, kChunks, false>), dim3(CeilDiv(rows, kWaves)), dim3(kBlock), 0, s, a, w,
+                           d, rows, ncols, eps);
+    }
+}
+
 template <typename WT>
 int LaunchRmsNorm(const char* name, const LlamaAddPushConstants* pc, uint32_t doMultiply, const float* a,
                   const WT* b, float* d, uint32_t gx, uint32_t gy, uint32_t gz, void* stream)
@@ -247,6 +319,28 @@ int LaunchRmsNorm(const char* name, const LlamaAddPushConstants* pc, uint32_t do
     p.multiply = doMultiply ? 1u : 0u;
     p.aligned = Aligned16(a) && Aligned16(d) ? 1u : 0u;
     p.wAligned = b != nullptr && Aligned16(b) ? 1u : 0u;
+    // Dense rows (the flat row index is the memory row), one weight row: the streaming kernel.
+    const uint32_t ncols = p.ncols;
+    const bool denseA = (gx == 1 || p.nb01 == ncols) && (gy == 1 || p.nb02 == static_cast<uint64_t>(ncols) * gx) &&
+                        (gz == 1 || p.nb03 == static_cast<uint64_t>(ncols) * gx * gy);
+    const bool oneWeightRow = !doMultiply || (pc->ne11 <= 1 && pc->ne12 <= 1 && pc->ne13 <= 1 && p.ne10 == ncols &&
+                                              p.wAligned && p.boff == 0);
+    if (denseA && oneWeightRow && p.aligned && (ncols & 3u) == 0 && ((p.aoff | p.doff) & 3u) == 0 &&
+        ncols <= 4 * kWave * kRmsCachedFloat4)
+    {
+        const float* aa = a + p.aoff;
+        float* dd = d + p.doff;
+        const hipStream_t s = AsStream(stream);
+        if (ncols <= 4 * kWave * 4)
+        {
+            LaunchRmsNormDense<WT, 4>(doMultiply != 0, aa, b, dd, p.total, ncols, p.eps, s);
+        }
+        else
+        {
+            LaunchRmsNormDense<WT, kRmsCachedFloat4>(doMultiply != 0, aa, b, dd, p.total, ncols, p.eps, s);
+        }
+        return LaunchStatus(name);
+    }
     hipLaunchKernelGGL((RmsNormRows<WT>), dim3(CeilDiv(total, kWaves)), dim3(kBlock), 0, AsStream(stream), a, b, d,
                        p);
     return LaunchStatus(name);

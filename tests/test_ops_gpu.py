@@ -184,6 +184,28 @@ def test_rms_norm_batched_decode_shape(mh, gpu, orc):
     assert close(y, orc.rms_norm(x, w, 1e-6), 1e-5) == 0
 
 
+@pytest.mark.parametrize("rows,cols,half", [(4096, 896, True), (33, 2048, False), (7, 1028, True), (5, 12, False)])
+def test_rms_norm_dense_and_strided_rows_agree(mh, gpu, orc, rows, cols, half):
+    """Dense rows take the streaming kernel; the same rows at a stride of cols + 4 take the general
+    one. Both match the oracle, and each other bit for bit (the same sums in the same order)."""
+    torch = gpu
+    x = orc.normal_f32(rows * cols, SEED + cols).reshape(rows, cols)
+    w = orc.normal_f16(cols, SEED + 1, 1.0, 0.1) if half else orc.normal_f32(cols, SEED + 1, 1.0, 0.1)
+    dense = rms(mh, gpu, x, w, 1e-6, half_weight=half)
+    padded = np.zeros((rows, cols + 4), np.float32)
+    padded[:, :cols] = x
+    xd = dev(torch, padded)
+    wd = dev(torch, w)
+    d = torch.empty(rows * cols, dtype=torch.float32, device="cuda")
+    pc = mh.rows_push_constants(cols, rows, 1e-6)
+    pc.nb01, pc.nb02, pc.nb03 = cols + 4, (cols + 4) * rows, (cols + 4) * rows
+    fn = mh.load().muyo_rms_norm_f32_f16w if half else mh.load().muyo_rms_norm_f32
+    run(mh, torch, fn(mh.ref(pc), 1, xd.data_ptr(), wd.data_ptr(), d.data_ptr(), None, rows, 1, 1, stream(torch)))
+    strided = host(d).reshape(rows, cols)
+    assert np.array_equal(dense, strided)
+    assert close(dense, orc.rms_norm(x, w, 1e-6), 1e-5) == 0
+
+
 def test_rms_norm_broadcast_and_offsets(mh, gpu, orc):
     """Weight shorter than the row (fastmod wrap) and a dispatch over (rows, channels)."""
     torch = gpu
@@ -374,9 +396,34 @@ def test_rope_batched_decode_shape(mh, gpu, orc):
                                                 heads * tokens, 1, 1, stream(torch)))
     got = host(d)
     bad = 0
-    for t in range(0, tokens, 8):
+    for t in range(tokens):  # every token
         bad += close(got[t], orc.rope_neox(x[t], int(pos[t]), pc.thetaScale), 1e-3)
     assert bad == 0
+
+
+@pytest.mark.parametrize("tokens,heads,hd", [(37, 14, 64), (5, 28, 128), (9, 3, 64), (2, 1, 8), (3, 2, 24)])
+def test_rope_streaming_and_general_paths_agree(mh, gpu, orc, tokens, heads, hd):
+    """The launcher streams whole 16-byte-aligned rows four heads at a time (head counts that are
+    no multiple of 4 included) and takes the element-wise kernel otherwise: here a destination
+    offset of one float forces the latter. Both match the oracle on every row and each other bit
+    for bit (they compute every angle with the same code)."""
+    torch = gpu
+    x = orc.normal_f32(tokens * heads * hd, SEED + 40 + hd).reshape(tokens, heads, hd)
+    pos = (np.arange(tokens, dtype=np.int32) * 613 + 7) % 2048
+    xd, pd = dev(torch, x), dev(torch, pos.astype(np.int32))
+    lib = mh.load()
+    fast = torch.empty_like(xd)
+    pc = mh.rope_push_constants(heads, hd, 1e6, tokens=tokens)
+    run(mh, torch, lib.muyo_rope_neox_f32(mh.ref(pc), xd.data_ptr(), pd.data_ptr(), None, fast.data_ptr(), None,
+                                          heads * tokens, 1, 1, stream(torch)))
+    slow = torch.zeros(tokens * heads * hd + 1, dtype=torch.float32, device="cuda")
+    pc1 = mh.rope_push_constants(heads, hd, 1e6, tokens=tokens, destination_offset=1)
+    run(mh, torch, lib.muyo_rope_neox_f32(mh.ref(pc1), xd.data_ptr(), pd.data_ptr(), None, slow.data_ptr(), None,
+                                          heads * tokens, 1, 1, stream(torch)))
+    got, ref = host(fast), host(slow)[1:].reshape(tokens, heads, hd)
+    assert np.array_equal(got, ref)
+    for t in range(tokens):
+        assert close(got[t], orc.rope_neox(x[t], int(pos[t]), pc.thetaScale), 1e-3) == 0, t
 
 
 def test_rope_into_key_cache_row(mh, gpu, orc):
