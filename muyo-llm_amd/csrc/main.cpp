@@ -34,15 +34,16 @@ int main(int argc, char** argv)
         }
         return RunTokenize(argv[2], argv[3]);
     }
+    // --forward checks its flags before it looks for a device.
+    if (std::strcmp(mode, "--forward") == 0)
+    {
+        return RunForward(argc, argv);
+    }
     int devices = 0;
     if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0)
     {
         std::fprintf(stderr, "[fail] no HIP device\n");
         return 1;
-    }
-    if (std::strcmp(mode, "--forward") == 0)
-    {
-        return RunForward(argc, argv);
     }
     std::printf("[muyo_llm] %s, mode %s\n", muyo_version(), mode);
     const int status = muyo_self_test(mode);

@@ -17,7 +17,8 @@ import pathlib
 import struct
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = HERE / "libmuyo_hip.so"
+# MUYO_HIP_LIBRARY names another build of the same library (the sanitizer build, for instance).
+LIB_PATH = pathlib.Path(os.environ.get("MUYO_HIP_LIBRARY") or HERE / "libmuyo_hip.so")
 
 u32 = ctypes.c_uint32
 i32 = ctypes.c_int32

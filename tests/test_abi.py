@@ -2,6 +2,7 @@
 declares, the contract structs have the reference's sizes, and argument errors are reported
 before anything touches a GPU."""
 import ctypes
+import os
 import pathlib
 import re
 import subprocess
@@ -182,6 +183,8 @@ def test_tokenizer_and_chat_headers_work_as_the_reference_classes(tmp_path, mh):
     """include/muyo/Tokenizer.h and include/muyo/ChatTemplate.h (mirrors of src/Tokenizer.h and
     src/ChatTemplate.h) compile as C++ and, linked to the library, encode the ChatML prompt as the
     Python binding does and decode it back (the tokenizer is host code: no device)."""
+    if os.environ.get("MUYO_HIP_LIBRARY"):
+        pytest.skip("links a g++ program against the library; the run over the product build covers it")
     import json
 
     import gguf_writer as gw

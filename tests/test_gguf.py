@@ -196,3 +196,60 @@ def test_refusals(tmp_path, mh):
     # A missing file.
     with pytest.raises(mh.MuyoError):
         mh.Gguf(tmp_path / "absent.gguf")
+
+
+def _exercise(g, keys):
+    """Every read the reader offers on an opened file; refusals are fine, crashes are not."""
+    try:
+        tensors = g.tensors()
+    except UnicodeDecodeError:  # a corrupted name; the table itself was read
+        tensors = []
+    for name, _, _, _ in tensors:
+        try:
+            g.tensor_bytes(name)
+        except Exception as e:  # noqa: BLE001 - any MuyoError is an answer
+            assert e.__class__.__name__ == "MuyoError", e
+    for key in keys:
+        g.uint_or(key, 7)
+        g.float_or(key, 0.5)
+        n = g.string_array_size(key)
+        # Strings come back as the file's bytes; a corrupted one need not be UTF-8.
+        for read in [lambda: g.string_or(key, "x")] + [lambda i=i: g.string_array_at(key, i) for i in range(min(n, 4))]:
+            try:
+                read()
+            except UnicodeDecodeError:
+                pass
+        g.string_array_at(key, n)
+
+
+def test_every_truncation_and_seeded_corruptions(tmp_path, mh):
+    """Every prefix of the header and tables, and 400 seeded corruptions of 1-4 bytes among them:
+    each file is refused with an error or opens and answers every read; none may read out of
+    bounds (tests/test_sanitized_host.py runs this under AddressSanitizer and UBSan)."""
+    import random
+
+    path = tmp_path / "x.gguf"
+    meta, _ = diverse_file(path)
+    good = path.read_bytes()
+    keys = [k for k, _, _ in meta] + ["missing.key"]
+    with mh.Gguf(path) as g:
+        data_offset = g.data_offset
+    for cut in range(data_offset):
+        path.write_bytes(good[:cut])
+        try:
+            with mh.Gguf(path) as g:
+                assert cut >= data_offset - 64, f"a file cut at {cut} of {data_offset} header bytes opened"
+                _exercise(g, keys)
+        except mh.MuyoError:
+            pass
+    rng = random.Random(2026)
+    for _ in range(400):
+        b = bytearray(good)
+        for _ in range(rng.randint(1, 4)):
+            b[rng.randrange(data_offset)] = rng.randrange(256)
+        path.write_bytes(bytes(b))
+        try:
+            with mh.Gguf(path) as g:
+                _exercise(g, keys)
+        except mh.MuyoError:
+            pass

@@ -15,6 +15,7 @@ Pins, in order of strength:
 The vocabulary is tests/golden/bpe_vocab.json (975 tokens trained on a small multilingual corpus).
 """
 import ctypes
+import os
 import sys
 import json
 import pathlib
@@ -304,7 +305,7 @@ def test_cli_tokenize(files, product):
     anchor; no device is needed."""
     import subprocess
 
-    cli = GOLDEN.parent.parent / "muyo-llm_amd" / "muyo_llm"
+    cli = pathlib.Path(os.environ.get("MUYO_LLM_CLI") or GOLDEN.parent.parent / "muyo-llm_amd" / "muyo_llm")
     if not cli.exists():
         pytest.skip("the muyo_llm CLI is not built")
     text = "Hello world! It's <|im_start|>user\n  ok"
