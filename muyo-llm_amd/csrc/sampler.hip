@@ -2,21 +2,23 @@
 // the engine of src/Sampler.h:40-41 (std::mt19937_64, one uniform double per sampled token), so a
 // decoder can pick its next token without reading the logits back.
 //
-//   Penalty : one workgroup; each token of the last-N window counts its occurrences with global
-//             atomics, and one thread per distinct token applies the penalty that many times in a
-//             row (src/Sampler.cpp:12-29 penalises once per occurrence), divides by the
-//             temperature and marks the token done
-//   Scale   : every other logit divided by the temperature (src/Sampler.cpp:44-47); each of 256
-//             workgroups also records the largest key of its slice
+//   Scale   : each of 256 workgroups owns a slice of the vocabulary. It counts in LDS how often
+//             each of its tokens occurs in the last-N window, applies the repetition penalty that
+//             many times in a row (src/Sampler.cpp:12-29 penalises once per occurrence), divides
+//             by the temperature (src/Sampler.cpp:44-47) and records its slice's largest key.
+//             (Slices too long for LDS counts take a separate one-workgroup Penalty kernel with
+//             global counts first.)
 //   Collect : the k-th largest of those 256 maxima is a threshold at least k keys reach, so the
 //             top k lies among the keys at or above it: those (typically a few times k) are
 //             gathered (k <= 256, vocabulary over 4096)
-//   Select  : otherwise, or when over 4096 keys tie at the top: rounds of workgroups that each
-//             sort 2048 keys in LDS (bitonic) and keep their k best, until 4096 remain (launched
-//             every time, they return at once when Collect sufficed)
-//   Final   : one workgroup sorts the candidates, forms the double weights exp(v_i - v_0), cuts
-//             at top-p, draws u from the engine and walks the kept weights to the target
-//             (src/Sampler.cpp:49-98), each sum in the reference's order by a single thread
+//   Select  : without a collection (k > 256): rounds of workgroups that each sort 2048 keys in
+//             LDS (bitonic) and keep their k best, until 4096 remain
+//   Final   : one workgroup orders the candidates (by rank when there are at most 512, else a
+//             bitonic sort; when over 4096 keys tie at the top and overflow the collection, it
+//             selects from the whole vocabulary itself, 4096 keys at a time), forms the double
+//             weights exp(v_i - v_0), cuts at top-p, draws u from the engine and walks the kept
+//             weights to the target (src/Sampler.cpp:49-98). Each sum runs in the reference's
+//             order in a single thread; the divisions run in parallel.
 //
 // The top-k order is (value descending, index ascending): equal values go to the lower index,
 // an order the reference leaves to std::partial_sort. Greedy (temperature <= 0) with a penalty is
@@ -36,6 +38,7 @@ constexpr int kPenaltyThreads = 1024;
 constexpr int kScaleThreads = 256;
 constexpr uint32_t kThresholdBlocks = 256;  // slices whose maxima set the collection threshold
 constexpr uint32_t kMarked = 0xFFFFFFFFu;   // a count word of a token the penalty finished
+constexpr uint32_t kScaleSliceMax = 2048;   // slice length whose penalty counts fit LDS
 
 // std::mt19937_64's parameters ([rand.predef]: mersenne_twister_engine<uint_fast64_t, 64, 312,
 // 156, 31, 0xb5026f5aa96619e9, 29, 0x5555555555555555, 17, 0x71d67fffeda60000, 37,
@@ -221,6 +224,26 @@ __global__ __launch_bounds__(64) void Mt64SeedKernel(Mt64State* state, uint64_t 
     }
 }
 
+/// The last-N window of the history for the penalty (src/Sampler.cpp:12-16).
+struct PenaltyWindow
+{
+    const int32_t* history;
+    const int32_t* position;  // n = *position + 1 when set, at most historyCount
+    uint32_t historyCount;
+    int32_t lastN;
+    float penalty;
+};
+
+/// penalty applied `times` times in a row (src/Sampler.cpp:18-27).
+__device__ __forceinline__ float Penalise(float v, uint32_t times, float penalty)
+{
+    for (uint32_t j = 0; j < times; ++j)
+    {
+        v = v > 0.0f ? v / penalty : v * penalty;
+    }
+    return v;
+}
+
 /// history[0..n) with n = *position + 1 (position set) or historyCount, at most historyCount.
 /// dst[t] = penalty^d(src[t]) for each token t seen d times in the window, divided by the
 /// temperature when `temperature` > 0 (src and dst may be the same buffer), and counts[t] set to
@@ -262,11 +285,7 @@ __global__ __launch_bounds__(kPenaltyThreads) void SamplePenaltyKernel(const flo
             const uint32_t times = atomicExch(&counts[t], kMarked);  // a count for one entry per token
             if (times != 0 && times != kMarked)
             {
-                float v = src[t];
-                for (uint32_t j = 0; j < times; ++j)
-                {
-                    v = v > 0.0f ? v / penalty : v * penalty;
-                }
+                const float v = Penalise(src[t], times, penalty);
                 dst[t] = temperature > 0.0f ? v / temperature : v;
             }
         }
@@ -290,18 +309,44 @@ __device__ __forceinline__ uint64_t BlockMaxKey(uint64_t key, uint64_t* scratch)
     return scratch[0];
 }
 
-/// Workgroup b of kThresholdBlocks owns logits [b * slice, (b + 1) * slice). dst[i] = src[i] /
-/// temperature (a copy when temperature <= 0), except for tokens the penalty marked, whose dst
-/// is final and whose mark is cleared here. With blockMax set, records the slice's largest key
-/// and (workgroup 0) zeroes the collection count.
+/// Workgroup b of kThresholdBlocks owns logits [b * slice, (b + 1) * slice). dst[i] =
+/// penalty^d(src[i]) / temperature, d being the occurrences of token i in the window (counted in
+/// LDS when `penalise`), without the division when temperature <= 0. Tokens
+/// the separate Penalty kernel marked (`counts` set) already hold their final dst; the mark is
+/// cleared here. With blockMax set, records the slice's largest key and (workgroup 0) zeroes the
+/// collection count.
 __global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* src, float* dst, uint32_t vocab,
-                                                                   float temperature, uint32_t* counts,
-                                                                   uint64_t* blockMax, uint32_t* collected)
+                                                                   float temperature, uint32_t* counts, bool penalise,
+                                                                   PenaltyWindow pw, uint64_t* blockMax,
+                                                                   uint32_t* collected)
 {
     __shared__ uint64_t scratch[kScaleThreads];
+    __shared__ uint32_t hits[kScaleSliceMax];
     const uint32_t slice = (vocab + gridDim.x - 1) / gridDim.x;
     const uint32_t begin = blockIdx.x * slice;
     const uint32_t end = min(begin + slice, vocab);
+    if (penalise)
+    {
+        for (uint32_t i = threadIdx.x; i < end - min(begin, end); i += kScaleThreads)
+        {
+            hits[i] = 0;
+        }
+        __syncthreads();
+        const uint32_t n = pw.position != nullptr
+                               ? min(static_cast<uint32_t>(max(*pw.position, -1) + 1), pw.historyCount)
+                               : pw.historyCount;
+        const uint32_t first =
+            (pw.lastN >= 0 && static_cast<uint32_t>(pw.lastN) < n) ? n - static_cast<uint32_t>(pw.lastN) : 0;
+        for (uint32_t i = first + threadIdx.x; i < n; i += kScaleThreads)
+        {
+            const int32_t t = pw.history[i];
+            if (t >= 0 && static_cast<uint32_t>(t) >= begin && static_cast<uint32_t>(t) < end)
+            {
+                atomicAdd(&hits[t - begin], 1u);
+            }
+        }
+        __syncthreads();
+    }
     uint64_t best = 0;
     for (uint32_t i = begin + threadIdx.x; i < end; i += kScaleThreads)
     {
@@ -313,7 +358,12 @@ __global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* 
         }
         else
         {
-            v = temperature > 0.0f ? src[i] / temperature : src[i];
+            v = src[i];
+            if (penalise)
+            {
+                v = Penalise(v, hits[i - begin], pw.penalty);
+            }
+            v = temperature > 0.0f ? v / temperature : v;
             dst[i] = v;
         }
         const uint64_t key = SampleKey(v, i);
@@ -333,6 +383,32 @@ __global__ __launch_bounds__(kScaleThreads) void SampleScaleKernel(const float* 
     }
 }
 
+/// The collection threshold from the kThresholdBlocks slice maxima: the k-th largest (distinct
+/// keys when the slice holds any, so exactly one thread finds itself at rank k - 1), or 0 (every
+/// key) when rank k - 1 falls among empty slices (maximum 0) or nowhere. kScaleThreads threads,
+/// maxima[] already in LDS; ends synchronised.
+__device__ uint64_t CollectionThreshold(const uint64_t* maxima, uint32_t k, uint64_t* threshold)
+{
+    static_assert(kScaleThreads == kThresholdBlocks, "one thread per slice maximum");
+    if (threadIdx.x == 0)
+    {
+        *threshold = 0;
+    }
+    __syncthreads();
+    const uint64_t mine = maxima[threadIdx.x];
+    uint32_t rank = 0;
+    for (uint32_t j = 0; j < kThresholdBlocks; ++j)
+    {
+        rank += maxima[j] > mine ? 1u : 0u;
+    }
+    if (rank == k - 1 && mine != 0)
+    {
+        *threshold = mine;
+    }
+    __syncthreads();
+    return *threshold;
+}
+
 /// Gathers every key of its slice at or above the threshold: the k-th largest of the
 /// kThresholdBlocks slice maxima (distinct keys when the slice holds any, so one thread finds
 /// itself at rank k - 1). At least k keys reach it: the maxima of rank 0..k-1.
@@ -344,26 +420,8 @@ __global__ __launch_bounds__(kScaleThreads) void SampleCollectKernel(const float
 {
     __shared__ uint64_t maxima[kThresholdBlocks];
     __shared__ uint64_t threshold;
-    const uint64_t mine = blockMax[threadIdx.x];
-    maxima[threadIdx.x] = mine;
-    if (threadIdx.x == 0)
-    {
-        // Empty slices (small vocabularies) have maximum 0 and share a rank; when rank k - 1 falls
-        // among them, or nowhere, every key is collected.
-        threshold = 0;
-    }
-    __syncthreads();
-    uint32_t rank = 0;
-    for (uint32_t j = 0; j < kThresholdBlocks; ++j)
-    {
-        rank += maxima[j] > mine ? 1u : 0u;
-    }
-    if (rank == k - 1 && mine != 0)
-    {
-        threshold = mine;
-    }
-    __syncthreads();
-    const uint64_t floor = threshold;
+    maxima[threadIdx.x] = blockMax[threadIdx.x];
+    const uint64_t floor = CollectionThreshold(maxima, k, &threshold);
     const uint32_t slice = (vocab + gridDim.x - 1) / gridDim.x;
     const uint32_t begin = blockIdx.x * slice;
     const uint32_t end = min(begin + slice, vocab);
@@ -401,13 +459,8 @@ __global__ __launch_bounds__(kScaleThreads) void SampleCollectKernel(const float
 /// below every real key.
 __global__ __launch_bounds__(kSelectThreads) void SampleSelectKernel(const float* __restrict__ values,
                                                                      const uint64_t* __restrict__ in, uint32_t count,
-                                                                     uint32_t k, uint64_t* __restrict__ out,
-                                                                     const uint32_t* collected)
+                                                                     uint32_t k, uint64_t* __restrict__ out)
 {
-    if (collected != nullptr && *collected <= kSampleFinalKeys)
-    {
-        return;  // the collection held every candidate
-    }
     __shared__ uint64_t keys[PaddedKeys(kSampleSliceKeys)];
     LoadKeys<kSampleSliceKeys, kSelectThreads>(keys, values, in, blockIdx.x * kSampleSliceKeys, count);
     SortDescending<kSampleSliceKeys, kSelectThreads>(keys);
@@ -417,8 +470,53 @@ __global__ __launch_bounds__(kSelectThreads) void SampleSelectKernel(const float
     }
 }
 
-/// Candidates: the collection (`collected` set and at most kSampleFinalKeys keys), else values[]
-/// or the last selection round's keys in[0..count).
+/// Orders keys[Slot(0..count)) (count <= 512, distinct keys) descending in place: each key's rank
+/// is the number of keys above it, so one pass over LDS and two barriers replace a sort network
+/// (for the few-times-k candidates a collection leaves). `ranked` holds 512 keys. Ends
+/// synchronised.
+__device__ void RankDescending(uint64_t* keys, uint64_t* ranked, uint32_t count)
+{
+    for (uint32_t i = threadIdx.x; i < count; i += kFinalThreads)
+    {
+        const uint64_t key = keys[Slot(i)];
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < count; ++j)
+        {
+            rank += keys[Slot(j)] > key ? 1u : 0u;
+        }
+        ranked[rank] = key;
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < count; i += kFinalThreads)
+    {
+        keys[Slot(i)] = ranked[i];
+    }
+    __syncthreads();
+}
+
+/// The k best keys of values[0..count) into keys[Slot(0..k)), descending: rounds that refill
+/// every slot past the best k so far with the next values and sort the 4096 (the collection's
+/// overflow, when over 4096 keys tie at the top; k <= 256). Ends synchronised.
+__device__ void SelectFromValues(uint64_t* keys, const float* __restrict__ values, uint32_t count, uint32_t k)
+{
+    uint32_t have = 0;
+    for (uint32_t base = 0; base < count;)
+    {
+        const uint32_t take = min(kSampleFinalKeys - have, count - base);
+        for (uint32_t j = have + threadIdx.x; j < kSampleFinalKeys; j += kFinalThreads)
+        {
+            const uint32_t i = base + (j - have);
+            keys[Slot(j)] = j - have < take ? SampleKey(values[i], i) : 0;
+        }
+        __syncthreads();
+        SortDescending<kSampleFinalKeys, kFinalThreads>(keys);
+        base += take;
+        have = k;
+    }
+}
+
+/// Candidates: the collection (`collected` set; when it overflowed, the whole of values[0..count)
+/// is selected from here), else values[] or the last selection round's keys in[0..count).
 __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* __restrict__ values,
                                                                    const uint64_t* __restrict__ in, uint32_t count,
                                                                    const uint64_t* __restrict__ gathered,
@@ -427,13 +525,17 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
                                                                    int32_t* token)
 {
     __shared__ uint64_t keys[PaddedKeys(kSampleFinalKeys)];
+    __shared__ uint64_t ranked[512];
     __shared__ double weight[kSampleMaxTopK];
+    __shared__ double share[kSampleMaxTopK];
+    __shared__ double totalWeight;
     __shared__ uint64_t old[kMt64Words];
     __shared__ uint64_t fresh[kMt64Words];
     // The engine's index and its next word, requested now so their latency hides under the sort.
     const uint64_t index = state->next;  // the same for every thread: written only at the end
     const bool twist = index >= kMt64Words;
     const uint64_t stored = state->x[twist ? 0 : index];
+    bool overflow = false;
     if (collected != nullptr)
     {
         const uint32_t n = *collected;
@@ -443,12 +545,19 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
             in = gathered;
             count = n;
         }
+        else
+        {
+            overflow = true;
+        }
     }
-    // The sort covers the next of 512 or 4096 keys (pads sort last).
-    if (count <= 512)
+    if (overflow)
+    {
+        SelectFromValues(keys, values, count, k);
+    }
+    else if (count <= 512)
     {
         LoadKeys<512, kFinalThreads>(keys, values, in, 0, count);
-        SortDescending<512, kFinalThreads>(keys);
+        RankDescending(keys, ranked, count);
     }
     else
     {
@@ -504,22 +613,34 @@ __global__ __launch_bounds__(kFinalThreads) void SampleFinalKernel(const float* 
     {
         __syncthreads();
     }
+    // src/Sampler.cpp:64-67: the total, summed in order by one thread; the normalised weights
+    // weight[j] / total, each one division, computed side by side.
+    if (threadIdx.x == 0)
+    {
+        double total = 0.0;
+        for (uint32_t j = 0; j < k; ++j)
+        {
+            total += weight[j];
+        }
+        totalWeight = total;
+    }
+    __syncthreads();
+    for (uint32_t j = threadIdx.x; j < k; j += kFinalThreads)
+    {
+        share[j] = weight[j] / totalWeight;
+    }
+    __syncthreads();
     if (threadIdx.x != 0)
     {
         return;
     }
-    // src/Sampler.cpp:64-84: the total, the shortest prefix whose normalised mass reaches top-p,
-    // and that prefix's mass, each summed in order.
-    double total = 0.0;
-    for (uint32_t j = 0; j < k; ++j)
-    {
-        total += weight[j];
-    }
+    // src/Sampler.cpp:68-84: the shortest prefix whose normalised mass reaches top-p, and that
+    // prefix's mass, each summed in order.
     uint32_t kept = k;
     double running = 0.0;
     for (uint32_t j = 0; j < k; ++j)
     {
-        running += weight[j] / total;
+        running += share[j];
         if (running >= static_cast<double>(topP))
         {
             kept = j + 1;
@@ -607,11 +728,15 @@ SampleWorkspace SampleWorkspaceAt(void* base, uint32_t vocab, const SampleConfig
     return ws;
 }
 
+/// Whether the scale kernel counts the penalty's occurrences itself (its slice fits LDS).
+bool PenaltyInScale(uint32_t vocab) { return CeilDiv(vocab, kThresholdBlocks) <= kScaleSliceMax; }
+
 uint32_t SampleLaunches(uint32_t vocab, const SampleConfig& c, bool)
 {
     const uint32_t k = RunK(c, vocab);
-    uint32_t launches = (c.repeatPenalty != 1.0f ? 1 : 0) + 1 + (Collects(vocab, k) ? 1 : 0) + 1;
-    for (uint32_t count = vocab; count > kSampleFinalKeys; count = CeilDiv(count, kSampleSliceKeys) * k)
+    const bool collect = Collects(vocab, k);
+    uint32_t launches = (c.repeatPenalty != 1.0f && !PenaltyInScale(vocab) ? 1 : 0) + 1 + (collect ? 1 : 0) + 1;
+    for (uint32_t count = vocab; !collect && count > kSampleFinalKeys; count = CeilDiv(count, kSampleSliceKeys) * k)
     {
         ++launches;
     }
@@ -635,34 +760,35 @@ hipError_t LaunchSample(hipStream_t s, const float* src, float* dst, uint32_t vo
     const uint32_t k = RunK(c, vocab);
     const bool penalise = c.repeatPenalty != 1.0f && (position != nullptr || historyCount > 0);
     const bool collect = Collects(vocab, k);
-    // The penalty goes first and finishes its tokens (penalty, then the division) from the raw
-    // logits; the scale kernel divides the rest. In place or into a separate buffer alike, dst
-    // ends as penalty^d(x) / T, as the reference leaves its logits.
-    if (penalise)
+    const bool penaltyInScale = penalise && PenaltyInScale(vocab);
+    // The penalty is applied with the division, penalty^d(x) / T, in place or into a separate
+    // buffer alike, as the reference leaves its logits: by the scale kernel from counts in LDS,
+    // or (long slices) by a Penalty kernel first that finishes and marks its tokens.
+    if (penalise && !penaltyInScale)
     {
         hipLaunchKernelGGL(SamplePenaltyKernel, dim3(1), dim3(kPenaltyThreads), 0, s, src, dst, vocab, history,
                            position, historyCount, c.repeatLastN, c.repeatPenalty, c.temperature, ws.counts);
     }
+    const PenaltyWindow window{history, position, historyCount, c.repeatLastN, c.repeatPenalty};
     hipLaunchKernelGGL(SampleScaleKernel, dim3(kThresholdBlocks), dim3(kScaleThreads), 0, s, src, dst, vocab,
-                       c.temperature, penalise ? ws.counts : nullptr, collect ? ws.blockMax : nullptr,
-                       ws.collected);
+                       c.temperature, penalise && !penaltyInScale ? ws.counts : nullptr, penaltyInScale, window,
+                       collect ? ws.blockMax : nullptr, ws.collected);
     if (collect)
     {
         hipLaunchKernelGGL(SampleCollectKernel, dim3(kThresholdBlocks), dim3(kScaleThreads), 0, s, dst, vocab, k,
                            ws.blockMax, ws.gathered, ws.collected);
     }
-    // Rounds of slice sorts until the final workgroup can hold every candidate; each round keeps
-    // k of 2048 keys per slice (k <= 1024), so the count at least halves. After a collection they
-    // run only when it overflowed.
+    // Without a collection: rounds of slice sorts until the final workgroup can hold every
+    // candidate; each round keeps k of 2048 keys per slice (k <= 1024), so the count at least
+    // halves. A collection that overflows is finished by the final workgroup from dst itself.
     const float* values = dst;
     const uint64_t* in = nullptr;
     uint32_t count = vocab;
     uint64_t* out = ws.candA;
-    while (count > kSampleFinalKeys)
+    while (!collect && count > kSampleFinalKeys)
     {
         const uint32_t slices = CeilDiv(count, kSampleSliceKeys);
-        hipLaunchKernelGGL(SampleSelectKernel, dim3(slices), dim3(kSelectThreads), 0, s, values, in, count, k, out,
-                           collect ? ws.collected : nullptr);
+        hipLaunchKernelGGL(SampleSelectKernel, dim3(slices), dim3(kSelectThreads), 0, s, values, in, count, k, out);
         count = slices * k;
         values = nullptr;
         in = out;

@@ -100,9 +100,10 @@ def test_ties_go_to_the_lower_index(mh, gpu, orc):
 
 
 @pytest.mark.parametrize("tied", [151936, 5000])
-def test_ties_at_the_top_fall_back_to_the_selection_rounds(mh, gpu, orc, tied):
+def test_ties_at_the_top_overflow_the_collection(mh, gpu, orc, tied):
     """More than 4096 keys at the collection threshold (all logits equal, or 5000 tied at the top):
-    the collection overflows and the selection rounds decide, still matching the oracle."""
+    the collection overflows and the final workgroup selects from every logit itself, still
+    matching the oracle."""
     vocab = 151936
     params = dict(temperature=1.0, top_k=40, top_p=0.95, repeat_penalty=1.0, seed=3)
     dev = DeviceSampler(mh, gpu, vocab, **params)
@@ -205,6 +206,6 @@ def test_decoder_sampling_graph_replay_matches_steps(mh, gpu, orc):
         dec.set_sampler()
         greedy_launches = dec.launches_per_step()
     assert ids == stepped
-    # Penalty, scale with the slice maxima, collection, one selection round (5000 > 4096 keys; it
-    # returns at once unless the collection overflowed) and the final draw.
-    assert launches == greedy_launches + 5
+    # Scale (with the penalty's counts and the slice maxima), the collection (5000 > 4096 keys)
+    # and the final draw.
+    assert launches == greedy_launches + 3
