@@ -598,7 +598,11 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
 //   v % 4 of the tile, and the V^T fragment reads the same keys (two 8-byte LDS reads).
 
 constexpr int kAttnKeys = 32;
-constexpr int kVStride = kAttnKeys + 8;  // halves per transposed V row
+// Halves per transposed V row. The even lane of each key pair stores both keys of a channel as one
+// 4-byte word, so the 16 storing lanes of a channel chunk write 64 contiguous bytes; 36 halves
+// (18 words) put the two chunks a wave stores at once 16 banks apart, and the MFMA fragment reads
+// of 32 consecutive rows (8 bytes each, 18 words apart) cover every bank once.
+constexpr int kVStride = kAttnKeys + 4;
 
 /// Grid (head splits, query tiles, kv heads): the splits of one tile are dispatched together and
 /// the longest tiles first.
@@ -679,15 +683,34 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
                 const uint32_t r = c % kAttnKeys;
                 const uint32_t cc = c / kAttnKeys;
                 *reinterpret_cast<half8*>(kTile + r * kKStride + cc * 8) = kReg[i];
-                // Rows past the tile's last query position may hold anything (NaN, inf): their
-                // weight is 0, and 0 * NaN would poison every query of the tile, so they enter
-                // the V tile as zeros. Their scores are masked to -inf by position.
-                const bool live = static_cast<int32_t>(kt * kAttnKeys + r) <= lastPos;
-                const half8 v = live ? vReg[i] : half8{};
+            }
+            // Rows past the tile's last query position may hold anything (NaN, inf): their weight
+            // is 0, and 0 * NaN would poison every query of the tile, so they enter the V tile as
+            // zeros. Their scores are masked to -inf by position. Lanes hold consecutive keys of a
+            // chunk (c % 32), so the odd lane's row reaches its even partner by a quad permute
+            // (lanes swapped in pairs) and the even lane stores both keys of each channel.
+            const uint32_t r = c % kAttnKeys;
+            const uint32_t cc = (c / kAttnKeys) % kChunks;
+            const bool live = static_cast<int32_t>(kt * kAttnKeys + r) <= lastPos;
+            const half8 v = live ? vReg[i] : half8{};
+            uint32_t mine[4];
+            __builtin_memcpy(mine, &v, sizeof(mine));
+            uint32_t other[4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
+            for (int d = 0; d < 4; ++d)
+            {
+                other[d] = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+                    static_cast<int>(mine[d]), static_cast<int>(mine[d]), 0xB1, 0xF, 0xF, false));
+            }
+            if (c < kAttnKeys * kChunks && (r & 1u) == 0)
+            {
+                uint32_t* row = reinterpret_cast<uint32_t*>(vTile) + ((cc * 8) * kVStride + r) / 2;
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
                 {
-                    reinterpret_cast<_Float16*>(vTile)[(cc * 8 + j) * kVStride + r] = v[j];
+                    // Channel 2d: the low halves of this key and the next; channel 2d + 1: the high.
+                    row[(2 * d) * (kVStride / 2)] = (mine[d] & 0xFFFFu) | (other[d] << 16);
+                    row[(2 * d + 1) * (kVStride / 2)] = (mine[d] >> 16) | (other[d] & 0xFFFF0000u);
                 }
             }
         }
