@@ -5,7 +5,7 @@
 // Hand-offs use self-validating 8-byte packets (f32 value in the low word, a per-write epoch in
 // the high word), stored and loaded with agent-scope relaxed atomics: a consumer keeps loading a
 // packet until it carries the epoch it expects, so no fence or flag is needed. Each workgroup's
-// first wave does all the waiting (the "poller") and hands what arrived to the other eight waves
+// first wave does all the waiting (the "poller") and hands what arrived to the other seven waves
 // through LDS at the one barrier between phases; those waves only compute, and request the next
 // phase's weights before that barrier, so the weights stream while the hand-off is in flight.
 // Every wait is bounded: on giving up, a workgroup records which wait failed and raises an abort
