@@ -442,6 +442,19 @@ def test_decoder_prefill_7b_width_full_prompt_equals_steps(mh, gpu, orc):
         1 + np.abs(orc.half_to_float(cache_s)).max())
 
 
+@pytest.mark.timeout(900)
+def test_decoder_prefill_7b_width_1024_tokens_matches_oracle(mh, gpu, orc):
+    """The 7B widths (hidden 3584, ffn 18944, 28/4 heads of 128) over a 1024-token prompt from row
+    0, which takes the 128 x 256 gate+up tiles, against the oracle fed token by token: the last
+    position's logits, the next token and every cache row (a small vocabulary keeps the oracle's
+    LM head cheap; the projections are full width)."""
+    orc.set_threads(16)
+    shape = dict(mh.QWEN25_7B, layers=2, vocab=2000)
+    dec, model = make_pair(mh, orc, shape, seed=90)
+    with dec:
+        check_against_oracle(dec, model, orc, shape, prompt(orc, 1024, shape["vocab"], 91), 0)
+
+
 def test_decoder_prefill_in_passes(mh, gpu, orc):
     """A prompt longer than one pass (2048 rows) runs in two; the second pass attends to the first
     through the cache."""
