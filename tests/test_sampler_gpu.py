@@ -56,6 +56,7 @@ CASES = [
     (4097, 1.0, 256, 0.9, 1.0, 64, 1.0),     # empty slices: the collection takes every key and overflows
     (20000, 1.0, 256, 0.95, 1.2, 64, 1.0),   # k at the number of slice maxima
     (20000, 1.0, 257, 0.95, 1.0, 64, 1.0),   # one past: selection rounds only
+    (600000, 0.9, 40, 0.95, 1.2, 64, 1.0),   # slices past the LDS counts: the separate penalty kernel
 ]
 
 
