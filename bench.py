@@ -109,7 +109,8 @@ def enqueue_step(dec, shape, stream) -> None:
 
 
 def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None, persistent=False):
-    """Returns (ms per step, positions timed, decoder launches per step). `sampler`: keyword
+    """Returns (ms per step, positions timed, decoder launches per step, generated ids, median ms
+    per step over 16 runs of the same positions). `sampler`: keyword
     parameters of the device sampler (greedy when None), with a synthetic prompt as history;
     `persistent`: the one-launch-per-token step instead of the graph-replayed kernels."""
     stream = torch.cuda.current_stream()
@@ -137,9 +138,23 @@ def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None, p
         ms = begin.elapsed_time(end) / steps
         ids = dec.generated_ids(steps)
         launches = dec.launches_per_step()
+        # The same steps again as 16 runs of steps/16 graph replays, an event after each run (the
+        # runs are queued ahead, so the GPU never waits on the host): the median run's time per
+        # step, its set-up kernels spread over the run.
+        runs = 16
+        per_run = max(1, steps // runs)
+        events = [torch.cuda.Event(enable_timing=True) for _ in range(runs + 1)]
+        torch.cuda.synchronize()
+        events[0].record(stream)
+        for i in range(runs):
+            dec.generate_async(ids[-1], first + i * per_run, per_run, stream.cuda_stream)
+            events[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per_step = sorted(events[i].elapsed_time(events[i + 1]) / per_run for i in range(runs))
+        median_ms = (per_step[runs // 2 - 1] + per_step[runs // 2]) / 2
     finally:
         dec.close()
-    return ms, list(range(first, first + steps)), launches, ids
+    return ms, list(range(first, first + steps)), launches, ids, median_ms
 
 
 def prefill_flops(c: dict, prompt: int) -> int:
@@ -688,7 +703,8 @@ def main() -> int:
         print(json.dumps(lines), flush=True)
         return 0
 
-    ms, positions, launches, ids = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed)
+    ms, positions, launches, ids, median_ms = time_decode(mh, torch, shape, args.position, args.steps, args.warmup,
+                                                          seed)
     total_bytes = sum(step_bytes(shape, p) for p in positions)
     value = total_bytes / (ms * 1e-3 * args.steps) / 1e9
 
@@ -701,14 +717,15 @@ def main() -> int:
     # The same decode with the device sampler after every step (the reference's sampling options
     # at common settings plus a repetition penalty): its cost per token over greedy.
     sampling = dict(temperature=0.7, top_k=40, top_p=0.95, repeat_penalty=1.1, repeat_last_n=64, seed=seed)
-    ms_s, _, launches_s, _ = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed, sampling)
+    ms_s, _, launches_s, _, _ = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed,
+                                            sampling)
     secondary["qwen2.5-0.5b-shape-sampled"] = {
         "sampler": sampling, "tok_per_s": round(1000.0 / ms_s, 1), "ms_per_step": round(ms_s, 5),
         "sampler_ms_per_token": round(ms_s - ms, 5), "launches_per_step": launches_s,
     }
     # The same greedy decode as one cooperative launch per token (the opt-in persistent step).
     if not args.no_persistent:
-        ms_p, _, launches_p, ids_p = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed,
+        ms_p, _, launches_p, ids_p, _ = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed,
                                                  persistent=True)
         secondary["qwen2.5-0.5b-shape-persistent"] = {
             "tok_per_s": round(1000.0 / ms_p, 1), "ms_per_step": round(ms_p, 5), "launches_per_step": launches_p,
@@ -720,12 +737,12 @@ def main() -> int:
     if not args.no_7b:
         shape7 = dict(mh.QWEN25_7B)
         steps7 = 16
-        ms7, pos7, _, _ = time_decode(mh, torch, shape7, 2048 - steps7 // 2, steps7, 4, seed + 7)
+        ms7, pos7, _, _, median7 = time_decode(mh, torch, shape7, 2048 - steps7 // 2, steps7, 4, seed + 7)
         bytes7 = sum(step_bytes(shape7, p) for p in pos7)
         gbs7 = bytes7 / (ms7 * 1e-3 * steps7) / 1e9
         secondary["qwen2.5-7b-shape"] = {
             "GB/s": round(gbs7, 1), "pct_of_peak": round(100 * gbs7 / HBM_PEAK_GBS, 1),
-            "tok_per_s": round(1000.0 / ms7, 1), "ms_per_step": round(ms7, 4),
+            "tok_per_s": round(1000.0 / ms7, 1), "ms_per_step": round(ms7, 4), "ms_per_step_median": round(median7, 4),
             "positions": f"{pos7[0]}..{pos7[-1]}", "bytes_per_step": bytes7 // steps7,
         }
         secondary["qwen2.5-7b-shape-prefill"] = prefill_line(mh, torch, shape7, 2048, 3, seed + 7, ms7)
@@ -738,6 +755,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_median": round(median_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
