@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <utility>
 #include <vector>
 
 #include "common.hpp"
@@ -121,14 +122,17 @@ struct MuyoDecoder
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 
-    // The persistent step (persistent.hpp): its plan, the transposed FFN_DOWN of every layer
-    // (rebuilt before a step whenever the weights may have changed), the per-layer pointer table,
-    // the hand-off arena and the control words.
+    // The persistent step (persistent.hpp): its plan, and an arena of its own, allocated when the
+    // step is first selected, holding the transposed FFN_DOWN of every layer (rebuilt before a
+    // step whenever the weights may have changed), the per-layer pointer table, the hand-off
+    // packets and the control words.
     const char* stepUnsupported = "not set up";
     bool persistent = false;
     bool downTDirty = true;
     StepPlan plan{};
-    std::vector<TensorSlot> downT;
+    size_t stepPackets = 0;
+    char* stepArena = nullptr;
+    std::vector<uint16_t*> downT;
     uint32_t* stepControl = nullptr;
 
     // Batched prefill (muyo_decoder_prefill): row-major activations of up to prefillRows prompt
@@ -467,27 +471,16 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     {
         d->stepUnsupported = "the step kernel does not fit a CU";
     }
-    TensorSlot stepLayers, packets, control;
-    size_t packetCount = 0;
     if (d->stepUnsupported == nullptr)
     {
-        // Attention blocks may read a block of rows past the last value cache; then the
-        // transposed down tensors (three rows of slack each), the pointer table, the arena.
+        // The step's attention blocks may read a block of rows past the last value cache.
         (void)place(static_cast<size_t>(kStepCacheSlackRows) * c.headDim * 2);
-        d->downT.resize(c.layers);
-        for (uint32_t l = 0; l < c.layers; ++l)
-        {
-            d->downT[l] = place((static_cast<size_t>(c.feedForward) + 3) * c.hidden * 2);
-        }
-        stepLayers = place(static_cast<size_t>(c.layers) * sizeof(StepLayer));
         d->plan.hidden = c.hidden;
         d->plan.ffn = c.feedForward;
         d->plan.heads = c.heads;
         d->plan.kvHeads = c.kvHeads;
         d->plan.headDim = c.headDim;
-        packetCount = StepPlanLayout(d->plan, static_cast<uint32_t>(cus));
-        packets = place(packetCount * sizeof(uint64_t));
-        control = place(kStepControlWords * sizeof(uint32_t));
+        d->stepPackets = StepPlanLayout(d->plan, static_cast<uint32_t>(cus));
     }
     const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
     const size_t group = c.heads / c.kvHeads;
@@ -578,62 +571,6 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->rng = d->At<Mt64State>(rng);
     d->sampleWorkspace = d->arena + sampleWorkspace.offset;
     d->argBlocks = LmHeadBlocks(d->dims);
-    if (d->stepUnsupported == nullptr)
-    {
-        StepPlan& p = d->plan;
-        p.layers = c.layers;
-        p.vocab = c.vocab;
-        p.maxSeq = c.maxSeq;
-        p.eps = c.rmsEps;
-        p.attnScale = d->dims.attnScale;
-        p.ropePow = d->dims.ropePow;
-        p.layer = d->At<StepLayer>(stepLayers);
-        p.embedding = d->At<uint16_t>(d->tokenEmbd);
-        p.head = d->At<uint16_t>(c.untiedOutput != 0 ? d->output : d->tokenEmbd);
-        p.outputNorm = d->At<float>(d->outputNorm);
-        p.logits = d->At<float>(d->logits);
-        p.state = d->state;
-        p.argValue = d->scratch.argValue;
-        p.argIndex = d->scratch.argIndex;
-        p.sampled = nullptr;
-        p.history = d->scratch.history;
-        p.historyCap = d->scratch.historyCap;
-        p.ids = d->ids;
-        p.idsCap = kIdsCapacity;
-        p.packets = d->At<uint64_t>(packets);
-        p.control = d->At<uint32_t>(control);
-        p.spinLimit = 1u << 20;
-        d->stepControl = p.control;
-        std::vector<StepLayer> table(c.layers);
-        for (uint32_t l = 0; l < c.layers; ++l)
-        {
-            StepLayer& t = table[l];
-            t.attnNorm = d->At<float>(d->Layer(l, kAttnNorm));
-            t.qkv = d->At<uint16_t>(d->Layer(l, kQkv));
-            t.qkvBias = d->At<float>(d->Layer(l, kQkvBias));
-            t.wo = d->At<uint16_t>(d->Layer(l, kOut));
-            t.ffnNorm = d->At<float>(d->Layer(l, kFfnNorm));
-            t.gate = d->At<uint16_t>(d->Layer(l, kGate));
-            t.up = d->At<uint16_t>(d->Layer(l, kUp));
-            t.downT = d->At<uint16_t>(d->downT[l]);
-            t.kcache = d->At<uint16_t>(d->Layer(l, kKCache));
-            t.vcache = d->At<uint16_t>(d->Layer(l, kVCache));
-        }
-        // Hand-off epochs start at 1 (the zeroed arena's packets carry epoch 0).
-        const uint32_t words[kStepControlWords] = {0, 0, 1, 0};
-        hipError_t st = hipMemcpy(d->arena + stepLayers.offset, table.data(), table.size() * sizeof(StepLayer),
-                                  hipMemcpyHostToDevice);
-        if (st == hipSuccess)
-        {
-            st = hipMemcpy(p.control, words, sizeof(words), hipMemcpyHostToDevice);
-        }
-        if (st != hipSuccess)
-        {
-            const int code = HipStatus(st, "decoder_create: persistent step tables");
-            muyo_decoder_destroy(d);
-            return code;
-        }
-    }
     *out = d;
     return MUYO_OK;
 }
@@ -666,11 +603,12 @@ extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
     {
         (void)hipStreamSynchronize(d->stream);
     }
-    if (d->arena != nullptr || d->prefillArena != nullptr)
+    if (d->arena != nullptr || d->prefillArena != nullptr || d->stepArena != nullptr)
     {
         (void)hipDeviceSynchronize();
         (void)hipFree(d->arena);
         (void)hipFree(d->prefillArena);
+        (void)hipFree(d->stepArena);
     }
     if (d->stream != nullptr)
     {
@@ -877,6 +815,105 @@ extern "C" int muyo_decoder_fill_kv_random(MuyoDecoder* d, uint32_t positions, u
 
 namespace
 {
+/// The persistent step's own arena (once per decoder, on first selection): the transposed FFN_DOWN
+/// of every layer (three rows of slack each), the per-layer pointer table, the hand-off packets
+/// (zeroed: epoch 0) and the control words, and the plan's pointers into it and the main arena.
+int SetUpStep(MuyoDecoder* d)
+{
+    if (d->stepArena != nullptr)
+    {
+        return MUYO_OK;
+    }
+    const MuyoQwen2Config& c = d->config;
+    size_t cursor = 0;
+    auto place = [&cursor](size_t bytes)
+    {
+        const size_t offset = cursor;
+        cursor = AlignUp(cursor + bytes);
+        return offset;
+    };
+    std::vector<size_t> downT(c.layers);
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        downT[l] = place((static_cast<size_t>(c.feedForward) + 3) * c.hidden * 2);
+    }
+    const size_t table = place(static_cast<size_t>(c.layers) * sizeof(StepLayer));
+    const size_t packets = place(d->stepPackets * sizeof(uint64_t));
+    const size_t control = place(kStepControlWords * sizeof(uint32_t));
+    char* arena = nullptr;
+    if (hipMalloc(reinterpret_cast<void**>(&arena), cursor) != hipSuccess)
+    {
+        return Fail(MUYO_E_NOMEM, "decoder: hipMalloc of the persistent step's %zu bytes failed", cursor);
+    }
+
+    StepPlan& p = d->plan;
+    p.layers = c.layers;
+    p.vocab = c.vocab;
+    p.maxSeq = c.maxSeq;
+    p.eps = c.rmsEps;
+    p.attnScale = d->dims.attnScale;
+    p.ropePow = d->dims.ropePow;
+    p.layer = reinterpret_cast<const StepLayer*>(arena + table);
+    p.embedding = d->At<uint16_t>(d->tokenEmbd);
+    p.head = d->At<uint16_t>(c.untiedOutput != 0 ? d->output : d->tokenEmbd);
+    p.outputNorm = d->At<float>(d->outputNorm);
+    p.logits = d->At<float>(d->logits);
+    p.state = d->state;
+    p.argValue = d->scratch.argValue;
+    p.argIndex = d->scratch.argIndex;
+    p.sampled = nullptr;
+    p.history = d->scratch.history;
+    p.historyCap = d->scratch.historyCap;
+    p.ids = d->ids;
+    p.idsCap = kIdsCapacity;
+    p.packets = reinterpret_cast<uint64_t*>(arena + packets);
+    p.control = reinterpret_cast<uint32_t*>(arena + control);
+    p.spinLimit = 1u << 20;
+    std::vector<StepLayer> rows(c.layers);
+    std::vector<uint16_t*> transposed(c.layers);
+    for (uint32_t l = 0; l < c.layers; ++l)
+    {
+        transposed[l] = reinterpret_cast<uint16_t*>(arena + downT[l]);
+        StepLayer& t = rows[l];
+        t.attnNorm = d->At<float>(d->Layer(l, kAttnNorm));
+        t.qkv = d->At<uint16_t>(d->Layer(l, kQkv));
+        t.qkvBias = d->At<float>(d->Layer(l, kQkvBias));
+        t.wo = d->At<uint16_t>(d->Layer(l, kOut));
+        t.ffnNorm = d->At<float>(d->Layer(l, kFfnNorm));
+        t.gate = d->At<uint16_t>(d->Layer(l, kGate));
+        t.up = d->At<uint16_t>(d->Layer(l, kUp));
+        t.downT = transposed[l];
+        t.kcache = d->At<uint16_t>(d->Layer(l, kKCache));
+        t.vcache = d->At<uint16_t>(d->Layer(l, kVCache));
+    }
+    // Hand-off epochs start at 1 (the zeroed packets carry epoch 0).
+    const uint32_t words[kStepControlWords] = {0, 0, 1, 0};
+    hipError_t st = hipMemsetAsync(arena, 0, cursor, d->stream);
+    if (st == hipSuccess)
+    {
+        st = hipMemcpyAsync(arena + table, rows.data(), rows.size() * sizeof(StepLayer), hipMemcpyHostToDevice,
+                            d->stream);
+    }
+    if (st == hipSuccess)
+    {
+        st = hipMemcpyAsync(p.control, words, sizeof(words), hipMemcpyHostToDevice, d->stream);
+    }
+    if (st == hipSuccess)
+    {
+        st = hipStreamSynchronize(d->stream);
+    }
+    if (st != hipSuccess)
+    {
+        (void)hipFree(arena);
+        return HipStatus(st, "decoder: persistent step tables");
+    }
+    d->stepArena = arena;
+    d->downT = std::move(transposed);
+    d->downTDirty = true;
+    d->stepControl = p.control;
+    return MUYO_OK;
+}
+
 /// The transposed FFN_DOWN copies, rebuilt when the weights may have changed since the last step.
 hipError_t EnsureDownT(MuyoDecoder* d, hipStream_t s)
 {
@@ -886,7 +923,7 @@ hipError_t EnsureDownT(MuyoDecoder* d, hipStream_t s)
     }
     for (uint32_t l = 0; l < d->config.layers; ++l)
     {
-        const hipError_t st = LaunchTranspose16(s, d->At<uint16_t>(d->Layer(l, kDown)), d->At<uint16_t>(d->downT[l]),
+        const hipError_t st = LaunchTranspose16(s, d->At<uint16_t>(d->Layer(l, kDown)), d->downT[l],
                                                 d->config.hidden, d->config.feedForward);
         if (st != hipSuccess)
         {
@@ -1398,6 +1435,14 @@ extern "C" int muyo_decoder_set_persistent(MuyoDecoder* d, int on)
         return Fail(MUYO_E_UNSUPPORTED, "decoder: no persistent step for this shape: %s", d->stepUnsupported);
     }
     MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
+    if (on != 0)
+    {
+        const int status = SetUpStep(d);
+        if (status != MUYO_OK)
+        {
+            return status;
+        }
+    }
     d->persistent = on != 0;
     return MUYO_OK;
 }

@@ -543,7 +543,6 @@ __device__ __forceinline__ void PollerProgram(const StepPlan& p, StepShared& sh,
     const uint32_t lane = cx.lane;
     const Roles& ro = cx.ro;
     const uint32_t group = cx.group;
-    const uint32_t qdim = cx.qdim;
     const uint32_t epoch0 = cx.epoch0;
     bool live = !Abandoned(p.control);
     float normW[kMaxRow / kWave];

@@ -97,3 +97,32 @@ def test_persistent_05b_greedy_32_steps(mh, gpu, orc):
         ids = dec.generate(4321, 1024, 32)
     want, _ = model.greedy(4321, 1024, 32)
     assert ids == want
+
+
+def test_persistent_arena_allocated_on_selection(mh, gpu, orc):
+    """The step's own arena (the transposed FFN_DOWN of every layer, about 209 MB on the 0.5B shape)
+    is allocated when the step is first selected, not at creation; weights written after selection
+    reach the transposed copies."""
+    torch = gpu
+    shape = mh.QWEN25_05B
+    down_t = shape["layers"] * (shape["ffn"] + 3) * shape["hidden"] * 2
+    with mh.Decoder(mh.qwen2_config(**shape)) as dec:
+        torch.cuda.synchronize()
+        before, _ = torch.cuda.mem_get_info()
+        dec.set_persistent(True)
+        after, _ = torch.cuda.mem_get_info()
+        assert before - after >= down_t, (before, after, down_t)
+        dec.set_persistent(False)
+        dec.set_persistent(True)  # the arena is kept, not allocated again
+        assert torch.cuda.mem_get_info()[0] > after - down_t // 2
+    dec, model = make_pair(mh, orc, SMALL, seed=5)
+    with dec:
+        dec.set_persistent(True)
+        dec.fill_random(6)
+        model.fill_random(6)
+        dec.fill_kv_random(20, 7)
+        model.fill_kv_random(20, 7)
+        got = dec.step(9, 20)
+        want, logits, _ = model.step(9, 20)
+        assert close(logits_of(dec, SMALL["vocab"]), logits, 1e-3) == 0
+        assert got == want
