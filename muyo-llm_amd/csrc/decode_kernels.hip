@@ -101,6 +101,26 @@ struct NormStage
     }
 };
 
+/// NormStage over an activation that arrives as `groups` partial vectors (the grouped o_proj's
+/// per-kv-group sums, the residual already in group 0): x = ((p0 + p1) + p2) + ..., rms_norm
+/// applied as NormStage does. Workgroup 0 also stores x to `sum`, the residual of the layer's
+/// down projection.
+struct PartsNormStage
+{
+    const float* parts;  // [groups][n]
+    uint32_t groups;
+    const float* w;
+    float eps;
+    float* sum;
+    static constexpr bool kCanDirect = false;  // the sum is stored once, through the staging path
+    static constexpr bool kDirect = false;
+    template <int kThreads, int kVec>
+    __device__ void Run(float4* xs, uint32_t n) const
+    {
+        StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr);
+    }
+};
+
 /// A staging policy applied by every lane to its own activation chunks, straight from global
 /// memory into registers (single-batch rows, where one segment covers the row): no LDS and no
 /// barrier, so the activation costs one latency that overlaps the weights'. Every segment reads
@@ -1500,6 +1520,115 @@ __global__ __launch_bounds__(128) void AttentionMergeKernel(DecodeScratch sc, fl
     }
 }
 
+/// o_proj split by kv group, with the attention merge in its prologue. Workgroup (b, g) owns
+/// group g's query heads, the W_o columns [g * gw, (g + 1) * gw) with gw = group * headDim
+/// (at most 1024), and rows b * 4 + w + k * 4 * gridDim.x (k < kRows) for its wave w. Every
+/// thread requests its merge operands, then its wave's row slices; the workgroup merges the
+/// group's chunk partials (AttentionMergeKernel's arithmetic, four channels per thread) into LDS
+/// while the weights are in flight (loads complete in order, so operands requested after the
+/// weights would wait for them: 8.8 -> 8.0 us at the 7B widths). The rows' dots go to
+/// parts[g][row], group 0 adding the residual; the next kernel's prologue sums the groups. A
+/// workgroup reads one group's partials instead of every head's, so the merge costs each
+/// workgroup gridChunks * gw floats.
+template <int kRows>
+__global__ __launch_bounds__(kBlock) void OProjGroupKernel(const uint16_t* __restrict__ wo, DecodeScratch sc,
+                                                           const float* __restrict__ residual,
+                                                           float* __restrict__ parts, uint32_t hidden,
+                                                           uint32_t qdim, uint32_t group, uint32_t headDim,
+                                                           uint32_t gridChunks)
+{
+    constexpr int kCpl = 2;
+    __shared__ float4 xs[2 * kWave * kCpl];
+    const uint32_t g = blockIdx.y;
+    const uint32_t gw = group * headDim;
+    const uint32_t nchunks = gw / 8;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t wave = threadIdx.x / kWave;
+    const uint32_t stride = kWaves * gridDim.x;
+    const uint32_t first = blockIdx.x * kWaves + wave;
+    // Merge operands first: thread t owns channels 4t..4t+3 of the group (one head).
+    const uint32_t t = threadIdx.x;
+    const uint32_t tc = min(t, gw / 4 - 1);
+    const uint32_t hh = 4 * tc / headDim;
+    const uint32_t d = 4 * tc % headDim;
+    float m[kMaxAttnChunks];
+    float l[kMaxAttnChunks];
+    float4 a[kMaxAttnChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+    {
+        const uint32_t cc = min(c, gridChunks - 1);
+        const uint64_t slot = (static_cast<uint64_t>(g) * gridChunks + cc) * group + hh;
+        m[c] = c < gridChunks ? sc.attnMax[slot] : -INFINITY;
+        l[c] = sc.attnSum[slot];
+        a[c] = *reinterpret_cast<const float4*>(sc.attnAcc + slot * headDim + d);
+    }
+    half8 w[kRows][kCpl];
+    float res[kRows];
+#pragma unroll
+    for (int k = 0; k < kRows; ++k)
+    {
+        const uint32_t row = min(first + k * stride, hidden - 1);
+        LoadBatch<kWave, kCpl>(wo + static_cast<uint64_t>(row) * qdim + g * gw, 0, nchunks, lane, w[k]);
+        res[k] = g == 0 ? residual[row] : 0.0f;
+    }
+    {
+        float top = -INFINITY;
+#pragma unroll
+        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+        {
+            top = fmaxf(top, m[c]);
+        }
+        float4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+        float den = 0.0f;
+        if (top != -INFINITY)
+        {
+#pragma unroll
+            for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+            {
+                const float e = exp2f(m[c] - top);
+                num.x = fmaf(e, a[c].x, num.x);
+                num.y = fmaf(e, a[c].y, num.y);
+                num.z = fmaf(e, a[c].z, num.z);
+                num.w = fmaf(e, a[c].w, num.w);
+                den = fmaf(e, l[c], den);
+            }
+        }
+        float4 out = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (den > 0.0f)
+        {
+            out = float4{num.x / den, num.y / den, num.z / den, num.w / den};
+        }
+        if (4 * t < gw)
+        {
+            xs[(t & 1u) ? nchunks + t / 2 : t / 2] = out;
+        }
+    }
+    __syncthreads();
+    float4 xlo[kCpl];
+    float4 xhi[kCpl];
+    LoadActivation<kWave, kCpl>(xs, xs + nchunks, nchunks, lane, xlo, xhi);
+    float sums[kRows];
+#pragma unroll
+    for (int k = 0; k < kRows; ++k)
+    {
+        sums[k] = DotRegisters<kWave, kCpl>(w[k], xlo, xhi, nchunks, lane);
+    }
+    GroupSumN<kWave>(sums);
+    if (lane == 0)
+    {
+#pragma unroll
+        for (int k = 0; k < kRows; ++k)
+        {
+            const uint32_t row = first + k * stride;
+            if (row < hidden)
+            {
+                parts[static_cast<uint64_t>(g) * hidden + row] = res[k] + sums[k];
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // Rope + append from separate q/k/v vectors (the per-op form of the QKV epilogue).
 
@@ -1652,6 +1781,61 @@ hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16
                      dims.headDim,    AttnGridChunks(dims.maxSeq, dims.headDim, kMergeAttnChunks)};
     ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
     return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
+}
+
+bool OProjInGroups(const DecodeDims& dims)
+{
+    const uint32_t gw = dims.heads / dims.kvHeads * dims.headDim;
+    return !MergeInOProj(dims) && gw <= 2 * kWave * 8 && gw % 8 == 0 && dims.headDim % 4 == 0 &&
+           dims.kvHeads <= kMaxStageParts;
+}
+
+template <int kRows>
+hipError_t LaunchOProjGroupsT(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                              const float* residual, float* parts)
+{
+    const dim3 grid(CeilDiv(dims.hidden, kWaves * kRows), dims.kvHeads);
+    hipLaunchKernelGGL(OProjGroupKernel<kRows>, grid, dim3(kBlock), 0, s, wo, scratch, residual, parts, dims.hidden,
+                       dims.heads * dims.headDim, dims.heads / dims.kvHeads, dims.headDim,
+                       AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks));
+    return hipGetLastError();
+}
+
+hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                             const float* residual, float* parts)
+{
+    if (!OProjInGroups(dims))
+    {
+        return hipErrorInvalidValue;
+    }
+    // About two workgroups per CU: the rows of each group spread over 2 * CUs / groups workgroups.
+    const uint32_t waves = std::max(1u, 2 * CuCount() * kWaves / dims.kvHeads);
+    const uint32_t perWave = CeilDiv(dims.hidden, waves);
+    if (perWave <= 1)
+    {
+        return LaunchOProjGroupsT<1>(s, dims, wo, scratch, residual, parts);
+    }
+    if (perWave <= 2)
+    {
+        return LaunchOProjGroupsT<2>(s, dims, wo, scratch, residual, parts);
+    }
+    if (perWave <= 4)
+    {
+        return LaunchOProjGroupsT<4>(s, dims, wo, scratch, residual, parts);
+    }
+    if (perWave <= 7)
+    {
+        return LaunchOProjGroupsT<7>(s, dims, wo, scratch, residual, parts);
+    }
+    return LaunchOProjGroupsT<8>(s, dims, wo, scratch, residual, parts);
+}
+
+hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const float* parts, const float* normW,
+                                   const uint16_t* wgate, const uint16_t* wup, float* act, float* sum)
+{
+    GateUpEpi epi{wgate, wup, act, dims.ffn, dims.hidden};
+    return LaunchFused<2>(s, dims.ffn, kNoLimit, dims.hidden, PartsNormStage{parts, dims.kvHeads, normW, dims.eps, sum},
+                          epi);
 }
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,

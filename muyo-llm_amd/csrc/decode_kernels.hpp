@@ -111,6 +111,19 @@ hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const Dec
 hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
                              const float* residual, float* out);
 
+/// True when o_proj runs split by kv group with the attention merge in its prologue (models
+/// whose q dim is too wide for MergeInOProj but whose group is at most 1024 channels wide).
+bool OProjInGroups(const DecodeDims& dims);
+
+/// o_proj per kv group: parts[g][row] = (g == 0 ? residual[row] : 0) + W_o[row, group g's columns]
+/// . merged attention of group g. The layer's hidden state is the sum of the kvHeads parts.
+hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                             const float* residual, float* parts);
+
+/// LaunchGateUpSwiGlu on the sum of the kvHeads o_proj parts, which it also stores to `sum`.
+hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const float* parts, const float* normW,
+                                   const uint16_t* wgate, const uint16_t* wup, float* act, float* sum);
+
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols);
 

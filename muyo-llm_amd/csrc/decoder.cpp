@@ -103,12 +103,14 @@ struct MuyoDecoder
     float* xMid = nullptr;
     float* q = nullptr;
     float* attnOut = nullptr;
+    float* oParts = nullptr;  // [kvHeads][hidden] o_proj sums per kv group (oProjGroups)
     float* act = nullptr;
     DecodeState* state = nullptr;
     int32_t* ids = nullptr;
     DecodeScratch scratch{};
     uint32_t argBlocks = 0;     // LM-head workgroups = argmax partials per step
     bool mergeInOProj = false;  // o_proj's prologue merges the attention partials
+    bool oProjGroups = false;   // o_proj runs per kv group, merging that group's partials
 
     // Sampling (muyo_decoder_set_sampler): off = greedy from the LM head's argmax partials.
     bool sampling = false;
@@ -259,7 +261,7 @@ hipError_t EnqueueAttention(MuyoDecoder* d, hipStream_t s, uint32_t l)
 {
     hipError_t status = LaunchAttention(s, d->dims, d->q, d->At<uint16_t>(d->Layer(l, kKCache)),
                                         d->At<uint16_t>(d->Layer(l, kVCache)), &d->state->position, d->scratch);
-    if (status == hipSuccess && !d->mergeInOProj)
+    if (status == hipSuccess && !d->mergeInOProj && !d->oProjGroups)
     {
         status = LaunchAttentionMerge(s, d->dims, d->scratch, d->attnOut);
     }
@@ -273,11 +275,23 @@ hipError_t EnqueueOProj(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* 
     {
         return LaunchOProjMerged(s, d->dims, wo, d->scratch, residual, out);
     }
+    if (d->oProjGroups)
+    {
+        return LaunchOProjGroups(s, d->dims, wo, d->scratch, residual, d->oParts);  // gate/up writes `out`
+    }
     return LaunchMatVecResidual(s, wo, d->attnOut, residual, out, d->config.hidden, d->config.heads * d->config.headDim);
 }
 
-hipError_t EnqueueGateUp(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* x)
+/// `x` is the hidden state after attention: read, or, when o_proj leaves per-group parts,
+/// written as their sum.
+hipError_t EnqueueGateUp(MuyoDecoder* d, hipStream_t s, uint32_t l, float* x)
 {
+    if (d->oProjGroups)
+    {
+        return LaunchGateUpSwiGluParts(s, d->dims, d->oParts, d->At<float>(d->Layer(l, kFfnNorm)),
+                                       d->At<uint16_t>(d->Layer(l, kGate)), d->At<uint16_t>(d->Layer(l, kUp)),
+                                       d->act, x);
+    }
     return LaunchGateUpSwiGlu(s, d->dims, x, d->At<float>(d->Layer(l, kFfnNorm)), d->At<uint16_t>(d->Layer(l, kGate)),
                               d->At<uint16_t>(d->Layer(l, kUp)), d->act);
 }
@@ -428,6 +442,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->dims.attnScale = 1.0F / std::sqrt(static_cast<float>(c.headDim));
     d->mergeInOProj = MergeInOProj(d->dims);
     d->dims.attnChunks = d->mergeInOProj ? kMergeAttnChunks : kMaxAttnChunks;
+    d->oProjGroups = OProjInGroups(d->dims);
 
     // Arena layout: embedding, output norm, logits, then each layer's tensors, then activations
     // and scratch. Every tensor starts on a 256-byte boundary.
@@ -490,6 +505,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot xMid = place(c.hidden * 4);
     const TensorSlot q = place(qdim * 4);
     const TensorSlot attnOut = place(qdim * 4);
+    const TensorSlot oParts = place(static_cast<size_t>(c.kvHeads) * c.hidden * 4);
     const TensorSlot act = place(static_cast<size_t>(c.feedForward) * 4);
     const TensorSlot state = place(sizeof(DecodeState));
     const TensorSlot ids = place(kIdsCapacity * 4);
@@ -555,6 +571,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->xMid = d->At<float>(xMid);
     d->q = d->At<float>(q);
     d->attnOut = d->At<float>(attnOut);
+    d->oParts = d->At<float>(oParts);
     d->act = d->At<float>(act);
     d->state = d->At<DecodeState>(state);
     d->ids = d->At<int32_t>(ids);
@@ -1072,7 +1089,7 @@ extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
     {
         return 0;
     }
-    const uint32_t greedy = d->persistent ? 1u : 2u + (d->mergeInOProj ? 5u : 6u) * d->config.layers;
+    const uint32_t greedy = d->persistent ? 1u : 2u + (d->mergeInOProj || d->oProjGroups ? 5u : 6u) * d->config.layers;
     return greedy + (d->sampling ? SampleLaunches(d->config.vocab, d->sample, true) : 0u);
 }
 

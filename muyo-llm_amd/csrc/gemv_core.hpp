@@ -214,10 +214,14 @@ __device__ __forceinline__ float RowDot(const uint16_t* __restrict__ row, uint32
 /// independent float4 loads (kVec per thread per round), so staging costs one memory latency.
 /// With kNorm the values are scaled by rsqrt(mean(x^2) + eps) * w in the order (scale * x) * w
 /// of rms_norm.comp:122; that path holds x and w in registers and needs n/4 <= kVec * threads.
-/// Ends with the block synchronised.
+/// With kNorm, x may also be `parts` (at most kMaxStageParts) consecutive vectors of n floats
+/// whose sum (added in order) is the activation; `sumOut`, when set, receives that sum. Ends
+/// with the block synchronised.
+constexpr uint32_t kMaxStageParts = 4;
+
 template <int kBlockThreads, int kVec, bool kNorm>
 __device__ __forceinline__ void StageSplit(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
-                                           float eps, float4* xs)
+                                           float eps, float4* xs, uint32_t parts = 1, float* sumOut = nullptr)
 {
     constexpr int kWaveCount = kBlockThreads / kWave;
     const uint32_t n4 = n / 4;
@@ -257,6 +261,47 @@ __device__ __forceinline__ void StageSplit(const float* __restrict__ x, const fl
             const uint32_t i = min(threadIdx.x + k * kBlockThreads, n4 - 1);
             v[k] = x4[i];
             g[k] = w4[i];
+        }
+        if (parts > 1)
+        {
+            // Every part's loads go out before any is added: one latency for all of them.
+            float4 more[kMaxStageParts - 1][kVec];
+#pragma unroll
+            for (uint32_t p = 1; p < kMaxStageParts; ++p)
+            {
+#pragma unroll
+                for (int k = 0; k < kVec; ++k)
+                {
+                    more[p - 1][k] = x4[min(p, parts - 1) * n4 + min(threadIdx.x + k * kBlockThreads, n4 - 1)];
+                }
+            }
+#pragma unroll
+            for (uint32_t p = 1; p < kMaxStageParts; ++p)
+            {
+#pragma unroll
+                for (int k = 0; k < kVec; ++k)
+                {
+                    if (p < parts)
+                    {
+                        v[k].x += more[p - 1][k].x;
+                        v[k].y += more[p - 1][k].y;
+                        v[k].z += more[p - 1][k].z;
+                        v[k].w += more[p - 1][k].w;
+                    }
+                }
+            }
+        }
+        if (sumOut != nullptr)
+        {
+            float4* s4 = reinterpret_cast<float4*>(sumOut);
+#pragma unroll
+            for (int k = 0; k < kVec; ++k)
+            {
+                if (threadIdx.x + k * kBlockThreads < n4)
+                {
+                    s4[threadIdx.x + k * kBlockThreads] = v[k];
+                }
+            }
         }
         float ss = 0.0f;
 #pragma unroll
