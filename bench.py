@@ -80,19 +80,21 @@ def kernel_bytes(c: dict, kind: str, position: int) -> int:
     """Algorithmic HBM bytes of one launch of a decode-step kernel at cache row `position`: weights
     once as fp16, K/V rows 0..position once as fp16, f32 activations once per kernel touching them.
     Attention writes per-chunk partials (head_dim + 2 floats per chunk and query head) that the
-    o_proj prologue (q dim <= 1024, 8 chunks) or the merge kernel (16 chunks) reads."""
+    o_proj prologue reads: all of them (q dim <= 1024, 8 chunks), or, split by kv group (16 chunks),
+    its group's, leaving one partial sum of the hidden state per kv group for gate/up's prologue
+    to add up (gate/up then also stores that sum, the down projection's residual)."""
     h, f, hd, v = c["hidden"], c["ffn"], c["head_dim"], c["vocab"]
     q, kv = c["heads"] * hd, c["kv_heads"] * hd
     merged = q <= 1024
     chunks = min(8 if merged else 16, -(-c["max_seq"] // (2048 // hd)))
     partials = 4 * chunks * c["heads"] * (hd + 2)
+    parts = 4 * c["kv_heads"] * h  # the grouped o_proj's per-group sums
     table = {
         "embed": 8 * 1024 + 2 * h + 4 * h,
         "qkv": 2 * (q + 2 * kv) * h + 4 * (q + 2 * kv) + 8 * h + 4 * q + 4 * kv,
         "attention": 4 * kv * (position + 1) + 4 * q + partials,
-        "merge": partials + 4 * q,
-        "o_proj": 2 * h * q + (partials if merged else 4 * q) + 8 * h,
-        "gate_up": 4 * f * h + 8 * h + 4 * f,
+        "o_proj": 2 * h * q + partials + 4 * h + (4 * h if merged else parts),
+        "gate_up": 4 * f * h + (8 * h if merged else parts + 8 * h) + 4 * f,
         "down": 2 * h * f + 4 * f + 8 * h,
         "lm_head": lm_head_bytes(c),
     }
@@ -561,6 +563,8 @@ def step_kind(name: str, previous: str | None) -> str | None:
         return "attention"
     if "AttentionMerge" in name:
         return "merge"
+    if "OProjGroup" in name:
+        return "o_proj"
     if "GateUpEpi" in name:
         return "gate_up"
     if "LmHeadEpi" in name:

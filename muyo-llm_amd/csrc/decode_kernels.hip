@@ -11,8 +11,10 @@
 //                    arrives; online softmax in log2 units; chunk partials (max, sum, P.V) to
 //                    scratch (neutral for a chunk without keys)
 //   [AttentionMerge: combine the chunk partials, when o_proj does not do it itself]
-//   OProj          : [merge prologue] o_proj GEMV + residual add
-//   GateUpSwiGlu   : rms_norm prologue -> gate and up GEMV rows -> silu(g)*u
+//   OProj          : [merge prologue] o_proj GEMV + residual add; or, split by kv group, each
+//                    workgroup merging its group's partials, one partial hidden state per group
+//   GateUpSwiGlu   : rms_norm prologue (summing the o_proj group parts) -> gate and up GEMV
+//                    rows -> silu(g)*u
 //   Down           : down GEMV + residual add
 //   LmHeadArgMax   : final rms_norm prologue -> tied LM head -> logits + per-workgroup argmax
 //

@@ -4,7 +4,8 @@
 // serialises device-wide, ~60 ns per workgroup): every cross-workgroup reduction is split at a
 // kernel boundary. The LM head leaves per-workgroup (max, index) partials that the next step's
 // first kernel (or a finalize kernel) reduces; attention leaves per-chunk softmax partials that
-// the o_proj kernel's prologue (or a small merge kernel) combines.
+// the o_proj kernel's prologue combines (all of them, or per kv group, leaving one partial sum per
+// group that gate/up's prologue adds up; otherwise a small merge kernel).
 #pragma once
 
 #include <hip/hip_runtime.h>

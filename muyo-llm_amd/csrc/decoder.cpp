@@ -3,7 +3,8 @@
 // It plays the role of RunFullModel's render graph (src/FullModel.cpp:685-998) plus its
 // feedToken/sampleNext loop (:1096-1117): one arena of device memory holds every weight, the
 // fp16 KV cache and the activations; one step is 2 + 5 * layers launches on one stream
-// (6 per layer when the attention partials need their own merge kernel; decode_kernels.hip).
+// (6 per layer for the shapes whose attention partials need their own merge kernel: q dim over
+// 1024 with a kv group over 1024 channels or more than four kv heads; decode_kernels.hip).
 // The first step runs eagerly; later steps replay a hipGraph captured once, because everything
 // that changes per token (token id, position, step counter) lives in device memory: the first
 // kernel of a step reduces the previous step's argmax partials into its token and advances the
