@@ -64,8 +64,9 @@ def test_decoder_small_steps_match_oracle(mh, gpu, orc):
 
 
 # Shapes off the two Qwen sizes: a full GQA group of 8 with head_dim 128 (q dim 1024, merged in
-# o_proj), a q dim past 1024 with head_dim 64 (separate merge kernel), odd cache lengths and rows
-# at the end of the cache.
+# o_proj), q dims past 1024 (o_proj split by kv group: four groups of 5 heads at head_dim 64, two
+# of 6 at 128), eight kv heads (more group parts than gate/up's prologue adds up: a separate merge
+# kernel), odd cache lengths and rows at the end of the cache.
 ODD_SHAPES = {
     "group8_hd128": (dict(layers=1, hidden=512, ffn=1024, heads=8, kv_heads=1, head_dim=128, vocab=500,
                           max_seq=300), 296),
@@ -73,7 +74,14 @@ ODD_SHAPES = {
                            max_seq=333), 329),
     "hidden_1536_short_cache": (dict(layers=1, hidden=1536, ffn=8960, heads=12, kv_heads=2, head_dim=128,
                                      vocab=300, max_seq=40), 36),
+    "kv8_merge_kernel": (dict(layers=2, hidden=512, ffn=1024, heads=16, kv_heads=8, head_dim=128, vocab=400,
+                              max_seq=200), 150),
 }
+
+
+# Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel).
+ODD_LAUNCHES = {"group8_hd128": 2 + 5, "qdim1280_hd64": 2 + 5 * 2, "hidden_1536_short_cache": 2 + 5,
+                "kv8_merge_kernel": 2 + 6 * 2}
 
 
 @pytest.mark.parametrize("name", sorted(ODD_SHAPES))
@@ -81,6 +89,7 @@ def test_decoder_odd_shapes_match_oracle(mh, gpu, orc, name):
     shape, start = ODD_SHAPES[name]
     dec, model = make_pair(mh, orc, shape, seed=31, kv_positions=start, kv_seed=32)
     with dec:
+        assert dec.launches_per_step() == ODD_LAUNCHES[name]
         token = 3
         for i in range(4):
             got = dec.step(token, start + i)
