@@ -656,6 +656,93 @@ def summarize_counters(root: pathlib.Path, which: str) -> str:
     return "\n".join(lines)
 
 
+def summarize_ops(root: pathlib.Path) -> str:
+    """Per-launcher figures of the per-op suite from rocprofv3 CSVs of `--ops-only` runs kept under
+    root (trace/, fetch/, write/, hit/, copy_fetch/, copy_write/, and ops.json, the trace run's
+    JSON line): kernel-trace durations, FETCH_SIZE and WRITE_SIZE scaled by what they read for a
+    256 MiB copy, the L2 hit rate. The suite runs its launchers in a fixed order, each launch
+    eagerly once and then from a replayed hipGraph; the fills between them are left out."""
+    import csv
+    from collections import defaultdict
+
+    ops = json.loads((root / "ops.json").read_text())["kernels"]
+    names = list(ops)
+
+    def rows(sub: str, suffix: str):
+        files = sorted((root / sub).rglob(f"*{suffix}"))
+        if not files:
+            raise SystemExit(f"no *{suffix} under {root / sub}")
+        with open(files[0], newline="") as fh:
+            return sorted(csv.DictReader(fh), key=lambda r: int(r["Dispatch_Id"]))
+
+    def segment(records):
+        """Dispatch id -> op name: runs of one (kernel, grid) between fills, in suite order."""
+        runs, last = [], None
+        for r in records:
+            kname = r["Kernel_Name"]
+            if "FillNormal" in kname or kname.startswith("void at::native") or kname.startswith("at::native"):
+                continue
+            key = (kname, r.get("Grid_Size_X") or r.get("Grid_Size"))
+            if key != last:
+                runs.append([])
+                last = key
+            runs[-1].append(int(r["Dispatch_Id"]))
+        if len(runs) != len(names):
+            raise SystemExit(f"{len(runs)} launcher runs in the trace, {len(names)} ops in ops.json")
+        return {d: name for name, ids in zip(names, runs) for d in ids}
+
+    def counter_means(sub: str, counters):
+        recs = rows(sub, "counter_collection.csv")
+        # One record per (dispatch, counter): segment on the distinct dispatches.
+        seen, firsts = set(), []
+        for r in recs:
+            if r["Dispatch_Id"] not in seen:
+                seen.add(r["Dispatch_Id"])
+                firsts.append(r)
+        which = segment(firsts)
+        acc = defaultdict(lambda: defaultdict(list))
+        for r in recs:
+            name = which.get(int(r["Dispatch_Id"]))
+            if name is not None and r["Counter_Name"] in counters:
+                acc[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+        return {n: {c: sum(v) / len(v) for c, v in d.items()} for n, d in acc.items()}
+
+    def copy_mean(sub: str, name: str) -> float:
+        vals = [float(r["Counter_Value"]) for r in rows(sub, "counter_collection.csv")
+                if "copyBuffer" in r["Kernel_Name"] and r["Counter_Name"] == name]
+        return sum(vals) / len(vals)
+
+    copy_kib = 2 * 4 * 64 * 1024 * 1024 / 2 / 1024  # 256 MiB read, 256 MiB written
+    fetch_scale = copy_kib / copy_mean("copy_fetch", "FETCH_SIZE")
+    write_scale = copy_kib / copy_mean("copy_write", "WRITE_SIZE")
+    trace = rows("trace", "kernel_trace.csv")
+    which = segment(trace)
+    durations = defaultdict(list)
+    for r in trace:
+        name = which.get(int(r["Dispatch_Id"]))
+        if name is not None:
+            durations[name].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1000.0)
+    fetch = counter_means("fetch", {"FETCH_SIZE"})
+    write = counter_means("write", {"WRITE_SIZE"})
+    hits = counter_means("hit", {"TCC_HIT_sum", "TCC_MISS_sum"})
+    lines = [f"fetch scale {fetch_scale:.4f}, write scale {write_scale:.4f} (256 MiB copy)",
+             "",
+             "| launcher | dispatches | avg µs | algorithmic bytes | counter bytes | counter/alg | GB/s (alg) | "
+             "% of 8 TB/s | L2 hit rate | copies rotated |",
+             "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for name in names:
+        us = sum(durations[name]) / len(durations[name])
+        alg = ops[name]["bytes_per_launch"]
+        got = (fetch.get(name, {}).get("FETCH_SIZE", 0.0) * fetch_scale + write.get(name, {}).get("WRITE_SIZE", 0.0)
+               * write_scale) * 1024
+        hit = hits.get(name, {})
+        rate = hit.get("TCC_HIT_sum", 0.0) / max(1.0, hit.get("TCC_HIT_sum", 0.0) + hit.get("TCC_MISS_sum", 0.0))
+        gbs = alg / (us * 1e-6) / 1e9
+        lines.append(f"| {name} | {len(durations[name])} | {us:.2f} | {alg:,} | {got:,.0f} | {got / alg:.3f} | "
+                     f"{gbs:,.0f} | {100 * gbs / HBM_PEAK_GBS:.1f} | {rate:.3f} | {ops[name]['rotated_copies']} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -675,13 +762,21 @@ def main() -> int:
                     help="print the per-kernel table of a step's rocprofv3 runs kept under DIR "
                          "(trace/, fetch/, write/, hit/, copy_fetch/, copy_write/) and exit")
     ap.add_argument("--shape", choices=["05b", "7b"], default="05b", help="shape for --summarize-counters")
+    ap.add_argument("--summarize-ops", metavar="DIR",
+                    help="print the per-launcher table of the per-op suite's rocprofv3 runs kept under DIR "
+                         "(trace/, fetch/, write/, hit/, copy_fetch/, copy_write/, ops.json) and exit")
     ap.add_argument("--launches", type=int, default=20, help="launches for --kernel-only")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the batched-prefill figures (2048-token prompts, 0.5B and 7B shapes)")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="only the per-op launcher suite (element-wise and reduction set, GEMV suite), for rocprofv3")
     args = ap.parse_args()
 
     if args.summarize_counters:
         print(summarize_counters(pathlib.Path(args.summarize_counters), args.shape), flush=True)
+        return 0
+    if args.summarize_ops:
+        print(summarize_ops(pathlib.Path(args.summarize_ops)), flush=True)
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -697,6 +792,9 @@ def main() -> int:
     mh.load()
     if args.kernel_only:
         print(json.dumps(kernel_only(mh, torch, args.kernel_only, args.launches)), flush=True)
+        return 0
+    if args.ops_only:
+        print(json.dumps({"kernels": time_ops(mh, torch, reps=3)}), flush=True)
         return 0
     shape = dict(mh.QWEN25_05B)
     seed = 20261201
