@@ -76,12 +76,21 @@ ODD_SHAPES = {
                                      vocab=300, max_seq=40), 36),
     "kv8_merge_kernel": (dict(layers=2, hidden=512, ffn=1024, heads=16, kv_heads=8, head_dim=128, vocab=400,
                               max_seq=200), 150),
+    # The grouped o_proj's rows per wave (ceil(hidden / (2 * CUs * 4 waves / kv heads)) on a
+    # 256-CU part): 1, 4 and 8 rows, beside the 2 of qdim1280_hd64 and 7 of the 7B shape.
+    "grouped_rows1": (dict(layers=1, hidden=512, ffn=768, heads=20, kv_heads=4, head_dim=64, vocab=300,
+                           max_seq=96), 90),
+    "grouped_rows4": (dict(layers=1, hidden=2048, ffn=1024, heads=32, kv_heads=4, head_dim=64, vocab=300,
+                           max_seq=96), 64),
+    "grouped_rows8": (dict(layers=1, hidden=4096, ffn=1024, heads=32, kv_heads=4, head_dim=128, vocab=300,
+                           max_seq=64), 60),
 }
 
 
 # Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel).
 ODD_LAUNCHES = {"group8_hd128": 2 + 5, "qdim1280_hd64": 2 + 5 * 2, "hidden_1536_short_cache": 2 + 5,
-                "kv8_merge_kernel": 2 + 6 * 2}
+                "kv8_merge_kernel": 2 + 6 * 2, "grouped_rows1": 2 + 5, "grouped_rows4": 2 + 5,
+                "grouped_rows8": 2 + 5}
 
 
 @pytest.mark.parametrize("name", sorted(ODD_SHAPES))
