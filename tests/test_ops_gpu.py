@@ -282,6 +282,26 @@ def test_argmax_reference_known_answer_and_ties(mh, gpu, orc):
     assert argmax(mh, gpu, tie).tolist() == [5000, 3]
 
 
+@pytest.mark.parametrize("cols", [1, 3, 1021, 4096, 4099, 8191, 151936])
+def test_argmax_ties_across_load_batches_and_tails(mh, gpu, orc, cols):
+    """A thread keeps four float4 loads in flight, 256 float4 apart, then finishes the row one
+    float4 and one scalar at a time. Equal maxima planted in every such position (each batch
+    slot, the float4 tail, the scalar tail) must resolve to the lowest index, as the host scan's
+    strict '>' does."""
+    rng = np.random.default_rng(cols)
+    rows = 8
+    x = rng.normal(0.0, 1.0, (rows, cols)).astype(np.float32)
+    n4 = cols // 4
+    for r in range(rows):
+        candidates = {c for c in (r, 4 * 256 + r, 2 * 4 * 256 + 3, 3 * 4 * 256 + 1, 4 * 4 * 256 + 2,
+                                  4 * (n4 - 1), 4 * n4, cols - 1) if 0 <= c < cols}
+        picks = sorted(candidates)[r % max(1, len(candidates)):] or sorted(candidates)
+        x[r, picks] = 7.5
+    want = orc.argmax_rows(x)
+    assert np.array_equal(want, np.argmax(x, axis=1))
+    assert np.array_equal(argmax(mh, gpu, x), want)
+
+
 def test_argmax_batched_decode_shape(mh, gpu, orc):
     """4096 rows x 151936 logits N(0, 2): 256 rows against the oracle, all rows against torch.argmax."""
     torch = gpu
