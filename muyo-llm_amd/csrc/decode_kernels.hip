@@ -859,6 +859,9 @@ struct LmHeadEpi
     float* argValue;
     int32_t* argIndex;
     uint32_t rows, cols;
+    // Two rounds of resident workgroups, each with half the rows: 0.5B LM head 42.6 -> 41.0 us,
+    // 7B 168.4 -> 164.1 us (three rounds: no better, or slower).
+    static constexpr uint32_t kResidentRounds = 2;
 
     __device__ uint32_t Units() const { return rows; }
     __device__ const uint16_t* Row(uint32_t unit, int) const { return table + static_cast<uint64_t>(unit) * cols; }
@@ -892,6 +895,19 @@ struct LmHeadEpi
 // ------------------------------------------------------------------------------------------------
 // Launch helpers for the fused GEMV.
 
+/// Rounds of resident workgroups a GEMV's grid may span: Epi::kResidentRounds, else 1.
+template <class E, class = void>
+struct ResidentRounds
+{
+    static constexpr uint32_t value = 1;
+};
+
+template <class E>
+struct ResidentRounds<E, std::void_t<decltype(E::kResidentRounds)>>
+{
+    static constexpr uint32_t value = E::kResidentRounds;
+};
+
 /// Workgroups of `kernel` the chip holds at once with `lds` bytes of dynamic LDS each.
 template <typename Kernel>
 uint32_t ResidentBlocks(Kernel kernel, int threads, size_t lds)
@@ -906,7 +922,8 @@ uint32_t ResidentBlocks(Kernel kernel, int threads, size_t lds)
 
 /// Launches `kernel` over `units`, or with shapeOut only reports its grid. The grid
 /// holds at most the workgroups resident at once (each stages the activation once and then
-/// strides over the units), so no workgroup waits for a second round.
+/// strides over the units), so no workgroup waits for a second round; an epilogue may allow
+/// more rounds (ResidentRounds).
 template <auto kKernel, class Stage, class Epi, int kThreads = kBlock>
 hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBlock, uint32_t blockCap, size_t lds,
                             uint32_t cols, const Stage& stage, const Epi& epi, GemvShape* shapeOut)
@@ -920,7 +937,8 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
         resident = ResidentBlocks(kernel, kThreads, lds);
         residentLds = lds;
     }
-    const uint32_t blocks = std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, resident}));
+    const uint32_t blocks =
+        std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, ResidentRounds<Epi>::value * resident}));
     if (shapeOut != nullptr)
     {
         *shapeOut = GemvShape{blocks, unitsPerBlock};
@@ -987,13 +1005,16 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
         }
         // More workgroups than CUs but few enough single-wave ones that every unit gets its own
         // segment in one round: single-wave workgroups balance the CUs (a 256-thread grid of
-        // 1.2 CUs' worth leaves most CUs with one workgroup and some with two).
+        // 1.2 CUs' worth leaves most CUs with one workgroup and some with two). A norm prologue
+        // stages its row in one round, kStageVec float4 per thread: one wave holds rows of up to
+        // 2048 floats, so wider normed rows keep 256-thread workgroups.
+        constexpr bool kSmallFits = Stage::kElementwise || (kLpr * kCpl * 2 + kWave - 1) / kWave <= kStageVec;
         GemvShape smallProbe{};
         constexpr uint32_t kSmallUnits = UnitsPerWave<kLpr, kNr, kSingle>();
         (void)LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
             s, units, kSmallUnits, blockCap, lds, cols, stage, epi, &smallProbe);
         const uint32_t small = smallProbe.blocks;
-        if (static_cast<uint64_t>(small) * kSmallUnits >= units)
+        if (kSmallFits && static_cast<uint64_t>(small) * kSmallUnits >= units)
         {
             return LaunchGemvKernel<&FusedMatVec<kLpr, kCpl, kNr, kSingle, Stage, Epi, kWave>, Stage, Epi, kWave>(
                 s, units, kSmallUnits, blockCap, lds, cols, stage, epi, shapeOut);

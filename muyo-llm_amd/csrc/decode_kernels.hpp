@@ -54,7 +54,7 @@ struct DecodeScratch
     uint32_t historyCap;
 };
 
-constexpr uint32_t kArgMaxBlocks = 1024;
+constexpr uint32_t kArgMaxBlocks = 2048;
 constexpr uint32_t kMaxAttnChunks = 16;    // attention chunks per kv head, at most
 constexpr uint32_t kMergeAttnChunks = 8;   // the same when o_proj's prologue merges the partials
 constexpr uint32_t kMaxSeq = 32768;

@@ -84,13 +84,17 @@ ODD_SHAPES = {
                            max_seq=96), 64),
     "grouped_rows8": (dict(layers=1, hidden=4096, ffn=1024, heads=32, kv_heads=4, head_dim=128, vocab=300,
                            max_seq=64), 60),
+    # Normed rows wider than one wave stages (3584 floats) with few enough units (2048 gate/up
+    # rows, 2000 LM-head rows) for single-wave workgroups: those GEMVs keep 256-thread ones.
+    "wide_rows_few_units": (dict(layers=1, hidden=3584, ffn=2048, heads=28, kv_heads=4, head_dim=128,
+                                 vocab=2000, max_seq=64), 40),
 }
 
 
 # Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel).
 ODD_LAUNCHES = {"group8_hd128": 2 + 5, "qdim1280_hd64": 2 + 5 * 2, "hidden_1536_short_cache": 2 + 5,
                 "kv8_merge_kernel": 2 + 6 * 2, "grouped_rows1": 2 + 5, "grouped_rows4": 2 + 5,
-                "grouped_rows8": 2 + 5}
+                "grouped_rows8": 2 + 5, "wide_rows_few_units": 2 + 5}
 
 
 @pytest.mark.parametrize("name", sorted(ODD_SHAPES))
