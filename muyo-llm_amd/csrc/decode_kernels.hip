@@ -790,6 +790,9 @@ struct ResidualEpi
 
 struct GateUpEpi
 {
+    // Two rounds of resident workgroups (7B gate/up 44.1 -> 43.0 us; the 0.5B one covers its
+    // units in one round of single-wave workgroups either way).
+    static constexpr uint32_t kResidentRounds = 2;
     const uint16_t* gate;
     const uint16_t* up;
     float* act;
