@@ -156,6 +156,7 @@ struct MuyoDecoder
     uint16_t* pActHi = nullptr;  // [rows][ffn] swiglu output
     uint16_t* pActLo = nullptr;
     float* pPartial = nullptr;   // [kMaxGemmSplits][rows][max(qkv rows, hidden)] K-split partial sums
+    size_t pPartialFloats = 0;  // (or the split attention's partials, when larger)
 
     template <typename T>
     T* At(const TensorSlot& slot) const
@@ -1248,8 +1249,12 @@ int EnsurePrefill(MuyoDecoder* d)
     const size_t attnLo = place(rows * qdim * 2);
     const size_t actHi = place(rows * c.feedForward * 2);
     const size_t actLo = place(rows * c.feedForward * 2);
-    // K-split partial sums of the GEMMs whose tiles alone leave the chip idle (GemmSplits).
-    const size_t partial = place(kMaxGemmSplits * rows * std::max<size_t>(qkvRows, c.hidden) * 4);
+    // K-split partial sums of the GEMMs whose tiles alone leave the chip idle (GemmSplits), and,
+    // between the q|k|v and o_proj GEMMs, the split attention's key-chunk partials.
+    const size_t partialFloats = std::max(kMaxGemmSplits * rows * std::max<size_t>(qkvRows, c.hidden),
+                                          PrefillAttentionWorkspaceFloats(static_cast<uint32_t>(rows), c.heads,
+                                                                          c.headDim));
+    const size_t partial = place(partialFloats * 4);
     char* arena = nullptr;
     if (hipMalloc(reinterpret_cast<void**>(&arena), cursor) != hipSuccess)
     {
@@ -1271,6 +1276,7 @@ int EnsurePrefill(MuyoDecoder* d)
     d->pActHi = reinterpret_cast<uint16_t*>(arena + actHi);
     d->pActLo = reinterpret_cast<uint16_t*>(arena + actLo);
     d->pPartial = reinterpret_cast<float*>(arena + partial);
+    d->pPartialFloats = partialFloats;
     return MUYO_OK;
 }
 
@@ -1315,9 +1321,11 @@ int EnqueuePrefillPass(MuyoDecoder* d, hipStream_t s, uint32_t rows, int32_t pos
         {
             return LaunchFailed(status, "prefill rope", l);
         }
+        // The q|k|v partials are consumed (rope) and o_proj's are not yet written: the split
+        // attention keeps its key-chunk partials in the same buffer meanwhile.
         if ((status = LaunchPrefillAttention(s, d->pQHi, d->pQLo, kcache, vcache, d->pAttnHi, d->pAttnLo, rows, pos0,
-                                             c.heads, c.kvHeads, c.headDim, c.maxSeq, d->dims.attnScale)) !=
-            hipSuccess)
+                                             c.heads, c.kvHeads, c.headDim, c.maxSeq, d->dims.attnScale,
+                                             d->pPartial, d->pPartialFloats)) != hipSuccess)
         {
             return LaunchFailed(status, "prefill attention", l);
         }

@@ -598,19 +598,97 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
 //   v % 4 of the tile, and the V^T fragment reads the same keys (two 8-byte LDS reads).
 
 constexpr int kAttnKeys = 32;
+constexpr uint32_t kAttnChunkTiles = 16;  // key tiles per chunk of a split query tile, at least
+
+/// Key tiles (of kAttnKeys) a query tile attends to: cache rows 0 .. its last query's position.
+__host__ __device__ inline uint32_t AttnKeyTiles(uint32_t qtile, uint32_t rows, int32_t pos0)
+{
+    const uint32_t last = qtile * 32 + 31 < rows ? qtile * 32 + 31 : rows - 1;
+    return (static_cast<uint32_t>(pos0) + last) / kAttnKeys + 1;
+}
+
+/// Work items of the split prefill attention, passed by value in the kernel arguments.
+struct AttnWork
+{
+    uint32_t count;       // items; 0: one item per query tile over all of its keys
+    uint32_t chunkTiles;  // key tiles per chunk
+    uint16_t tile[kAttnMaxItems];
+    uint8_t chunk[kAttnMaxItems];
+};
+
+/// Softmax partials of the chunks of split tiles: [kAttnMaxChunks][rows][heads] (running max in
+/// natural-log units, sum) and [kAttnMaxChunks][rows][heads][headDim] (unnormalised P.V).
+struct AttnPartials
+{
+    float* max;
+    float* sum;
+    float* acc;
+};
+
+/// Combines the chunk partials of the split tiles' queries into their output planes: out = sum_c
+/// e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c, M the largest m_c (a chunk with no key of the query
+/// weighs 0). A thread per (query, head, 4 channels); queries of unsplit tiles are left alone.
+__global__ __launch_bounds__(256) void PrefillAttnMergeKernel(AttnPartials part, uint16_t* __restrict__ ohi,
+                                                              uint16_t* __restrict__ olo, uint32_t rows, int32_t pos0,
+                                                              uint32_t heads, uint32_t headDim, uint32_t chunkTiles)
+{
+    const uint32_t quads = headDim / 4;
+    const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i >= static_cast<uint64_t>(rows) * heads * quads)
+    {
+        return;
+    }
+    const uint32_t channel = static_cast<uint32_t>(i % quads) * 4;
+    const uint32_t head = static_cast<uint32_t>(i / quads % heads);
+    const uint32_t m = static_cast<uint32_t>(i / quads / heads);
+    const uint32_t keyTiles = AttnKeyTiles(m / 32, rows, pos0);
+    if (keyTiles <= chunkTiles)
+    {
+        return;
+    }
+    const uint32_t chunks = (keyTiles + chunkTiles - 1) / chunkTiles;
+    float top = -INFINITY;
+    for (uint32_t c = 0; c < chunks; ++c)
+    {
+        top = fmaxf(top, part.max[(static_cast<uint64_t>(c) * rows + m) * heads + head]);
+    }
+    float den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t c = 0; c < chunks; ++c)
+    {
+        const uint64_t at = (static_cast<uint64_t>(c) * rows + m) * heads + head;
+        const float mc = part.max[at];
+        const float w = mc == -INFINITY ? 0.0f : expf(mc - top);
+        const float4 a = *reinterpret_cast<const float4*>(part.acc + at * headDim + channel);
+        den = fmaf(w, part.sum[at], den);
+        num.x = fmaf(w, a.x, num.x);
+        num.y = fmaf(w, a.y, num.y);
+        num.z = fmaf(w, a.z, num.z);
+        num.w = fmaf(w, a.w, num.w);
+    }
+    const float inv = 1.0f / den;
+    StoreSplit4(ohi, olo, static_cast<uint64_t>(m) * heads * headDim + head * headDim + channel, num.x * inv,
+                num.y * inv, num.z * inv, num.w * inv);
+}
 // Halves per transposed V row. The even lane of each key pair stores both keys of a channel as one
 // 4-byte word, so the 16 storing lanes of a channel chunk write 64 contiguous bytes; 36 halves
 // (18 words) put the two chunks a wave stores at once 16 banks apart, and the MFMA fragment reads
 // of 32 consecutive rows (8 bytes each, 18 words apart) cover every bank once.
 constexpr int kVStride = kAttnKeys + 4;
 
-/// Grid (head splits, query tiles, kv heads): the splits of one tile are dispatched together and
-/// the longest tiles first.
+/// Grid (head splits, work items, kv heads): the splits of one item are dispatched together.
+/// Without work items (work.count 0) item y is query tile tiles - 1 - y over all of its keys (the
+/// longest tiles first) and writes the output planes. With them, item y is query tile
+/// work.tile[y] over key tiles [c * C, (c + 1) * C) of its range (c = work.chunk[y],
+/// C = work.chunkTiles); a tile split over several chunks leaves each chunk's unnormalised
+/// softmax partial (running max, sum, P.V) in slot c of `part` for PrefillAttnMergeKernel, a tile
+/// of one chunk writes its planes directly. A causal tile's key range grows with its position, so
+/// the split evens the workgroups' work: a 2048-token prompt is 64 tiles of 1..64 key tiles.
 template <int kHd, int kHeadsPerBlock>
 __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel(
     const uint16_t* __restrict__ qhi, const uint16_t* __restrict__ qlo, const uint16_t* __restrict__ kcache,
     const uint16_t* __restrict__ vcache, uint16_t* __restrict__ ohi, uint16_t* __restrict__ olo, uint32_t rows,
-    int32_t pos0, uint32_t heads, uint32_t kvHeads, uint32_t maxSeq, float scale)
+    int32_t pos0, uint32_t heads, uint32_t kvHeads, uint32_t maxSeq, float scale, AttnWork work, AttnPartials part)
 {
     constexpr int kKStride = kHd + 8;
     constexpr int kChunks = kHd / 8;
@@ -620,8 +698,8 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
     __shared__ __attribute__((aligned(16))) uint16_t vTile[kHd * kVStride];
 
     const uint32_t group = heads / kvHeads;
-    const uint32_t tiles = gridDim.y;
-    const uint32_t qtile = tiles - 1 - blockIdx.y;  // longest rows first
+    const bool itemized = work.count > 0;
+    const uint32_t qtile = itemized ? work.tile[blockIdx.y] : gridDim.y - 1 - blockIdx.y;  // longest first
     const uint32_t g = blockIdx.z;
     const uint32_t wave = threadIdx.x / kWave;
     const uint32_t lane = threadIdx.x % kWave;
@@ -634,7 +712,11 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
     const uint32_t mq = m0 + lane % 32 < rows ? m0 + lane % 32 : rows - 1;
     const int32_t qpos = pos0 + static_cast<int32_t>(mq);
     const int32_t lastPos = pos0 + static_cast<int32_t>(m0 + 31 < rows ? m0 + 31 : rows - 1);
-    const uint32_t keyTiles = static_cast<uint32_t>(lastPos) / kAttnKeys + 1;
+    const uint32_t keyTiles = AttnKeyTiles(qtile, rows, pos0);
+    const uint32_t chunk = itemized ? work.chunk[blockIdx.y] : 0;
+    const uint32_t ktBegin = itemized ? chunk * work.chunkTiles : 0;
+    const uint32_t ktEnd = itemized ? min(keyTiles, ktBegin + work.chunkTiles) : keyTiles;
+    const bool partial = itemized && keyTiles > work.chunkTiles;  // the tile spans several chunks
 
     half8 qh[kHd / 16], ql[kHd / 16];
     {
@@ -670,8 +752,8 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
             vReg[i] = *reinterpret_cast<const half8*>(vBase + static_cast<uint64_t>(key) * kHd + cc * 8);
         }
     };
-    loadTile(0);
-    for (uint32_t kt = 0; kt < keyTiles; ++kt)
+    loadTile(ktBegin);
+    for (uint32_t kt = ktBegin; kt < ktEnd; ++kt)
     {
         __syncthreads();  // every wave is done with the previous tile
 #pragma unroll
@@ -715,7 +797,7 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
             }
         }
         __syncthreads();
-        if (kt + 1 < keyTiles)
+        if (kt + 1 < ktEnd)
         {
             loadTile(kt + 1);  // in flight while this tile is multiplied
         }
@@ -743,13 +825,16 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
             tileMax = fmaxf(tileMax, p[r]);
         }
         tileMax = fmaxf(tileMax, __shfl_xor(tileMax, 32));
-        const float newMax = fmaxf(runMax, tileMax);  // finite: key 0 is in every query's range
-        const float factor = expf(runMax - newMax);
+        // Finite over a query's whole range (key 0 is in it), but a chunk of a split tile may hold
+        // no key of a query yet: then nothing accumulates (factor 1, weights 0).
+        const float newMax = fmaxf(runMax, tileMax);
+        const bool none = newMax == -INFINITY;
+        const float factor = none ? 1.0f : expf(runMax - newMax);
         float sum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
         {
-            p[r] = expf(p[r] - newMax);
+            p[r] = none ? 0.0f : expf(p[r] - newMax);
             sum += p[r];
         }
         runSum = runSum * factor + sum;
@@ -789,7 +874,29 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
 
     const float total = runSum + __shfl_xor(runSum, 32);
     const uint32_t m = m0 + lane % 32;
-    if (active && m < rows)
+    if (active && m < rows && partial)
+    {
+        // Slot `chunk`: the running max and sum of the query (both halves of the wave agree on
+        // the max; their sums are added), and its unnormalised P.V.
+        const uint64_t at = (static_cast<uint64_t>(chunk) * rows + m) * heads + head;
+        if (h == 0)
+        {
+            part.max[at] = runMax;
+            part.sum[at] = total;
+        }
+#pragma unroll
+        for (int c = 0; c < kHd / 32; ++c)
+        {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+            {
+                const uint32_t channel = c * 32 + 8 * q + 4 * h;
+                *reinterpret_cast<float4*>(part.acc + at * kHd + channel) =
+                    make_float4(o[c][4 * q], o[c][4 * q + 1], o[c][4 * q + 2], o[c][4 * q + 3]);
+            }
+        }
+    }
+    else if (active && m < rows)
     {
         const float inv = 1.0f / total;
         const uint64_t base = static_cast<uint64_t>(m) * qdim + head * kHd;
@@ -928,7 +1035,8 @@ hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows,
 
 hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint16_t* qlo, const uint16_t* kcache,
                                   const uint16_t* vcache, uint16_t* ohi, uint16_t* olo, uint32_t rows, int32_t pos0,
-                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale)
+                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale,
+                                  float* workspace, size_t workspaceFloats)
 {
     if (rows == 0 || kvHeads == 0 || heads % kvHeads != 0 || heads / kvHeads > 8 || pos0 < 0 ||
         static_cast<uint64_t>(pos0) + rows > maxSeq)
@@ -946,16 +1054,53 @@ hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint
     {
         cus = 256;
     }
-    const bool fills = static_cast<uint64_t>(CeilDiv(rows, 32)) * kvHeads >= static_cast<uint64_t>(cus);
+    const uint32_t tiles = CeilDiv(rows, 32);
+    const bool fills = static_cast<uint64_t>(tiles) * kvHeads >= static_cast<uint64_t>(cus);
     const uint32_t perBlock = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 || !fills ? 4 : 8;
-    const dim3 grid(CeilDiv(group, perBlock), CeilDiv(rows, 32), kvHeads);
+    // Split the long tiles' key ranges into chunks of at least kAttnChunkTiles key tiles (and at
+    // most kAttnMaxChunks per tile), items ordered longest first.
+    AttnWork work{};
+    AttnPartials part{};
+    const uint32_t longest = AttnKeyTiles(tiles - 1, rows, pos0);
+    const uint32_t chunkTiles = std::max(kAttnChunkTiles, CeilDiv(longest, kAttnMaxChunks));
+    if (workspace != nullptr && workspaceFloats >= PrefillAttentionWorkspaceFloats(rows, heads, headDim) &&
+        longest > chunkTiles)
+    {
+        work.chunkTiles = chunkTiles;
+        for (uint32_t len = chunkTiles; len > 0 && work.count < kAttnMaxItems; --len)
+        {
+            for (uint32_t t = tiles; t-- > 0;)
+            {
+                const uint32_t keyTiles = AttnKeyTiles(t, rows, pos0);
+                for (uint32_t c = 0; c * chunkTiles < keyTiles; ++c)
+                {
+                    if (std::min(chunkTiles, keyTiles - c * chunkTiles) == len && work.count < kAttnMaxItems)
+                    {
+                        work.tile[work.count] = static_cast<uint16_t>(t);
+                        work.chunk[work.count] = static_cast<uint8_t>(c);
+                        ++work.count;
+                    }
+                }
+            }
+        }
+        const size_t stats = static_cast<size_t>(kAttnMaxChunks) * rows * heads;
+        part = AttnPartials{workspace, workspace + stats, workspace + 2 * stats};
+    }
+    const dim3 grid(CeilDiv(group, perBlock), work.count > 0 ? work.count : tiles, kvHeads);
     const dim3 block(kWave * perBlock);
-#define MUYO_PREFILL_ATTENTION(HD, P)                                                                        \
-    if (headDim == HD && perBlock == P)                                                                      \
-    {                                                                                                        \
-        hipLaunchKernelGGL((PrefillAttentionKernel<HD, P>), grid, block, 0, s, qhi, qlo, kcache, vcache, ohi, \
-                           olo, rows, pos0, heads, kvHeads, maxSeq, scale);                                  \
-        return hipGetLastError();                                                                            \
+#define MUYO_PREFILL_ATTENTION(HD, P)                                                                         \
+    if (headDim == HD && perBlock == P)                                                                       \
+    {                                                                                                         \
+        hipLaunchKernelGGL((PrefillAttentionKernel<HD, P>), grid, block, 0, s, qhi, qlo, kcache, vcache, ohi,  \
+                           olo, rows, pos0, heads, kvHeads, maxSeq, scale, work, part);                       \
+        if (work.count == 0)                                                                                  \
+        {                                                                                                     \
+            return hipGetLastError();                                                                         \
+        }                                                                                                     \
+        const uint64_t threads = static_cast<uint64_t>(rows) * heads * (headDim / 4);                         \
+        hipLaunchKernelGGL(PrefillAttnMergeKernel, dim3(static_cast<uint32_t>(CeilDiv(threads, 256))),        \
+                           dim3(256), 0, s, part, ohi, olo, rows, pos0, heads, headDim, work.chunkTiles);      \
+        return hipGetLastError();                                                                             \
     }
     MUYO_PREFILL_ATTENTION(64, 1)
     MUYO_PREFILL_ATTENTION(64, 2)

@@ -29,6 +29,14 @@ hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_
 
 /// Most K splits of a prefill GEMM.
 constexpr uint32_t kMaxGemmSplits = 4;
+constexpr uint32_t kAttnMaxChunks = 8;    // key chunks a split prefill-attention query tile takes at most
+constexpr uint32_t kAttnMaxItems = 512;   // work items of one split attention launch (64 tiles x 8)
+
+/// Floats of the workspace the split prefill attention needs for `rows` queries.
+inline size_t PrefillAttentionWorkspaceFloats(uint32_t rows, uint32_t heads, uint32_t headDim)
+{
+    return static_cast<size_t>(kAttnMaxChunks) * rows * heads * (headDim + 2);
+}
 
 /// K splits for a GEMM of this shape: more than one when its output tiles alone leave most SIMDs
 /// without a wave (the 0.5B shape's q|k|v, o_proj and down at 2048 rows).
@@ -65,8 +73,11 @@ hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows,
                                  uint32_t splits = 1, const float* bias = nullptr);
 
 /// Causal attention of the queries at positions pos0 + m (m < rows) over cache rows 0..pos0 + m:
-/// out[m][h * headDim + c] as hi/lo planes [rows][heads * headDim].
+/// out[m][h * headDim + c] as hi/lo planes [rows][heads * headDim]. With a workspace of at least
+/// PrefillAttentionWorkspaceFloats floats, query tiles with long key ranges are split into key
+/// chunks run by separate workgroups and merged by a second kernel.
 hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint16_t* qlo, const uint16_t* kcache,
                                   const uint16_t* vcache, uint16_t* ohi, uint16_t* olo, uint32_t rows, int32_t pos0,
-                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale);
+                                  uint32_t heads, uint32_t kvHeads, uint32_t headDim, uint32_t maxSeq, float scale,
+                                  float* workspace = nullptr, size_t workspaceFloats = 0);
 }  // namespace muyo
