@@ -453,6 +453,18 @@ int muyo_rope_split_append_f16kv(const float* qkv, uint32_t rows, int32_t pos0, 
 int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, const void* kcache, const void* vcache,
                                  void* out_hi, void* out_lo, uint32_t rows, int32_t pos0, uint32_t heads,
                                  uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq, float scale, void* stream);
+/* muyo_prefill_attention_f16kv with a caller-owned workspace (16-byte aligned, at least
+ * muyo_prefill_attention_workspace_bytes(rows, heads, head_dim) bytes, no clearing needed): query
+ * tiles (32 queries) whose causal range is longer than 512 keys are split into key chunks run by
+ * separate workgroups, and a second kernel combines their softmax partials. The same results to
+ * f32 rounding. A prompt whose chunks would exceed 512 work items (past about 4096 queries)
+ * runs unsplit. muyo_decoder_prefill runs this path.
+ * Calls that overlap in time need their own workspaces. */
+size_t muyo_prefill_attention_workspace_bytes(uint32_t rows, uint32_t heads, uint32_t head_dim); /* 0: unsupported */
+int muyo_prefill_attention_f16kv_ws(const void* q_hi, const void* q_lo, const void* kcache, const void* vcache,
+                                    void* out_hi, void* out_lo, uint32_t rows, int32_t pos0, uint32_t heads,
+                                    uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq, float scale,
+                                    void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * Token sampling on the device. Replaces the reference's host sampler, muyo_llm::Sampler

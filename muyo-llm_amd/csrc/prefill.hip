@@ -1058,13 +1058,19 @@ hipError_t LaunchPrefillAttention(hipStream_t s, const uint16_t* qhi, const uint
     const bool fills = static_cast<uint64_t>(tiles) * kvHeads >= static_cast<uint64_t>(cus);
     const uint32_t perBlock = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 || !fills ? 4 : 8;
     // Split the long tiles' key ranges into chunks of at least kAttnChunkTiles key tiles (and at
-    // most kAttnMaxChunks per tile), items ordered longest first.
+    // most kAttnMaxChunks per tile), items ordered longest first. Prompts whose chunks would not
+    // fit kAttnMaxItems (past 2048 queries) run unsplit.
     AttnWork work{};
     AttnPartials part{};
     const uint32_t longest = AttnKeyTiles(tiles - 1, rows, pos0);
     const uint32_t chunkTiles = std::max(kAttnChunkTiles, CeilDiv(longest, kAttnMaxChunks));
+    uint64_t items = 0;
+    for (uint32_t t = 0; t < tiles; ++t)
+    {
+        items += CeilDiv(AttnKeyTiles(t, rows, pos0), chunkTiles);
+    }
     if (workspace != nullptr && workspaceFloats >= PrefillAttentionWorkspaceFloats(rows, heads, headDim) &&
-        longest > chunkTiles)
+        longest > chunkTiles && items <= kAttnMaxItems)
     {
         work.chunkTiles = chunkTiles;
         for (uint32_t len = chunkTiles; len > 0 && work.count < kAttnMaxItems; --len)
@@ -1249,12 +1255,12 @@ extern "C" int muyo_rope_split_append_f16kv(const float* qkv, uint32_t rows, int
                     name);
 }
 
-extern "C" int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, const void* kcache,
-                                            const void* vcache, void* out_hi, void* out_lo, uint32_t rows,
-                                            int32_t pos0, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
-                                            uint32_t max_seq, float scale, void* stream)
+namespace
 {
-    const char* name = "prefill_attention_f16kv";
+int CheckPrefillAttentionArgs(const char* name, const void* q_hi, const void* q_lo, const void* kcache,
+                              const void* vcache, const void* out_hi, const void* out_lo, uint32_t rows, int32_t pos0,
+                              uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t max_seq)
+{
     if (q_hi == nullptr || q_lo == nullptr || kcache == nullptr || vcache == nullptr || out_hi == nullptr ||
         out_lo == nullptr)
     {
@@ -1275,10 +1281,62 @@ extern "C" int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, 
     {
         return Fail(MUYO_E_CONTRACT, "%s: every buffer must be 16-byte aligned", name);
     }
+    return MUYO_OK;
+}
+}  // namespace
+
+extern "C" int muyo_prefill_attention_f16kv(const void* q_hi, const void* q_lo, const void* kcache,
+                                            const void* vcache, void* out_hi, void* out_lo, uint32_t rows,
+                                            int32_t pos0, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                            uint32_t max_seq, float scale, void* stream)
+{
+    const char* name = "prefill_attention_f16kv";
+    const int args = CheckPrefillAttentionArgs(name, q_hi, q_lo, kcache, vcache, out_hi, out_lo, rows, pos0, heads,
+                                               kv_heads, head_dim, max_seq);
+    if (args != MUYO_OK)
+    {
+        return args;
+    }
     return Launched(LaunchPrefillAttention(AsStream(stream), static_cast<const uint16_t*>(q_hi),
                                            static_cast<const uint16_t*>(q_lo), static_cast<const uint16_t*>(kcache),
                                            static_cast<const uint16_t*>(vcache), static_cast<uint16_t*>(out_hi),
                                            static_cast<uint16_t*>(out_lo), rows, pos0, heads, kv_heads, head_dim,
                                            max_seq, scale),
+                    name);
+}
+
+extern "C" size_t muyo_prefill_attention_workspace_bytes(uint32_t rows, uint32_t heads, uint32_t head_dim)
+{
+    if (rows == 0 || heads == 0 || (head_dim != 64 && head_dim != 128))
+    {
+        return 0;
+    }
+    return PrefillAttentionWorkspaceFloats(rows, heads, head_dim) * sizeof(float);
+}
+
+extern "C" int muyo_prefill_attention_f16kv_ws(const void* q_hi, const void* q_lo, const void* kcache,
+                                               const void* vcache, void* out_hi, void* out_lo, uint32_t rows,
+                                               int32_t pos0, uint32_t heads, uint32_t kv_heads, uint32_t head_dim,
+                                               uint32_t max_seq, float scale, void* workspace,
+                                               uint64_t workspace_bytes, void* stream)
+{
+    const char* name = "prefill_attention_f16kv_ws";
+    const int args = CheckPrefillAttentionArgs(name, q_hi, q_lo, kcache, vcache, out_hi, out_lo, rows, pos0, heads,
+                                               kv_heads, head_dim, max_seq);
+    if (args != MUYO_OK)
+    {
+        return args;
+    }
+    const size_t floats = PrefillAttentionWorkspaceFloats(rows, heads, head_dim);
+    if (workspace == nullptr || !Aligned16(workspace) || workspace_bytes < floats * sizeof(float))
+    {
+        return Fail(MUYO_E_CONTRACT, "%s: needs a 16-byte aligned workspace of %zu bytes (got %llu)", name,
+                    floats * sizeof(float), static_cast<unsigned long long>(workspace_bytes));
+    }
+    return Launched(LaunchPrefillAttention(AsStream(stream), static_cast<const uint16_t*>(q_hi),
+                                           static_cast<const uint16_t*>(q_lo), static_cast<const uint16_t*>(kcache),
+                                           static_cast<const uint16_t*>(vcache), static_cast<uint16_t*>(out_hi),
+                                           static_cast<uint16_t*>(out_lo), rows, pos0, heads, kv_heads, head_dim,
+                                           max_seq, scale, static_cast<float*>(workspace), floats),
                     name);
 }

@@ -203,6 +203,9 @@ _SIGNATURES = {
     "muyo_gemm_swiglu_split_f16": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, u32, vp]),
     "muyo_rope_split_append_f16kv": (ctypes.c_int, [vp, u32, i32, u32, u32, u32, u32, vp, vp, vp, vp, vp, vp]),
     "muyo_prefill_attention_f16kv": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, i32, u32, u32, u32, u32, f32, vp]),
+    "muyo_prefill_attention_workspace_bytes": (ctypes.c_size_t, [u32, u32, u32]),
+    "muyo_prefill_attention_f16kv_ws": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, u32, i32, u32, u32, u32, u32, f32, vp,
+                                                       u64, vp]),
     "muyo_tokenizer_create": (ctypes.c_int, [vp, ctypes.POINTER(vp)]),
     "muyo_tokenizer_destroy": (None, [vp]),
     "muyo_tokenizer_vocab_size": (ctypes.c_uint64, [vp]),

@@ -234,7 +234,7 @@ def test_rope_split_append_matches_oracle(mh, gpu, orc, heads, kv_heads, head_di
 
 
 def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, seed, check=None,
-                           poison=False):
+                           poison=False, split=False):
     q = orc.normal_f32(rows * heads * head_dim, seed).reshape(rows, heads * head_dim)
     kc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 1).reshape(kv_heads, max_seq, head_dim)
     vc = orc.normal_f16(kv_heads * max_seq * head_dim, seed + 2).reshape(kv_heads, max_seq, head_dim)
@@ -248,9 +248,18 @@ def prefill_attention_case(mh, torch, orc, heads, kv_heads, head_dim, rows, pos0
     ohi, olo = planes(torch, (rows, heads * head_dim))
     scale = 1.0 / math.sqrt(head_dim)
     keep = [dev(torch, qhi), dev(torch, qlo), dev(torch, kc), dev(torch, vc)]
-    run(mh, torch, mh.load().muyo_prefill_attention_f16kv(*(t.data_ptr() for t in keep),
-                                                          ohi.data_ptr(), olo.data_ptr(), rows, pos0, heads,
-                                                          kv_heads, head_dim, max_seq, scale, stream(torch)))
+    lib = mh.load()
+    if split:
+        # The workspace starts as NaN: the merge must read only slots the chunks wrote.
+        size = lib.muyo_prefill_attention_workspace_bytes(rows, heads, head_dim)
+        ws = torch.full((size // 4,), float("nan"), dtype=torch.float32, device="cuda")
+        run(mh, torch, lib.muyo_prefill_attention_f16kv_ws(*(t.data_ptr() for t in keep), ohi.data_ptr(),
+                                                           olo.data_ptr(), rows, pos0, heads, kv_heads, head_dim,
+                                                           max_seq, scale, ws.data_ptr(), size, stream(torch)))
+    else:
+        run(mh, torch, lib.muyo_prefill_attention_f16kv(*(t.data_ptr() for t in keep), ohi.data_ptr(),
+                                                        olo.data_ptr(), rows, pos0, heads, kv_heads, head_dim,
+                                                        max_seq, scale, stream(torch)))
     got = joined(ohi, olo)
     assert np.isfinite(got).all()
     for m in (range(rows) if check is None else check):
@@ -291,6 +300,37 @@ def test_prefill_attention_ignores_rows_past_the_prompt(mh, gpu, orc, heads, kv_
     """The last key tile covers cache rows past the prompt's last position; NaN and infinity there
     must not reach any query's output (a weight of 0 times NaN is NaN)."""
     prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, 3 + rows, poison=True)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rows,pos0,max_seq,check", [
+    (14, 2, 64, 512, 0, 512, None),         # last tile exactly 16 key tiles: nothing split
+    (14, 2, 64, 513, 0, 544, None),         # one query past it: a 16 + 1 split of the last tile
+    (14, 2, 64, 600, 0, 640, None),         # tiles 16..18 in two chunks
+    (14, 2, 64, 40, 1000, 2048, None),      # after an earlier prompt: every tile split in three
+    (28, 4, 128, 33, 2015, 2048, None),     # 7B heads, ending at the last cache row: four chunks
+    (8, 1, 128, 64, 1100, 1200, None),      # a full group of 8 over a ragged cache
+    (4, 4, 64, 96, 8000, 8192, range(0, 96, 5)),  # 251+ key tiles: chunks of 32 key tiles, eight per tile
+    (14, 2, 64, 2048, 0, 2048, [0, 31, 511, 512, 543, 544, 1000, 1535, 1536, 2046, 2047]),
+    (28, 4, 128, 2048, 0, 2048, [0, 33, 512, 1023, 1024, 1500, 2015, 2016, 2047]),
+    (14, 2, 64, 2100, 0, 2112, [0, 2047, 2048, 2099]),  # past the decoder's 2048-row passes: 170 items
+    (14, 2, 64, 4160, 0, 4160, [0, 2047, 3000, 4159]),  # its chunks would be 564 work items: runs unsplit
+])
+def test_prefill_attention_key_chunks_match_per_token_attention(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0,
+                                                               max_seq, check):
+    """Query tiles split into key chunks, combined by the merge kernel, against the oracle's
+    attention of each query."""
+    prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, 11 + rows + pos0, check,
+                           split=True)
+
+
+@pytest.mark.parametrize("heads,kv_heads,head_dim,rows,pos0,max_seq", [
+    (14, 2, 64, 600, 30, 1024),     # the split tiles' last key tile mostly past the prompt
+    (28, 4, 128, 40, 1000, 2048),
+])
+def test_prefill_attention_key_chunks_ignore_rows_past_the_prompt(mh, gpu, orc, heads, kv_heads, head_dim, rows,
+                                                                  pos0, max_seq):
+    prefill_attention_case(mh, gpu, orc, heads, kv_heads, head_dim, rows, pos0, max_seq, 5 + rows, poison=True,
+                           split=True)
 
 
 def test_prefill_attention_refusals(mh, gpu):
