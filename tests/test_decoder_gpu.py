@@ -88,13 +88,20 @@ ODD_SHAPES = {
     # rows, 2000 LM-head rows) for single-wave workgroups: those GEMVs keep 256-thread ones.
     "wide_rows_few_units": (dict(layers=1, hidden=3584, ffn=2048, heads=28, kv_heads=4, head_dim=128,
                                  vocab=2000, max_seq=64), 40),
+    # Long caches: attention rounds past the first (which covers 2048 rows), 128 key blocks per
+    # chunk merged in o_proj at head_dim 64, 64 per chunk over 16 chunks merged per kv group.
+    "long_cache_32k_hd64": (dict(layers=1, hidden=256, ffn=512, heads=4, kv_heads=2, head_dim=64, vocab=300,
+                                 max_seq=32768), 32760),
+    "long_cache_16k_grouped_hd128": (dict(layers=1, hidden=512, ffn=512, heads=12, kv_heads=4, head_dim=128,
+                                          vocab=300, max_seq=16384), 16000),
 }
 
 
 # Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel).
 ODD_LAUNCHES = {"group8_hd128": 2 + 5, "qdim1280_hd64": 2 + 5 * 2, "hidden_1536_short_cache": 2 + 5,
                 "kv8_merge_kernel": 2 + 6 * 2, "grouped_rows1": 2 + 5, "grouped_rows4": 2 + 5,
-                "grouped_rows8": 2 + 5, "wide_rows_few_units": 2 + 5}
+                "grouped_rows8": 2 + 5, "wide_rows_few_units": 2 + 5, "long_cache_32k_hd64": 2 + 5,
+                "long_cache_16k_grouped_hd128": 2 + 5}
 
 
 @pytest.mark.parametrize("name", sorted(ODD_SHAPES))

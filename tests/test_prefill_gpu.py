@@ -414,6 +414,15 @@ def test_decoder_prefill_odd_shapes(mh, gpu, orc, name):
         check_against_oracle(dec, model, orc, shape, prompt(orc, shape["max_seq"] - 5, shape["vocab"], 52), 0)
 
 
+def test_decoder_prefill_after_long_cache(mh, gpu, orc):
+    """A 100-token prompt appended at cache row 15000 of 16384 (o_proj per kv group at head_dim
+    128): each query tile's 470-472 key tiles split into eight chunks and merged."""
+    shape = dict(layers=1, hidden=512, ffn=512, heads=12, kv_heads=4, head_dim=128, vocab=300, max_seq=16384)
+    dec, model = make_pair(mh, orc, shape, seed=53, kv_positions=15000, kv_seed=54)
+    with dec:
+        check_against_oracle(dec, model, orc, shape, prompt(orc, 100, shape["vocab"], 55), 15000)
+
+
 def test_decoder_prefill_05b_prompt_then_greedy(mh, gpu, orc, capsys):
     """Qwen2.5-0.5B shape: a 96-token prompt from row 0, then 16 greedy tokens, against the oracle
     fed token by token."""
