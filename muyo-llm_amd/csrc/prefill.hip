@@ -550,11 +550,12 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1
     epi.Finish(acc, n0 + wn * 32 * kNb, m0 + wm * 64, rows);
 }
 
-/// 128 x 128 tiles when they, with the K splits, give two workgroups per CU; 64-token tiles
-/// otherwise.
+/// 128 x 128 tiles when they, with the K splits, give two workgroups per CU, or unsplit fill at
+/// least seven eighths of that (448 of 512 on 256 CUs); 64-token tiles otherwise.
 bool BigTiles(uint32_t rows, uint32_t virtualRows, uint32_t splits = 1)
 {
-    return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128) * splits >= 512;
+    const uint64_t tiles = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 128);
+    return tiles * splits >= 512 || (splits == 1 && tiles * 8 >= 512 * 7);
 }
 
 /// 128-token x 256-row tiles (a wave 64 tokens x 128 rows, two workgroups per CU) when they give
@@ -985,6 +986,13 @@ uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k)
     if (bigTiles >= 512)
     {
         return bigTiles < 1024 && halves ? 2 : 1;
+    }
+    // At least seven eighths of one round: unsplit. K halves would add partial planes that the
+    // next norm sums (7B o_proj and down, 448 tiles: the two norms 36.6 -> 17.9 us, the GEMMs
+    // unchanged).
+    if (bigTiles * 8 >= 512 * 7)
+    {
+        return 1;
     }
     // 128 x 128 tiles over two K halves, where that grid fills two workgroups per CU.
     if (bigTiles * 2 >= 512 && halves)
