@@ -256,10 +256,11 @@ struct PlainEpi
     uint32_t n, k;
     float* partial = nullptr;
 
-    __device__ const uint16_t* WRow(uint32_t row) const
-    {
-        return w + static_cast<uint64_t>(row < n ? row : n - 1) * k;
-    }
+    /// Weight rows u + r (r < 16 or 32, u a multiple of that): row u's index and address, uniform
+    /// across the workgroup (clamped to the last row); row u + r is r * k elements on.
+    __device__ uint32_t WFirst(uint32_t u) const { return u; }
+    __device__ uint32_t WCount() const { return n; }
+    __device__ const uint16_t* WRows(uint32_t u) const { return w + static_cast<uint64_t>(min(u, n - 1)) * k; }
 
     template <int kNb>
     __device__ void Finish(const floatx16 (&acc)[kNb][2], uint32_t n0, uint32_t m0, uint32_t rows) const
@@ -327,11 +328,14 @@ struct SwiGluEpi
     uint16_t* hlo;
     uint32_t ffn, k;
 
-    __device__ const uint16_t* WRow(uint32_t row) const
+    /// Virtual rows u + r (r < 16 or 32, u a multiple of that) are gate or up rows f + r of one
+    /// matrix, f = (u / 64) * 32 + u % 32: uniform across the workgroup (the address clamped to
+    /// the last row).
+    __device__ uint32_t WFirst(uint32_t u) const { return (u / 64) * 32 + u % 32; }
+    __device__ uint32_t WCount() const { return ffn; }
+    __device__ const uint16_t* WRows(uint32_t u) const
     {
-        const uint32_t f = (row / 64) * 32 + row % 32;
-        const uint64_t offset = static_cast<uint64_t>(f < ffn ? f : ffn - 1) * k;
-        return (row % 64 < 32 ? gate : up) + offset;
+        return (u % 64 < 32 ? gate : up) + static_cast<uint64_t>(min(WFirst(u), ffn - 1)) * k;
     }
 
     /// Blocks 2p and 2p + 1 of a wave's kNb are the gate and up rows of the same 32 f.
@@ -402,34 +406,18 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1
     const uint32_t m0 = (mFast != 0 ? linear % gridDim.y : blockIdx.y) * kBM;
     const uint32_t n0 = (mFast != 0 ? linear / gridDim.y : blockIdx.x) * kBN;
 
-    const uint16_t* aSrc[kALoads];
-    uint32_t aDst[kALoads];
-    uint32_t aCol[kALoads];
-#pragma unroll
-    for (int i = 0; i < kALoads; ++i)
-    {
-        const uint32_t c = tid + i * kThreads;
-        const uint32_t plane = c / (kBM * kChunks);
-        const uint32_t row = (c / kChunks) % kBM;
-        const uint32_t cc = c % kChunks;
-        const uint32_t m = m0 + row < rows ? m0 + row : rows - 1;
-        aSrc[i] = (plane == 0 ? ahi : alo) + static_cast<uint64_t>(m) * k + cc * 8;
-        aDst[i] = (plane * kBM + row) * kGemmStride + cc * 8;
-        aCol[i] = cc * 8;
-    }
-    const uint16_t* wSrc[kWLoads];
-    uint32_t wDst[kWLoads];
-    uint32_t wCol[kWLoads];
-#pragma unroll
-    for (int i = 0; i < kWLoads; ++i)
-    {
-        const uint32_t c = tid + i * kThreads;
-        const uint32_t row = c / kChunks;
-        const uint32_t cc = c % kChunks;
-        wSrc[i] = epi.WRow(n0 + row) + cc * 8;
-        wDst[i] = (2 * kBM + row) * kGemmStride + cc * 8;
-        wCol[i] = cc * 8;
-    }
+    // Each thread loads one 16-byte chunk (column `col`) of rows r0, r0 + kRowsPerPass, ... of the
+    // A planes and of the weight. A row group's address is uniform across the workgroup and the
+    // lane adds r0 * k + col, so the addresses cost one register (scalar base + vector offset)
+    // rather than a 64-bit pointer per load. A lane whose row is past the matrix reads its group's
+    // first row instead (in bounds; its products land in outputs that are not stored), so the
+    // loads need no branches.
+    constexpr uint32_t kRowsPerPass = kThreads / kChunks;
+    static_assert(kBM % kRowsPerPass == 0 && 32 % kRowsPerPass == 0, "row groups");
+    const uint32_t r0 = tid / kChunks;
+    const uint32_t col = (tid % kChunks) * 8;
+    const uint32_t laneOffset = r0 * k + col;
+    const uint32_t dst = r0 * kGemmStride + col;
 
     const uint32_t kBegin = blockIdx.z * kPerSplit;
     const uint32_t kEnd = min(k, kBegin + kPerSplit);
@@ -440,15 +428,38 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1
     auto load = [&](auto buf, uint32_t k0)
     {
         constexpr int b = decltype(buf)::value;
+        // A chunk past kEnd (only in a K tile that runs past it) reads the tile's first chunk of
+        // its row instead, and is zeroed below.
+        const bool past = k0 + kGemmBK > kEnd && k0 + col >= kEnd;
+        const uint32_t c = past ? 0u : col;
+        const uint32_t offset = past ? r0 * k : laneOffset;
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
         {
-            aReg[b][i] = k0 + aCol[i] < kEnd ? *reinterpret_cast<const half8*>(aSrc[i] + k0) : half8{};
+            const uint32_t plane = i * kRowsPerPass / kBM;
+            const uint32_t row = m0 + i * kRowsPerPass % kBM;
+            const uint16_t* base = (plane == 0 ? ahi : alo) + static_cast<uint64_t>(min(row, rows - 1)) * k + k0;
+            aReg[b][i] = *reinterpret_cast<const half8*>(base + (row + r0 < rows ? offset : c));
         }
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
         {
-            wReg[b][i] = k0 + wCol[i] < kEnd ? *reinterpret_cast<const half8*>(wSrc[i] + k0) : half8{};
+            const uint32_t u = n0 + i * kRowsPerPass;
+            const uint16_t* base = epi.WRows(u) + k0;
+            wReg[b][i] = *reinterpret_cast<const half8*>(base + (epi.WFirst(u) + r0 < epi.WCount() ? offset : c));
+        }
+        if (past)
+        {
+#pragma unroll
+            for (int i = 0; i < kALoads; ++i)
+            {
+                aReg[b][i] = half8{};
+            }
+#pragma unroll
+            for (int i = 0; i < kWLoads; ++i)
+            {
+                wReg[b][i] = half8{};
+            }
         }
     };
 
@@ -482,12 +493,13 @@ __global__ __launch_bounds__(kWave * kWm * kWn, kNb == 4 || kStages == 2 ? 2 : 1
 #pragma unroll
         for (int i = 0; i < kALoads; ++i)
         {
-            *reinterpret_cast<half8*>(lds + aDst[i]) = aReg[b][i];
+            // Plane p's row r sits at LDS row p * kBM + r, i.e. row i * kRowsPerPass + r0.
+            *reinterpret_cast<half8*>(lds + dst + i * kRowsPerPass * kGemmStride) = aReg[b][i];
         }
 #pragma unroll
         for (int i = 0; i < kWLoads; ++i)
         {
-            *reinterpret_cast<half8*>(lds + wDst[i]) = wReg[b][i];
+            *reinterpret_cast<half8*>(lds + dst + (2 * kBM + i * kRowsPerPass) * kGemmStride) = wReg[b][i];
         }
         __syncthreads();
         if (k0 + kStages * kGemmBK < kEnd)
