@@ -572,7 +572,8 @@ bool BigTiles(uint32_t rows, uint32_t virtualRows, uint32_t splits = 1)
 
 /// 128-token x 256-row tiles (a wave 64 tokens x 128 rows, two workgroups per CU) when they give
 /// four workgroups per CU or more: an activation fragment read from LDS feeds twice the
-/// matrix-core work. With fewer tiles the last round's imbalance costs more than that gains.
+/// matrix-core work. With fewer tiles the last round's imbalance costs more than that gains,
+/// unless K splits make them one nearly full round (LaunchGemm).
 bool WideTiles(uint32_t rows, uint32_t virtualRows)
 {
     return static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 256) >= 1024;
@@ -590,7 +591,8 @@ hipError_t LaunchGemm(hipStream_t s, const uint16_t* ahi, const uint16_t* alo, c
     // Token tiles fastest where the weight outweighs the activation planes and K is whole (the
     // gate+up GEMMs: 7B 1200 -> 1087 us; the K-split q|k|v and o_proj measured slower so).
     const uint32_t mFast = splits == 1 && static_cast<uint64_t>(virtualRows) * 2 > static_cast<uint64_t>(rows) * 4;
-    if (WideTiles(rows, virtualRows))
+    const uint64_t wideSplits = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(virtualRows, 256) * splits;
+    if (WideTiles(rows, virtualRows) || (splits > 1 && wideSplits * 8 >= 512 * 7 && wideSplits <= 512))
     {
         hipLaunchKernelGGL((GemmSplitKernel<2, 2, Epi, 4, 1>), dim3(CeilDiv(virtualRows, 256), CeilDiv(rows, 128), splits),
                            dim3(256), 0, s, ahi, alo, epi, rows, k, kPerSplit, mFast);
@@ -999,9 +1001,16 @@ uint32_t GemmSplits(uint32_t rows, uint32_t n, uint32_t k)
     {
         return bigTiles < 1024 && halves ? 2 : 1;
     }
-    // At least seven eighths of one round: unsplit. K halves would add partial planes that the
-    // next norm sums (7B o_proj and down, 448 tiles: the two norms 36.6 -> 17.9 us, the GEMMs
-    // unchanged).
+    // 128 x 256 tiles over two K halves that fill seven eighths to all of one round (7B o_proj
+    // and down, 448 workgroups): the wide tiles' matrix-core work per LDS read outweighs the
+    // partial planes the next norm sums (o_proj + down 727 -> 614 us, the norms 18 -> 37 us).
+    const uint64_t wideHalves = static_cast<uint64_t>(CeilDiv(rows, 128)) * CeilDiv(n, 256) * 2;
+    if (halves && wideHalves * 8 >= 512 * 7 && wideHalves <= 512)
+    {
+        return 2;
+    }
+    // Otherwise at least seven eighths of one round of 128 x 128 tiles: unsplit, with no partial
+    // planes for the next norm to sum.
     if (bigTiles * 8 >= 512 * 7)
     {
         return 1;
