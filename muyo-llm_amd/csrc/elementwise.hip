@@ -216,11 +216,10 @@ __device__ __forceinline__ float YarnRamp(float low, float high, uint32_t i0)
 
 /// cos and sin of pair iw's angle at position `pos`, scaled by mscale (rope_funcs.glsl:17-35's
 /// rope_yarn); `power` is thetaScale^(iw / 2). Both rope kernels use it, so they agree bit for bit.
-__device__ __forceinline__ void RopeAngle(const LlamaRopePushConstants& p, const float* __restrict__ ff, uint32_t iw,
-                                          float power, int32_t pos, float& c, float& s)
+__device__ __forceinline__ void RopeAngleWith(const LlamaRopePushConstants& p, float freqFactor, uint32_t iw,
+                                              float power, int32_t pos, float& c, float& s)
 {
     const float thetaBase = static_cast<float>(pos) * power;
-    const float freqFactor = p.hasFf != 0 ? ff[iw / 2] : 1.0f;
     const float thetaExtrap = thetaBase / freqFactor;
     float mscale = p.attnFactor;
     const float thetaInterp = p.freqScale * thetaExtrap;
@@ -239,6 +238,12 @@ __device__ __forceinline__ void RopeAngle(const LlamaRopePushConstants& p, const
     s = sinf(theta) * mscale;
 }
 
+__device__ __forceinline__ void RopeAngle(const LlamaRopePushConstants& p, const float* __restrict__ ff, uint32_t iw,
+                                          float power, int32_t pos, float& c, float& s)
+{
+    RopeAngleWith(p, p.hasFf != 0 ? ff[iw / 2] : 1.0f, iw, power, pos, c, s);
+}
+
 /// The rotation of one pair, with its fused multiply-adds written out so that both rope kernels
 /// round identically: (x0 c - x1 s, x0 s + x1 c).
 __device__ __forceinline__ void RopeRotate(float x0, float x1, float c, float s, float& y0, float& y1)
@@ -254,7 +259,9 @@ constexpr uint32_t kRopeHeadsPerThread = 4;
 /// offsets on 16-byte boundaries, no set_rows, whole tokens. Thread t takes quad q (pairs
 /// 4q..4q+3: four floats from each half of a row) of up to four heads of one token, so each
 /// angle's cos and sin serve four rows; rows are loaded and stored 16 bytes at a time with
-/// non-temporal hints, the loads issued before the table of powers is built.
+/// non-temporal hints. The position and frequency factors are requested before the rows (loads
+/// complete in order, so the angles would otherwise wait for the rows), and the table of powers
+/// and the angles are computed while the rows are in flight.
 __global__ __launch_bounds__(kBlock) void RopeNeoxRows(const float* __restrict__ x, const int32_t* __restrict__ positions,
                                                        const float* __restrict__ ff, float* __restrict__ d,
                                                        LlamaRopePushConstants p, uint32_t tokens)
@@ -273,6 +280,13 @@ __global__ __launch_bounds__(kBlock) void RopeNeoxRows(const float* __restrict__
     const uint32_t i2 = token - i3 * p.ne02;
     const uint64_t xRow = p.aOffset + static_cast<uint64_t>(i3) * p.nb03 + static_cast<uint64_t>(i2) * p.nb02 + 4u * q;
     const uint64_t dRow = p.dOffset + static_cast<uint64_t>(i3) * p.nb13 + static_cast<uint64_t>(i2) * p.nb12 + 4u * q;
+    const int32_t pos = positions[i2];
+    float freq[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+    {
+        freq[e] = p.hasFf != 0 ? ff[4u * q + static_cast<uint32_t>(e)] : 1.0f;
+    }
     float4v lo[kRopeHeadsPerThread];
     float4v hi[kRopeHeadsPerThread];
 #pragma unroll
@@ -283,7 +297,6 @@ __global__ __launch_bounds__(kBlock) void RopeNeoxRows(const float* __restrict__
         lo[k] = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(row));
         hi[k] = __builtin_nontemporal_load(reinterpret_cast<const float4v*>(row + half));
     }
-    const int32_t pos = positions[i2];
     for (uint32_t j = threadIdx.x; j < half; j += kBlock)
     {
         thetaPow[j] = powf(p.thetaScale, static_cast<float>(j));
@@ -299,7 +312,7 @@ __global__ __launch_bounds__(kBlock) void RopeNeoxRows(const float* __restrict__
     for (int e = 0; e < 4; ++e)
     {
         const uint32_t j = 4u * q + static_cast<uint32_t>(e);
-        RopeAngle(p, ff, 2u * j, thetaPow[j], pos, c[e], sn[e]);
+        RopeAngleWith(p, freq[e], 2u * j, thetaPow[j], pos, c[e], sn[e]);
     }
 #pragma unroll
     for (uint32_t k = 0; k < kRopeHeadsPerThread; ++k)
