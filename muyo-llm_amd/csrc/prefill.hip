@@ -19,6 +19,7 @@ namespace
 {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef uint16_t ushort4v __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ floatx16 Mfma(half8 a, half8 b, floatx16 c)
 {
@@ -229,6 +230,99 @@ __global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __rest
         const uint32_t v = (heads + kvHeads) * headDim + channel;
         vcache[base] = FloatToHalfBits(value(v));
         vcache[base + 1] = FloatToHalfBits(value(v + 1));
+    }
+}
+
+/// RopeSplitAppendKernel with four pairs (or four v channels) per thread: 16-byte loads, 8-byte
+/// stores and the same arithmetic per element (head_dim % 8 == 0, buffers aligned). The table of
+/// powers is requested before the partial sums, so the angles are computed while the sums are
+/// in flight (loads complete in order).
+__global__ __launch_bounds__(256) void RopeSplitAppendQuadKernel(const float* __restrict__ qkv, uint32_t rows,
+                                                                 int32_t pos0, uint32_t heads, uint32_t kvHeads,
+                                                                 uint32_t headDim, uint32_t maxSeq,
+                                                                 const float* __restrict__ ropePow,
+                                                                 uint16_t* __restrict__ qhi, uint16_t* __restrict__ qlo,
+                                                                 uint16_t* __restrict__ kcache,
+                                                                 uint16_t* __restrict__ vcache, uint32_t splits,
+                                                                 const float* __restrict__ bias)
+{
+    const uint32_t half = headDim / 2;
+    const uint32_t quads = half / 4;
+    const uint32_t ropeUnits = (heads + kvHeads) * quads;
+    const uint32_t units = ropeUnits + kvHeads * headDim / 4;
+    const uint64_t index = blockIdx.x * 256ull + threadIdx.x;
+    if (index >= static_cast<uint64_t>(rows) * units)
+    {
+        return;
+    }
+    const uint32_t m = static_cast<uint32_t>(index / units);
+    const uint32_t unit = static_cast<uint32_t>(index % units);
+    const int32_t pos = pos0 + static_cast<int32_t>(m);
+    const uint32_t width = (heads + 2 * kvHeads) * headDim;
+    const float* row = qkv + static_cast<uint64_t>(m) * width;
+    const uint64_t stride = static_cast<uint64_t>(rows) * width;
+    auto value4 = [&](uint32_t col) {
+        float4v a = *reinterpret_cast<const float4v*>(row + col);
+        if (splits > 1)
+        {
+            for (uint32_t z = 1; z < splits; ++z)
+            {
+                a += *reinterpret_cast<const float4v*>(row + z * stride + col);
+            }
+            a += *reinterpret_cast<const float4v*>(bias + col);
+        }
+        return a;
+    };
+    if (unit < ropeUnits)
+    {
+        const uint32_t head = unit / quads;
+        const uint32_t j = (unit % quads) * 4;
+        const float4v power = *reinterpret_cast<const float4v*>(ropePow + j);
+        const float4v s0 = value4(head * headDim + j);
+        const float4v s1 = value4(head * headDim + j + half);
+        float c[4];
+        float sn[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            const float theta = static_cast<float>(pos) * power[e];
+            c[e] = cosf(theta);
+            sn[e] = sinf(theta);
+        }
+        float o0[4];
+        float o1[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+        {
+            o0[e] = s0[e] * c[e] - s1[e] * sn[e];
+            o1[e] = s0[e] * sn[e] + s1[e] * c[e];
+        }
+        if (head < heads)
+        {
+            const uint64_t at = static_cast<uint64_t>(m) * heads * headDim + head * headDim + j;
+            StoreSplit4(qhi, qlo, at, o0[0], o0[1], o0[2], o0[3]);
+            StoreSplit4(qhi, qlo, at + half, o1[0], o1[1], o1[2], o1[3]);
+        }
+        else
+        {
+            const uint64_t base = (static_cast<uint64_t>(head - heads) * maxSeq + pos) * headDim + j;
+            const ushort4v k0 = {FloatToHalfBits(o0[0]), FloatToHalfBits(o0[1]), FloatToHalfBits(o0[2]),
+                                 FloatToHalfBits(o0[3])};
+            const ushort4v k1 = {FloatToHalfBits(o1[0]), FloatToHalfBits(o1[1]), FloatToHalfBits(o1[2]),
+                                 FloatToHalfBits(o1[3])};
+            *reinterpret_cast<ushort4v*>(kcache + base) = k0;
+            *reinterpret_cast<ushort4v*>(kcache + base + half) = k1;
+        }
+    }
+    else
+    {
+        const uint32_t channel = 4 * (unit - ropeUnits);  // within kvHeads * headDim
+        const uint32_t g = channel / headDim;
+        const uint64_t base = (static_cast<uint64_t>(g) * maxSeq + pos) * headDim + channel % headDim;
+        const float4v v = value4((heads + kvHeads) * headDim + channel);
+        const ushort4v out = {FloatToHalfBits(v[0]), FloatToHalfBits(v[1]), FloatToHalfBits(v[2]),
+                              FloatToHalfBits(v[3])};
+        *reinterpret_cast<ushort4v*>(vcache + base) = out;
     }
 }
 
@@ -1068,6 +1162,16 @@ hipError_t LaunchRopeSplitAppend(hipStream_t s, const float* qkv, uint32_t rows,
         splits > kMaxGemmSplits || (splits > 1 && bias == nullptr))
     {
         return hipErrorInvalidValue;
+    }
+    const auto aligned = [](const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; };
+    if (headDim % 8 == 0 && aligned(qkv, 16) && aligned(ropePow, 16) && (bias == nullptr || aligned(bias, 16)) &&
+        aligned(qhi, 8) && aligned(qlo, 8) && aligned(kcache, 8) && aligned(vcache, 8))
+    {
+        // Threads: four pairs of a rotated head each, or four v channels.
+        const uint64_t quads = static_cast<uint64_t>(rows) * ((heads + kvHeads) * (headDim / 8) + kvHeads * headDim / 4);
+        hipLaunchKernelGGL(RopeSplitAppendQuadKernel, dim3(CeilDiv(quads, 256)), dim3(256), 0, s, qkv, rows, pos0,
+                           heads, kvHeads, headDim, maxSeq, ropePow, qhi, qlo, kcache, vcache, splits, bias);
+        return hipGetLastError();
     }
     hipLaunchKernelGGL(RopeSplitAppendKernel, dim3(CeilDiv(total, 256)), dim3(256), 0, s, qkv, rows, pos0, heads,
                        kvHeads, headDim, maxSeq, ropePow, qhi, qlo, kcache, vcache, splits, bias);
