@@ -144,6 +144,146 @@ __global__ __launch_bounds__(256) void RmsNormSplitKernel(float* __restrict__ x,
     }
 }
 
+/// RmsNormSplitKernel with kT threads per row (one wave, or the whole 256-thread workgroup) and
+/// at most kChunks 16-byte chunks of the row per thread, all requested before the first is used:
+/// every K split's part, the residual and the weight in one round of loads instead of one round
+/// per chunk. The sums run in SplitSum::At's order; the sum of squares meets across the row's
+/// waves in LDS.
+template <int kT>
+__global__ __launch_bounds__(256) void RmsNormSplitRowsKernel(float* __restrict__ x, const float* __restrict__ w,
+                                                              uint32_t rows, uint32_t cols, float eps,
+                                                              uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
+                                                              SplitSum sum)
+{
+    constexpr int kChunks = 4;
+    constexpr int kRowsPerBlock = 256 / kT;
+    constexpr int kWavesPerRow = kT / kWave;
+    __shared__ float squares[kRowsPerBlock * kWavesPerRow];
+    const uint32_t row = blockIdx.x * kRowsPerBlock + threadIdx.x / kT;
+    const uint32_t t = threadIdx.x % kT;
+    const bool live = row < rows;
+    const uint64_t base = static_cast<uint64_t>(live ? row : 0) * cols;
+    float4 v[kChunks];
+    float4 part[kMaxGemmSplits - 1][kChunks];
+    float4 res[kChunks];
+    float4 g[kChunks];
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+    {
+        const uint32_t i = (t + c * kT) * 4;
+        const bool in = i < cols;
+        const uint64_t at = base + (in ? i : 0);
+        v[c] = *reinterpret_cast<const float4*>((sum.splits > 0 ? sum.partial : x) + at);
+#pragma unroll
+        for (uint32_t z = 1; z < kMaxGemmSplits; ++z)
+        {
+            if (z < sum.splits)
+            {
+                part[z - 1][c] = *reinterpret_cast<const float4*>(sum.partial + z * sum.stride + at);
+            }
+        }
+        if (sum.splits > 0 && sum.residual != nullptr)
+        {
+            res[c] = *reinterpret_cast<const float4*>(sum.residual + at);
+        }
+        if (w != nullptr)
+        {
+            g[c] = *reinterpret_cast<const float4*>(w + (in ? i : 0));
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+    {
+        const uint32_t i = (t + c * kT) * 4;
+        if (sum.splits > 0)
+        {
+#pragma unroll
+            for (uint32_t z = 1; z < kMaxGemmSplits; ++z)
+            {
+                if (z < sum.splits)
+                {
+                    v[c].x += part[z - 1][c].x;
+                    v[c].y += part[z - 1][c].y;
+                    v[c].z += part[z - 1][c].z;
+                    v[c].w += part[z - 1][c].w;
+                }
+            }
+            if (sum.residual != nullptr)
+            {
+                v[c] = make_float4(res[c].x + v[c].x, res[c].y + v[c].y, res[c].z + v[c].z, res[c].w + v[c].w);
+            }
+            if (live && i < cols)
+            {
+                *reinterpret_cast<float4*>(x + base + i) = v[c];
+            }
+        }
+        if (i < cols)
+        {
+            ss += v[c].x * v[c].x + v[c].y * v[c].y + v[c].z * v[c].z + v[c].w * v[c].w;
+        }
+    }
+    if (w == nullptr)
+    {
+        return;
+    }
+    ss = GroupSum<kWave>(ss);
+    if constexpr (kWavesPerRow > 1)
+    {
+        const uint32_t wave = threadIdx.x / kWave;
+        if (threadIdx.x % kWave == 0)
+        {
+            squares[wave] = ss;
+        }
+        __syncthreads();
+        const uint32_t first = (threadIdx.x / kT) * kWavesPerRow;
+        ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kWavesPerRow; ++k)
+        {
+            ss += squares[first + k];
+        }
+    }
+    if (!live)
+    {
+        return;
+    }
+    const float scale = 1.0f / sqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+    for (int c = 0; c < kChunks; ++c)
+    {
+        const uint32_t i = (t + c * kT) * 4;
+        if (i < cols)
+        {
+            StoreSplit4(hi, lo, base + i, (scale * v[c].x) * g[c].x, (scale * v[c].y) * g[c].y,
+                        (scale * v[c].z) * g[c].z, (scale * v[c].w) * g[c].w);
+        }
+    }
+}
+
+/// The row kernel for `cols`: a wave per row up to 1024 columns, the workgroup per row up to 4096,
+/// else the loop kernel.
+hipError_t LaunchRmsNormSplitRows(hipStream_t s, float* x, const float* w, uint32_t rows, uint32_t cols, float eps,
+                                  uint16_t* hi, uint16_t* lo, const SplitSum& sum)
+{
+    if (cols <= 4 * 4 * kWave)
+    {
+        hipLaunchKernelGGL(RmsNormSplitRowsKernel<kWave>, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols,
+                           eps, hi, lo, sum);
+    }
+    else if (cols <= 4 * 4 * 256)
+    {
+        hipLaunchKernelGGL(RmsNormSplitRowsKernel<256>, dim3(rows), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo,
+                           sum);
+    }
+    else
+    {
+        hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo,
+                           sum);
+    }
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void SplitF32Kernel(const float* __restrict__ x, uint64_t quads,
                                                       uint16_t* __restrict__ hi, uint16_t* __restrict__ lo)
 {
@@ -1051,9 +1191,7 @@ hipError_t LaunchRmsNormSplit(hipStream_t s, const float* x, const float* w, uin
     {
         return hipErrorInvalidValue;
     }
-    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, const_cast<float*>(x), w, rows,
-                       cols, eps, hi, lo, SplitSum{});
-    return hipGetLastError();
+    return LaunchRmsNormSplitRows(s, const_cast<float*>(x), w, rows, cols, eps, hi, lo, SplitSum{});
 }
 
 hipError_t LaunchReduceRmsNormSplit(hipStream_t s, const float* residual, const float* partial, uint32_t splits,
@@ -1065,9 +1203,7 @@ hipError_t LaunchReduceRmsNormSplit(hipStream_t s, const float* residual, const 
         return hipErrorInvalidValue;
     }
     const SplitSum sum{residual, partial, splits, static_cast<uint64_t>(rows) * cols};
-    hipLaunchKernelGGL(RmsNormSplitKernel, dim3(CeilDiv(rows, 4)), dim3(256), 0, s, x, w, rows, cols, eps, hi, lo,
-                       sum);
-    return hipGetLastError();
+    return LaunchRmsNormSplitRows(s, x, w, rows, cols, eps, hi, lo, sum);
 }
 
 hipError_t LaunchSplitF32(hipStream_t s, const float* x, uint64_t count, uint16_t* hi, uint16_t* lo)
