@@ -908,24 +908,38 @@ __global__ __launch_bounds__(256) void PrefillAttnMergeKernel(AttnPartials part,
         return;
     }
     const uint32_t chunks = (keyTiles + chunkTiles - 1) / chunkTiles;
-    float top = -INFINITY;
-    for (uint32_t c = 0; c < chunks; ++c)
+    // Every slot's operands requested at once (slots past `chunks` reread slot 0 and weigh 0).
+    float mc[kAttnMaxChunks];
+    float lc[kAttnMaxChunks];
+    float4 ac[kAttnMaxChunks];
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxChunks; ++c)
     {
-        top = fmaxf(top, part.max[(static_cast<uint64_t>(c) * rows + m) * heads + head]);
+        const uint64_t at = (static_cast<uint64_t>(c < chunks ? c : 0) * rows + m) * heads + head;
+        mc[c] = part.max[at];
+        lc[c] = part.sum[at];
+        ac[c] = *reinterpret_cast<const float4*>(part.acc + at * headDim + channel);
+    }
+    float top = -INFINITY;
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxChunks; ++c)
+    {
+        top = c < chunks ? fmaxf(top, mc[c]) : top;
     }
     float den = 0.0f;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t c = 0; c < chunks; ++c)
+#pragma unroll
+    for (uint32_t c = 0; c < kAttnMaxChunks; ++c)
     {
-        const uint64_t at = (static_cast<uint64_t>(c) * rows + m) * heads + head;
-        const float mc = part.max[at];
-        const float w = mc == -INFINITY ? 0.0f : expf(mc - top);
-        const float4 a = *reinterpret_cast<const float4*>(part.acc + at * headDim + channel);
-        den = fmaf(w, part.sum[at], den);
-        num.x = fmaf(w, a.x, num.x);
-        num.y = fmaf(w, a.y, num.y);
-        num.z = fmaf(w, a.z, num.z);
-        num.w = fmaf(w, a.w, num.w);
+        if (c < chunks)
+        {
+            const float w = mc[c] == -INFINITY ? 0.0f : expf(mc[c] - top);
+            den = fmaf(w, lc[c], den);
+            num.x = fmaf(w, ac[c].x, num.x);
+            num.y = fmaf(w, ac[c].y, num.y);
+            num.z = fmaf(w, ac[c].z, num.z);
+            num.w = fmaf(w, ac[c].w, num.w);
+        }
     }
     const float inv = 1.0f / den;
     StoreSplit4(ohi, olo, static_cast<uint64_t>(m) * heads * headDim + head * headDim + channel, num.x * inv,
