@@ -112,7 +112,7 @@ GEMM_SHAPES = [
     (200, 1152, 896),   # 0.5B QKV
     (300, 896, 896),    # 0.5B o_proj
     (67, 896, 4864),    # 0.5B down: long K
-    (640, 1152, 896),   # enough tiles for the 128 x 128 launch
+    (640, 1152, 896),   # 45 tiles of 128 x 128: the 64-token tiles
 ]
 
 
@@ -163,6 +163,44 @@ def test_gemm_split_integer_inputs_are_exact(mh, gpu):
     run(mh, torch, mh.load().muyo_gemm_split_f16(*(t.data_ptr() for t in keep), None, None, out.data_ptr(),
                                                  rows, n, k, stream(torch)))
     assert np.array_equal(host(out), a.astype(np.float64) @ w.astype(np.float64).T)
+
+
+@pytest.mark.parametrize("rows,n,k", [(1990, 4600, 136), (1990, 16300, 72)])
+def test_gemm_split_large_grids_integer_exact(mh, gpu, rows, n, k):
+    """Integer inputs on the 128 x 128 and 128 x 256 tile kernels (576 and 1040 tiles, the second
+    with token tiles fastest): a last token tile of 70 rows, a last weight tile of 120 or 172
+    rows and a K tail inside the last K tile, whose lanes past the matrix read in-bounds rows."""
+    torch = gpu
+    rng = np.random.default_rng(rows + n + k)
+    a = rng.integers(-8, 9, (rows, k)).astype(np.float32)
+    w = rng.integers(-8, 9, (n, k)).astype(np.float16)
+    ahi, alo = split_np(a)
+    out = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    keep = [dev(torch, ahi), dev(torch, alo), dev(torch, w.view(np.uint16))]
+    run(mh, torch, mh.load().muyo_gemm_split_f16(*(t.data_ptr() for t in keep), None, None, out.data_ptr(),
+                                                 rows, n, k, stream(torch)))
+    assert np.array_equal(host(out), a.astype(np.float64) @ w.astype(np.float64).T)
+
+
+def test_gemm_swiglu_wide_tiles_integer_products(mh, gpu):
+    """The 128 x 256 swiglu tiles (1040 of them) on integer inputs: both products exact, the
+    swiglu of them to the planes' precision; ragged token and ffn tiles and a K tail."""
+    torch = gpu
+    rows, ffn, k = 1990, 8200, 40
+    rng = np.random.default_rng(77)
+    a = rng.integers(-2, 3, (rows, k)).astype(np.float32)
+    wg = rng.integers(-2, 3, (ffn, k)).astype(np.float16)
+    wu = rng.integers(-2, 3, (ffn, k)).astype(np.float16)
+    ahi, alo = split_np(a)
+    hhi, hlo = planes(torch, (rows, ffn))
+    keep = [dev(torch, ahi), dev(torch, alo), dev(torch, wg.view(np.uint16)), dev(torch, wu.view(np.uint16))]
+    run(mh, torch, mh.load().muyo_gemm_swiglu_split_f16(*(t.data_ptr() for t in keep), hhi.data_ptr(),
+                                                        hlo.data_ptr(), rows, ffn, k, stream(torch)))
+    g = a.astype(np.float64) @ wg.astype(np.float64).T
+    u = a.astype(np.float64) @ wu.astype(np.float64).T
+    want = g / (1.0 + np.exp(-g)) * u
+    got = joined(hhi, hlo)
+    assert np.abs(got - want).max() <= 1e-5 * (1.0 + np.abs(want)).max()
 
 
 @pytest.mark.parametrize("rows,ffn,k", [(1, 8, 8), (45, 100, 72), (200, 4864, 896), (700, 4864, 896)])
