@@ -507,12 +507,14 @@ def test_decoder_prefill_equals_steps_on_gpu(mh, gpu, orc):
     assert ids_p == ids_s
 
 
-def test_decoder_prefill_7b_width_full_prompt_equals_steps(mh, gpu, orc):
-    """The 7B widths over a full 2048-token prompt, where o_proj and down take 128 x 128 tiles over
-    two K halves and the gate+up 128 x 256 tiles: the same logits, cache rows and next token as
-    2048 of the decoder's own steps."""
+@pytest.mark.parametrize("count", [2048, 1990])
+def test_decoder_prefill_7b_width_full_prompt_equals_steps(mh, gpu, orc, count):
+    """The 7B widths over a 2048-token (and a 1990-token: ragged last token tiles) prompt, where
+    q|k|v takes 128 x 128 tiles over two K halves, o_proj and down 128 x 256 tiles over two K
+    halves and the gate+up 128 x 256 tiles: the same logits, cache rows and next token as the
+    decoder's own steps."""
     shape = dict(mh.QWEN25_7B, layers=2)
-    tokens = prompt(orc, 2048, shape["vocab"], 63)
+    tokens = prompt(orc, count, shape["vocab"], 63)
     with mh.Decoder(mh.qwen2_config(**shape)) as dec:
         dec.fill_random(64)
         nxt = dec.prefill(tokens, 0)
