@@ -878,7 +878,7 @@ struct AttnWork
 };
 
 /// Softmax partials of the chunks of split tiles: [kAttnMaxChunks][rows][heads] (running max in
-/// natural-log units, sum) and [kAttnMaxChunks][rows][heads][headDim] (unnormalised P.V).
+/// log2 units, sum) and [kAttnMaxChunks][rows][heads][headDim] (unnormalised P.V).
 struct AttnPartials
 {
     float* max;
@@ -887,7 +887,7 @@ struct AttnPartials
 };
 
 /// Combines the chunk partials of the split tiles' queries into their output planes: out = sum_c
-/// e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c, M the largest m_c (a chunk with no key of the query
+/// 2^(m_c - M) acc_c / sum_c 2^(m_c - M) l_c, M the largest m_c (a chunk with no key of the query
 /// weighs 0). A thread per (query, head, 4 channels); queries of unsplit tiles are left alone.
 __global__ __launch_bounds__(256) void PrefillAttnMergeKernel(AttnPartials part, uint16_t* __restrict__ ohi,
                                                               uint16_t* __restrict__ olo, uint32_t rows, int32_t pos0,
@@ -933,7 +933,7 @@ __global__ __launch_bounds__(256) void PrefillAttnMergeKernel(AttnPartials part,
     {
         if (c < chunks)
         {
-            const float w = mc[c] == -INFINITY ? 0.0f : expf(mc[c] - top);
+            const float w = mc[c] == -INFINITY ? 0.0f : exp2f(mc[c] - top);
             den = fmaf(w, lc[c], den);
             num.x = fmaf(w, ac[c].x, num.x);
             num.y = fmaf(w, ac[c].y, num.y);
@@ -1009,8 +1009,9 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
     {
         o[c] = floatx16{};
     }
-    float runMax = -INFINITY;
+    float runMax = -INFINITY;  // log2 units: scores scaled by log2(e), weights 2^(s - max)
     float runSum = 0.0f;
+    const float scaleLog2 = scale * 1.44269504088896340736f;
     const uint16_t* kBase = kcache + static_cast<uint64_t>(g) * maxSeq * kHd;
     const uint16_t* vBase = vcache + static_cast<uint64_t>(g) * maxSeq * kHd;
 
@@ -1096,7 +1097,7 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
         for (int r = 0; r < 16; ++r)
         {
             const int32_t key = static_cast<int32_t>(kt * kAttnKeys + 8 * (r / 4) + 4 * h + r % 4);
-            p[r] = key <= qpos ? st[r] * scale : -INFINITY;
+            p[r] = key <= qpos ? st[r] * scaleLog2 : -INFINITY;
             tileMax = fmaxf(tileMax, p[r]);
         }
         tileMax = fmaxf(tileMax, __shfl_xor(tileMax, 32));
@@ -1104,12 +1105,12 @@ __global__ __launch_bounds__(kWave * kHeadsPerBlock) void PrefillAttentionKernel
         // no key of a query yet: then nothing accumulates (factor 1, weights 0).
         const float newMax = fmaxf(runMax, tileMax);
         const bool none = newMax == -INFINITY;
-        const float factor = none ? 1.0f : expf(runMax - newMax);
+        const float factor = none ? 1.0f : exp2f(runMax - newMax);
         float sum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r)
         {
-            p[r] = none ? 0.0f : expf(p[r] - newMax);
+            p[r] = none ? 0.0f : exp2f(p[r] - newMax);
             sum += p[r];
         }
         runSum = runSum * factor + sum;
