@@ -136,8 +136,9 @@ struct DirectStage : Base
 
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c 2^(m_c - M) acc_c /
 /// sum_c 2^(m_c - M) l_c (flash-decoding's combine, maxima in log2 units). Every slot of the
-/// grid takes part; chunks without keys hold the neutral partial, so no position is needed and
-/// every partial is requested at entry.
+/// grid (at most kChunks) takes part; chunks without keys hold the neutral partial, so no
+/// position is needed and every partial is requested at entry.
+template <uint32_t kChunks>
 struct MergeStage
 {
     const float* attnMax;
@@ -160,14 +161,14 @@ struct MergeStage
         __shared__ float weight[kMergeSlots];
         const uint32_t nchunks = n / 8;
         uint32_t items[kMergeItems];
-        float acc[kMergeItems][kMergeAttnChunks];
+        float acc[kMergeItems][kChunks];
 #pragma unroll
         for (uint32_t k = 0; k < kMergeItems; ++k)
         {
             items[k] = min(threadIdx.x + k * kBlock, n - 1);
             const uint32_t h = items[k] / headDim;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
                 acc[k][c] = attnAcc[Slot(h, c) * headDim + items[k] % headDim];
             }
@@ -175,32 +176,32 @@ struct MergeStage
         if (threadIdx.x < heads)
         {
             const uint32_t h = threadIdx.x;
-            float m[kMergeAttnChunks];
-            float l[kMergeAttnChunks];
+            float m[kChunks];
+            float l[kChunks];
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
                 m[c] = c < gridChunks ? attnMax[Slot(h, c)] : -INFINITY;
                 l[c] = attnSum[Slot(h, c)];
             }
             float top = -INFINITY;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
                 top = fmaxf(top, m[c]);
             }
             float den = 0.0f;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
                 m[c] = top == -INFINITY ? 0.0f : exp2f(m[c] - top);  // 0 for neutral and absent slots
                 den = fmaf(m[c], l[c], den);
             }
             const float inv = den > 0.0f ? 1.0f / den : 0.0f;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
-                weight[h * kMergeAttnChunks + c] = m[c] * inv;
+                weight[h * kChunks + c] = m[c] * inv;
             }
         }
         __syncthreads();
@@ -211,9 +212,9 @@ struct MergeStage
             const uint32_t h = items[k] / headDim;
             float out = 0.0f;
 #pragma unroll
-            for (uint32_t c = 0; c < kMergeAttnChunks; ++c)
+            for (uint32_t c = 0; c < kChunks; ++c)
             {
-                out = fmaf(weight[h * kMergeAttnChunks + c], acc[k][c], out);
+                out = fmaf(weight[h * kChunks + c], acc[k][c], out);
             }
             const uint32_t item = threadIdx.x + k * kBlock;
             if (item < n)
@@ -1290,7 +1291,8 @@ __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, con
 // neutral partial (-inf, 0, 0), so the merge needs no position either.
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kAttnBlocksPerRound = 8;  // key blocks per lane per round: 2048 keys of a 2048-row cache in one round
+// kAttnBlocksPerRound (decode_kernels.hpp) key blocks per lane per round: 2048 keys of a 2048-row
+// cache in one round with the long grids.
 
 /// Sum (kMax false) or maximum over the slices of one wave: the lanes equal modulo kRC. Every
 /// lane ends with the same bit pattern as the others of its class (each step combines the same
@@ -1321,7 +1323,7 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
 {
     constexpr int kRC = kHd / 8;           // lanes per key
     constexpr int kSlices = kBlock / kRC;  // keys of a block, side by side
-    constexpr int kR = kAttnBlocksPerRound;
+    constexpr int kR = static_cast<int>(kAttnBlocksPerRound);
     static_assert(kSlices == 2048 / kHd, "slice count must match AttnSlices");
     __shared__ float waveMax[kWaves];
     __shared__ float waveSum[kWaves];
@@ -1811,9 +1813,16 @@ hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16
                              const float* residual, float* out)
 {
     const uint32_t qdim = dims.heads * dims.headDim;
-    MergeStage stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads, dims.heads / dims.kvHeads,
-                     dims.headDim,    AttnGridChunks(dims.maxSeq, dims.headDim, kMergeAttnChunks)};
+    const uint32_t chunks = AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks);
     ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
+    if (chunks <= kShortAttnChunks)
+    {
+        MergeStage<kShortAttnChunks> stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads,
+                                           dims.heads / dims.kvHeads, dims.headDim, chunks};
+        return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
+    }
+    MergeStage<kMergeAttnChunks> stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads,
+                                       dims.heads / dims.kvHeads, dims.headDim, chunks};
     return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
 }
 

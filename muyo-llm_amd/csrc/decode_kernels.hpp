@@ -57,6 +57,7 @@ struct DecodeScratch
 constexpr uint32_t kArgMaxBlocks = 2048;
 constexpr uint32_t kMaxAttnChunks = 16;    // attention chunks per kv head, at most
 constexpr uint32_t kMergeAttnChunks = 8;   // the same when o_proj's prologue merges the partials
+constexpr uint32_t kShortAttnChunks = 4;   // the same while every chunk's keys fit its first round
 constexpr uint32_t kMaxSeq = 32768;
 
 /// Keys one attention workgroup processes side by side: its 256 lanes hold one 16-byte slice of
@@ -70,6 +71,13 @@ inline uint32_t AttnGridChunks(uint32_t maxSeq, uint32_t headDim, uint32_t maxCh
     const uint32_t bySlices = (maxSeq + AttnSlices(headDim) - 1) / AttnSlices(headDim);
     return bySlices < maxChunks ? bySlices : maxChunks;
 }
+
+/// Key blocks an attention chunk requests at entry, before the position is known.
+constexpr uint32_t kAttnBlocksPerRound = 8;
+
+/// Keys kShortAttnChunks chunks cover in their first round: a step at a position below this
+/// needs no second round with the short grid.
+inline uint32_t ShortAttnKeys(uint32_t headDim) { return kShortAttnChunks * kAttnBlocksPerRound * AttnSlices(headDim); }
 
 /// Grid of a fused GEMV launch: `blocks` workgroups; when blocks * unitsPerBlock covers the
 /// units, workgroup i owns units [i * unitsPerBlock, (i + 1) * unitsPerBlock).

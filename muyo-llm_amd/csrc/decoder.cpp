@@ -122,8 +122,10 @@ struct MuyoDecoder
     void* sampleWorkspace = nullptr;
 
     bool warm = false;
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // One graph per attention grid: [0] the long grid, [1] the short one (kShortAttnChunks chunks,
+    // used while the position is below ShortAttnKeys and o_proj merges the partials).
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
 
     // The persistent step (persistent.hpp): its plan, and an arena of its own, allocated when the
     // step is first selected, holding the transposed FFN_DOWN of every layer (rebuilt before a
@@ -364,28 +366,43 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
     return MUYO_OK;
 }
 
-/// One step on `s`: eager the first time, graph replay afterwards.
-int RunStep(MuyoDecoder* d, hipStream_t s)
+/// The step at `position` on `s`: eager the first time, graph replay afterwards. While o_proj
+/// merges the attention partials and the position is below ShortAttnKeys, attention runs on
+/// kShortAttnChunks chunks, whose first round of key blocks then covers every key: half the
+/// partials for the merge to read (0.5B step at cache rows 960..1087: 0.561 -> 0.546 ms), where
+/// past that point the second round costs more than the merge saves.
+int RunStep(MuyoDecoder* d, hipStream_t s, int32_t position)
 {
+    const uint32_t longChunks = d->dims.attnChunks;
+    const int variant =
+        d->mergeInOProj && static_cast<uint32_t>(position) < ShortAttnKeys(d->config.headDim) ? 1 : 0;
+    d->dims.attnChunks = variant == 1 ? kShortAttnChunks : longChunks;
+    int status = MUYO_OK;
     if (!d->warm)
     {
-        const int status = Enqueue(d, s);
-        if (status != MUYO_OK)
-        {
-            return status;
-        }
-        d->warm = true;
-        return MUYO_OK;
+        status = Enqueue(d, s);
+        d->warm = status == MUYO_OK;
+        d->dims.attnChunks = longChunks;
+        return status;
     }
-    if (d->exec == nullptr)
+    if (d->exec[variant] == nullptr)
     {
         // Capture on the decoder's own stream after everything queued on `s` has been ordered
         // before it (the capture itself runs nothing).
-        MUYO_HIP_CHECK(hipStreamSynchronize(s));
-        MUYO_HIP_CHECK(hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed));
-        const int status = Enqueue(d, d->stream);
+        hipError_t sync = hipStreamSynchronize(s);
+        if (sync == hipSuccess)
+        {
+            sync = hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed);
+        }
+        if (sync != hipSuccess)
+        {
+            d->dims.attnChunks = longChunks;
+            return HipStatus(sync, "graph capture");
+        }
+        status = Enqueue(d, d->stream);
         hipGraph_t graph = nullptr;
         const hipError_t end = hipStreamEndCapture(d->stream, &graph);
+        d->dims.attnChunks = longChunks;
         if (status != MUYO_OK)
         {
             if (graph != nullptr)
@@ -398,10 +415,11 @@ int RunStep(MuyoDecoder* d, hipStream_t s)
         {
             return HipStatus(end, "hipStreamEndCapture");
         }
-        d->graph = graph;
-        MUYO_HIP_CHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+        d->graph[variant] = graph;
+        MUYO_HIP_CHECK(hipGraphInstantiate(&d->exec[variant], d->graph[variant], nullptr, nullptr, 0));
     }
-    MUYO_HIP_CHECK(hipGraphLaunch(d->exec, s));
+    d->dims.attnChunks = longChunks;
+    MUYO_HIP_CHECK(hipGraphLaunch(d->exec[variant], s));
     return MUYO_OK;
 }
 
@@ -610,13 +628,16 @@ extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
     {
         return;
     }
-    if (d->exec != nullptr)
+    for (int v = 0; v < 2; ++v)
     {
-        (void)hipGraphExecDestroy(d->exec);
-    }
-    if (d->graph != nullptr)
-    {
-        (void)hipGraphDestroy(d->graph);
+        if (d->exec[v] != nullptr)
+        {
+            (void)hipGraphExecDestroy(d->exec[v]);
+        }
+        if (d->graph[v] != nullptr)
+        {
+            (void)hipGraphDestroy(d->graph[v]);
+        }
     }
     if (d->stream != nullptr)
     {
@@ -1031,7 +1052,7 @@ extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_
     MUYO_HIP_CHECK(LaunchSetState(s, d->state, d->scratch, token, position, d->argBlocks));
     for (uint32_t i = 0; i < count; ++i)
     {
-        const int status = RunStep(d, s);
+        const int status = RunStep(d, s, position + static_cast<int32_t>(i));
         if (status != MUYO_OK)
         {
             return status;
@@ -1100,15 +1121,18 @@ namespace
 /// The next step re-records its launches (eagerly, then a fresh capture).
 void DropGraph(MuyoDecoder* d)
 {
-    if (d->exec != nullptr)
+    for (int v = 0; v < 2; ++v)
     {
-        (void)hipGraphExecDestroy(d->exec);
-        d->exec = nullptr;
-    }
-    if (d->graph != nullptr)
-    {
-        (void)hipGraphDestroy(d->graph);
-        d->graph = nullptr;
+        if (d->exec[v] != nullptr)
+        {
+            (void)hipGraphExecDestroy(d->exec[v]);
+            d->exec[v] = nullptr;
+        }
+        if (d->graph[v] != nullptr)
+        {
+            (void)hipGraphDestroy(d->graph[v]);
+            d->graph[v] = nullptr;
+        }
     }
     d->warm = false;
 }

@@ -153,6 +153,23 @@ def test_decoder_05b_greedy_32_steps(mh, gpu, orc, capsys, position):
     assert ids == want
 
 
+def test_decoder_05b_greedy_across_the_short_attention_grid(mh, gpu, orc, capsys):
+    """Qwen2.5-0.5B shape from cache row 1000: 48 greedy tokens, the first 24 on the short
+    attention grid (4 chunks while the position is below 1024), the rest on the long one (8
+    chunks), replayed from the two graphs in turn, against the oracle."""
+    orc.set_threads(16)
+    shape = mh.QWEN25_05B
+    position = 1000
+    dec, model = make_pair(mh, orc, shape, seed=2031, kv_positions=position, kv_seed=2032)
+    start = int(orc.uniform_f32(1, 98)[0] * 0.5 * shape["vocab"] + 0.5 * shape["vocab"])
+    with dec:
+        ids = dec.generate(start, position, 48)
+    want, margins = model.greedy(start, position, 48)
+    with capsys.disabled():
+        print(f"\n[0.5b greedy p={position} across grids] ids {ids[20:28]}... min margin {min(margins):.3g}")
+    assert ids == want
+
+
 @pytest.mark.parametrize("position", [1024, 2047])
 def test_decoder_05b_single_step_long_cache(mh, gpu, orc, position):
     orc.set_threads(16)
