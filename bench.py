@@ -110,19 +110,16 @@ def enqueue_step(dec, shape, stream) -> None:
     dec.enqueue_kernel("LM_HEAD", 0, stream)
 
 
-def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None, persistent=False):
+def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
     """Returns (ms per step, positions timed, decoder launches per step, generated ids, median ms
     per step over 16 runs of the same positions). `sampler`: keyword
-    parameters of the device sampler (greedy when None), with a synthetic prompt as history;
-    `persistent`: the one-launch-per-token step instead of the graph-replayed kernels."""
+    parameters of the device sampler (greedy when None), with a synthetic prompt as history."""
     stream = torch.cuda.current_stream()
     start = max(1, position - steps // 2 - warmup)
     dec = mh.Decoder(mh.qwen2_config(**shape))
     try:
         dec.fill_random(seed)
         dec.fill_kv_random(start, seed + 1)
-        if persistent:
-            dec.set_persistent(True)
         if sampler is not None:
             dec.set_history([(7919 * i) % shape["vocab"] for i in range(start)])
             dec.set_sampler(**sampler)
@@ -511,23 +508,6 @@ def kernel_only(mh, torch, which: str, launches: int) -> dict:
         e.record(stream)
         torch.cuda.synchronize()
         nbytes = 2 * 4 * n
-    elif which == "persistent_05b":
-        shape = dict(mh.QWEN25_05B)
-        launches = min(launches, 512)
-        dec = mh.Decoder(mh.qwen2_config(**shape))
-        try:
-            dec.fill_random(20261201)
-            dec.fill_kv_random(1024, 20261202)
-            dec.set_persistent(True)
-            dec.generate_async(9707, 1024, 4, stream.cuda_stream)
-            torch.cuda.synchronize()
-            b.record(stream)
-            dec.generate_async(9707, 1028, launches, stream.cuda_stream)
-            e.record(stream)
-            torch.cuda.synchronize()
-        finally:
-            dec.close()
-        nbytes = sum(step_bytes(shape, 1028 + i) for i in range(launches)) // launches
     elif which in ("step_05b", "step_7b"):
         shape = dict(mh.QWEN25_05B if which == "step_05b" else mh.QWEN25_7B)
         position = 1024 if which == "step_05b" else 2040
@@ -753,9 +733,7 @@ def main() -> int:
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op launcher suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape secondary figure")
-    ap.add_argument("--no-persistent", action="store_true",
-                    help="skip the persistent-step figure (rocprofv3 does not survive its cooperative launch)")
-    ap.add_argument("--kernel-only", choices=["lm_head", "copy", "step_05b", "step_7b", "persistent_05b"],
+    ap.add_argument("--kernel-only", choices=["lm_head", "copy", "step_05b", "step_7b"],
                     help="only launch one kernel back to back, or whole decode steps kernel by kernel "
                          "(0.5B shape from cache row 1024, 7B shape from row 2040), for rocprofv3")
     ap.add_argument("--summarize-counters", metavar="DIR",
@@ -825,14 +803,6 @@ def main() -> int:
         "sampler": sampling, "tok_per_s": round(1000.0 / ms_s, 1), "ms_per_step": round(ms_s, 5),
         "sampler_ms_per_token": round(ms_s - ms, 5), "launches_per_step": launches_s,
     }
-    # The same greedy decode as one cooperative launch per token (the opt-in persistent step).
-    if not args.no_persistent:
-        ms_p, _, launches_p, ids_p, _ = time_decode(mh, torch, shape, args.position, args.steps, args.warmup, seed,
-                                                 persistent=True)
-        secondary["qwen2.5-0.5b-shape-persistent"] = {
-            "tok_per_s": round(1000.0 / ms_p, 1), "ms_per_step": round(ms_p, 5), "launches_per_step": launches_p,
-            "same_ids_as_graph_path": ids_p == ids,
-        }
     # Batched prefill of a 2048-token prompt, against feeding it one decode step per token (the
     # reference's feedToken loop) at this run's decode rate.
     secondary["qwen2.5-0.5b-shape-prefill"] = prefill_line(mh, torch, shape, 2048, 5, seed, ms)

@@ -286,18 +286,6 @@ int muyo_decoder_generated_ids(MuyoDecoder* decoder, int32_t* ids, uint32_t coun
 /* Number of kernel launches one step enqueues (for reporting). */
 uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* decoder);
 
-/* The persistent step: for shapes it supports (hidden <= 896, heads * head_dim <= 1024, an FFN of at
- * most 21 rows per CU, head_dim 64 or 128) one cooperative launch per token runs every layer and
- * the LM head, its workgroups handing activations to each other through device memory. It is
- * opt-in: the graph-replayed kernel sequence, which computes the same step, is the default because
- * it is faster on MI355X (each all-to-all hand-off costs about as much as a kernel boundary).
- * MUYO_E_UNSUPPORTED (with the reason) for other shapes. A persistent step
- * that gave up waiting on a hand-off (bounded waits) makes muyo_decoder_generate/step return
- * MUYO_E_STATE. No reference counterpart: it replaces the per-node dispatch of
- * src/FullModel.cpp:685-998 as a whole. */
-int muyo_decoder_set_persistent(MuyoDecoder* decoder, int on);
-int muyo_decoder_persistent(const MuyoDecoder* decoder);
-
 /* Kernels of one step, for per-kernel timing and profiling. */
 enum
 {

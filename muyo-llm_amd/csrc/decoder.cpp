@@ -9,10 +9,6 @@
 // that changes per token (token id, position, step counter) lives in device memory: the first
 // kernel of a step reduces the previous step's argmax partials into its token and advances the
 // position. Greedy generation therefore needs no host round trip between tokens.
-//
-// Shapes the persistent step supports (persistent.hpp) run instead as one cooperative launch per
-// token that covers every layer and the LM head when muyo_decoder_set_persistent selects it (the
-// graph path stays the default: it is the faster of the two); both compute the same step.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -21,7 +17,6 @@
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
-#include "persistent.hpp"
 #include "prefill.hpp"
 #include "sampler.hpp"
 
@@ -126,19 +121,6 @@ struct MuyoDecoder
     // used while the position is below ShortAttnKeys and o_proj merges the partials).
     hipGraph_t graph[2] = {nullptr, nullptr};
     hipGraphExec_t exec[2] = {nullptr, nullptr};
-
-    // The persistent step (persistent.hpp): its plan, and an arena of its own, allocated when the
-    // step is first selected, holding the transposed FFN_DOWN of every layer (rebuilt before a
-    // step whenever the weights may have changed), the per-layer pointer table, the hand-off
-    // packets and the control words.
-    const char* stepUnsupported = "not set up";
-    bool persistent = false;
-    bool downTDirty = true;
-    StepPlan plan{};
-    size_t stepPackets = 0;
-    char* stepArena = nullptr;
-    std::vector<uint16_t*> downT;
-    uint32_t* stepControl = nullptr;
 
     // Batched prefill (muyo_decoder_prefill): row-major activations of up to prefillRows prompt
     // tokens, allocated on first use. Split planes (hi, lo) feed the matrix cores.
@@ -366,59 +348,93 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
     return MUYO_OK;
 }
 
+/// The next step re-records its launches (eagerly, then a fresh capture).
+void DropGraph(MuyoDecoder* d)
+{
+    for (int v = 0; v < 2; ++v)
+    {
+        if (d->exec[v] != nullptr)
+        {
+            (void)hipGraphExecDestroy(d->exec[v]);
+            d->exec[v] = nullptr;
+        }
+        if (d->graph[v] != nullptr)
+        {
+            (void)hipGraphDestroy(d->graph[v]);
+            d->graph[v] = nullptr;
+        }
+    }
+    d->warm = false;
+}
+
+/// Captures the step with attention on `chunks` chunks per kv head into graph[variant] and
+/// instantiates it. Runs nothing.
+int CaptureStep(MuyoDecoder* d, int variant, uint32_t chunks)
+{
+    const uint32_t longChunks = d->dims.attnChunks;
+    const hipError_t begin = hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed);
+    if (begin != hipSuccess)
+    {
+        return HipStatus(begin, "graph capture");
+    }
+    d->dims.attnChunks = chunks;
+    const int status = Enqueue(d, d->stream);
+    d->dims.attnChunks = longChunks;
+    hipGraph_t graph = nullptr;
+    const hipError_t end = hipStreamEndCapture(d->stream, &graph);
+    if (status != MUYO_OK)
+    {
+        if (graph != nullptr)
+        {
+            (void)hipGraphDestroy(graph);
+        }
+        return status;
+    }
+    if (end != hipSuccess)
+    {
+        return HipStatus(end, "hipStreamEndCapture");
+    }
+    d->graph[variant] = graph;
+    MUYO_HIP_CHECK(hipGraphInstantiate(&d->exec[variant], d->graph[variant], nullptr, nullptr, 0));
+    return MUYO_OK;
+}
+
 /// The step at `position` on `s`: eager the first time, graph replay afterwards. While o_proj
 /// merges the attention partials and the position is below ShortAttnKeys, attention runs on
 /// kShortAttnChunks chunks, whose first round of key blocks then covers every key: half the
 /// partials for the merge to read (0.5B step at cache rows 960..1087: 0.561 -> 0.546 ms), where
-/// past that point the second round costs more than the merge saves.
+/// past that point the second round costs more than the merge saves. Both graphs are captured
+/// together, at the first replayed step, so crossing ShortAttnKeys later only switches between
+/// two hipGraphLaunch calls (no synchronisation, no capture).
 int RunStep(MuyoDecoder* d, hipStream_t s, int32_t position)
 {
     const uint32_t longChunks = d->dims.attnChunks;
     const int variant =
         d->mergeInOProj && static_cast<uint32_t>(position) < ShortAttnKeys(d->config.headDim) ? 1 : 0;
-    d->dims.attnChunks = variant == 1 ? kShortAttnChunks : longChunks;
-    int status = MUYO_OK;
     if (!d->warm)
     {
-        status = Enqueue(d, s);
-        d->warm = status == MUYO_OK;
+        d->dims.attnChunks = variant == 1 ? kShortAttnChunks : longChunks;
+        const int status = Enqueue(d, s);
         d->dims.attnChunks = longChunks;
+        d->warm = status == MUYO_OK;
         return status;
     }
-    if (d->exec[variant] == nullptr)
+    if (d->exec[0] == nullptr)
     {
-        // Capture on the decoder's own stream after everything queued on `s` has been ordered
-        // before it (the capture itself runs nothing).
-        hipError_t sync = hipStreamSynchronize(s);
-        if (sync == hipSuccess)
+        // Captured on the decoder's own stream once everything queued on `s` has run (the
+        // capture itself runs nothing).
+        MUYO_HIP_CHECK(hipStreamSynchronize(s));
+        int status = CaptureStep(d, 0, longChunks);
+        if (status == MUYO_OK && d->mergeInOProj)
         {
-            sync = hipStreamBeginCapture(d->stream, hipStreamCaptureModeRelaxed);
+            status = CaptureStep(d, 1, kShortAttnChunks);
         }
-        if (sync != hipSuccess)
-        {
-            d->dims.attnChunks = longChunks;
-            return HipStatus(sync, "graph capture");
-        }
-        status = Enqueue(d, d->stream);
-        hipGraph_t graph = nullptr;
-        const hipError_t end = hipStreamEndCapture(d->stream, &graph);
-        d->dims.attnChunks = longChunks;
         if (status != MUYO_OK)
         {
-            if (graph != nullptr)
-            {
-                (void)hipGraphDestroy(graph);
-            }
+            DropGraph(d);
             return status;
         }
-        if (end != hipSuccess)
-        {
-            return HipStatus(end, "hipStreamEndCapture");
-        }
-        d->graph[variant] = graph;
-        MUYO_HIP_CHECK(hipGraphInstantiate(&d->exec[variant], d->graph[variant], nullptr, nullptr, 0));
     }
-    d->dims.attnChunks = longChunks;
     MUYO_HIP_CHECK(hipGraphLaunch(d->exec[variant], s));
     return MUYO_OK;
 }
@@ -488,34 +504,6 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
             d->layers[static_cast<size_t>(l) * kLayerTensorCount + t] =
                 place(LayerTensorBytes(c, static_cast<LayerTensor>(t)));
         }
-    }
-    int cus = 0;
-    int current = 0;
-    if (hipGetDevice(&current) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, current) != hipSuccess || cus <= 0)
-    {
-        cus = 0;
-    }
-    d->stepUnsupported = StepUnsupported(c.hidden, c.feedForward, c.heads, c.kvHeads, c.headDim,
-                                         static_cast<uint32_t>(cus));
-    if (d->stepUnsupported == nullptr && c.layers > kStepMaxLayers)
-    {
-        d->stepUnsupported = "more than 64 layers";
-    }
-    if (d->stepUnsupported == nullptr && StepResidentPerCu() < 1)
-    {
-        d->stepUnsupported = "the step kernel does not fit a CU";
-    }
-    if (d->stepUnsupported == nullptr)
-    {
-        // The step's attention blocks may read a block of rows past the last value cache.
-        (void)place(static_cast<size_t>(kStepCacheSlackRows) * c.headDim * 2);
-        d->plan.hidden = c.hidden;
-        d->plan.ffn = c.feedForward;
-        d->plan.heads = c.heads;
-        d->plan.kvHeads = c.kvHeads;
-        d->plan.headDim = c.headDim;
-        d->stepPackets = StepPlanLayout(d->plan, static_cast<uint32_t>(cus));
     }
     const size_t qdim = static_cast<size_t>(c.heads) * c.headDim;
     const size_t group = c.heads / c.kvHeads;
@@ -643,12 +631,11 @@ extern "C" void muyo_decoder_destroy(MuyoDecoder* d)
     {
         (void)hipStreamSynchronize(d->stream);
     }
-    if (d->arena != nullptr || d->prefillArena != nullptr || d->stepArena != nullptr)
+    if (d->arena != nullptr || d->prefillArena != nullptr)
     {
         (void)hipDeviceSynchronize();
         (void)hipFree(d->arena);
         (void)hipFree(d->prefillArena);
-        (void)hipFree(d->stepArena);
     }
     if (d->stream != nullptr)
     {
@@ -711,7 +698,6 @@ extern "C" int muyo_decoder_tensor(MuyoDecoder* d, uint32_t kind, uint32_t layer
     if (device_ptr != nullptr)
     {
         *device_ptr = d->arena + slot.offset;
-        d->downTDirty = true;  // the caller may write the weights through the pointer
     }
     if (bytes != nullptr)
     {
@@ -735,7 +721,6 @@ extern "C" int muyo_decoder_upload(MuyoDecoder* d, uint32_t kind, uint32_t layer
     }
     MUYO_HIP_CHECK(hipMemcpyAsync(d->arena + slot.offset, host, bytes, hipMemcpyHostToDevice, d->stream));
     MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
-    d->downTDirty = true;
     return MUYO_OK;
 }
 
@@ -763,7 +748,6 @@ extern "C" int muyo_decoder_fill_random(MuyoDecoder* d, uint64_t seed)
     {
         return Fail(MUYO_E_NULL, "decoder is NULL");
     }
-    d->downTDirty = true;
     int status = FillTensor(d, d->tokenEmbd, true, muyo_tensor_seed(seed, MUYO_TENSOR_TOKEN_EMBD, 0), 0.0, 0.02);
     if (status == MUYO_OK)
     {
@@ -853,176 +837,6 @@ extern "C" int muyo_decoder_fill_kv_random(MuyoDecoder* d, uint32_t positions, u
     return MUYO_OK;
 }
 
-namespace
-{
-/// The persistent step's own arena (once per decoder, on first selection): the transposed FFN_DOWN
-/// of every layer (three rows of slack each), the per-layer pointer table, the hand-off packets
-/// (zeroed: epoch 0) and the control words, and the plan's pointers into it and the main arena.
-int SetUpStep(MuyoDecoder* d)
-{
-    if (d->stepArena != nullptr)
-    {
-        return MUYO_OK;
-    }
-    const MuyoQwen2Config& c = d->config;
-    size_t cursor = 0;
-    auto place = [&cursor](size_t bytes)
-    {
-        const size_t offset = cursor;
-        cursor = AlignUp(cursor + bytes);
-        return offset;
-    };
-    std::vector<size_t> downT(c.layers);
-    for (uint32_t l = 0; l < c.layers; ++l)
-    {
-        downT[l] = place((static_cast<size_t>(c.feedForward) + 3) * c.hidden * 2);
-    }
-    const size_t table = place(static_cast<size_t>(c.layers) * sizeof(StepLayer));
-    const size_t packets = place(d->stepPackets * sizeof(uint64_t));
-    const size_t control = place(kStepControlWords * sizeof(uint32_t));
-    char* arena = nullptr;
-    if (hipMalloc(reinterpret_cast<void**>(&arena), cursor) != hipSuccess)
-    {
-        return Fail(MUYO_E_NOMEM, "decoder: hipMalloc of the persistent step's %zu bytes failed", cursor);
-    }
-
-    StepPlan& p = d->plan;
-    p.layers = c.layers;
-    p.vocab = c.vocab;
-    p.maxSeq = c.maxSeq;
-    p.eps = c.rmsEps;
-    p.attnScale = d->dims.attnScale;
-    p.ropePow = d->dims.ropePow;
-    p.layer = reinterpret_cast<const StepLayer*>(arena + table);
-    p.embedding = d->At<uint16_t>(d->tokenEmbd);
-    p.head = d->At<uint16_t>(c.untiedOutput != 0 ? d->output : d->tokenEmbd);
-    p.outputNorm = d->At<float>(d->outputNorm);
-    p.logits = d->At<float>(d->logits);
-    p.state = d->state;
-    p.argValue = d->scratch.argValue;
-    p.argIndex = d->scratch.argIndex;
-    p.sampled = nullptr;
-    p.history = d->scratch.history;
-    p.historyCap = d->scratch.historyCap;
-    p.ids = d->ids;
-    p.idsCap = kIdsCapacity;
-    p.packets = reinterpret_cast<uint64_t*>(arena + packets);
-    p.control = reinterpret_cast<uint32_t*>(arena + control);
-    p.spinLimit = 1u << 20;
-    std::vector<StepLayer> rows(c.layers);
-    std::vector<uint16_t*> transposed(c.layers);
-    for (uint32_t l = 0; l < c.layers; ++l)
-    {
-        transposed[l] = reinterpret_cast<uint16_t*>(arena + downT[l]);
-        StepLayer& t = rows[l];
-        t.attnNorm = d->At<float>(d->Layer(l, kAttnNorm));
-        t.qkv = d->At<uint16_t>(d->Layer(l, kQkv));
-        t.qkvBias = d->At<float>(d->Layer(l, kQkvBias));
-        t.wo = d->At<uint16_t>(d->Layer(l, kOut));
-        t.ffnNorm = d->At<float>(d->Layer(l, kFfnNorm));
-        t.gate = d->At<uint16_t>(d->Layer(l, kGate));
-        t.up = d->At<uint16_t>(d->Layer(l, kUp));
-        t.downT = transposed[l];
-        t.kcache = d->At<uint16_t>(d->Layer(l, kKCache));
-        t.vcache = d->At<uint16_t>(d->Layer(l, kVCache));
-    }
-    // Hand-off epochs start at 1 (the zeroed packets carry epoch 0).
-    const uint32_t words[kStepControlWords] = {0, 0, 1, 0};
-    hipError_t st = hipMemsetAsync(arena, 0, cursor, d->stream);
-    if (st == hipSuccess)
-    {
-        st = hipMemcpyAsync(arena + table, rows.data(), rows.size() * sizeof(StepLayer), hipMemcpyHostToDevice,
-                            d->stream);
-    }
-    if (st == hipSuccess)
-    {
-        st = hipMemcpyAsync(p.control, words, sizeof(words), hipMemcpyHostToDevice, d->stream);
-    }
-    if (st == hipSuccess)
-    {
-        st = hipStreamSynchronize(d->stream);
-    }
-    if (st != hipSuccess)
-    {
-        (void)hipFree(arena);
-        return HipStatus(st, "decoder: persistent step tables");
-    }
-    d->stepArena = arena;
-    d->downT = std::move(transposed);
-    d->downTDirty = true;
-    d->stepControl = p.control;
-    return MUYO_OK;
-}
-
-/// The transposed FFN_DOWN copies, rebuilt when the weights may have changed since the last step.
-hipError_t EnsureDownT(MuyoDecoder* d, hipStream_t s)
-{
-    if (!d->downTDirty)
-    {
-        return hipSuccess;
-    }
-    for (uint32_t l = 0; l < d->config.layers; ++l)
-    {
-        const hipError_t st = LaunchTranspose16(s, d->At<uint16_t>(d->Layer(l, kDown)), d->downT[l],
-                                                d->config.hidden, d->config.feedForward);
-        if (st != hipSuccess)
-        {
-            return st;
-        }
-    }
-    d->downTDirty = false;
-    return hipSuccess;
-}
-
-/// `count` persistent steps: one cooperative launch per token (plus the sampler's kernels when
-/// sampling), the argmax partials one per workgroup.
-int GeneratePersistent(MuyoDecoder* d, hipStream_t s, int32_t token, int32_t position, uint32_t count)
-{
-    MUYO_HIP_CHECK(EnsureDownT(d, s));
-    const uint32_t grid = d->plan.grid;
-    d->plan.sampled = d->sampling ? d->sampledToken : nullptr;
-    DecodeScratch scratch = d->scratch;
-    scratch.sampled = d->sampling ? d->sampledToken : nullptr;
-    MUYO_HIP_CHECK(LaunchSetState(s, d->state, scratch, token, position, grid));
-    const MuyoQwen2Config& c = d->config;
-    for (uint32_t i = 0; i < count; ++i)
-    {
-        MUYO_HIP_CHECK(LaunchStep(s, d->plan));
-        if (d->sampling)
-        {
-            MUYO_HIP_CHECK(LaunchSample(s, d->At<float>(d->logits), d->sampleLogits, c.vocab, d->scratch.history,
-                                        &d->state->position, c.maxSeq, d->sample, d->rng,
-                                        SampleWorkspaceAt(d->sampleWorkspace, c.vocab, d->sample), d->sampledToken));
-        }
-    }
-    MUYO_HIP_CHECK(LaunchFinalize(s, d->state, scratch, grid, d->ids, kIdsCapacity));
-    return MUYO_OK;
-}
-
-/// After the stream has drained: a persistent step whose wait gave up reports it (and the
-/// control words are reset so the next call starts clean).
-int StepOutcome(MuyoDecoder* d)
-{
-    if (!d->persistent || d->stepControl == nullptr)
-    {
-        return MUYO_OK;
-    }
-    uint32_t words[2] = {0, 0};
-    MUYO_HIP_CHECK(hipMemcpy(words, d->stepControl, sizeof(words), hipMemcpyDeviceToHost));
-    if (words[kStepError] == 0 && words[kStepAbort] == 0)
-    {
-        return MUYO_OK;
-    }
-    static const uint32_t kClear[2] = {0, 0};
-    MUYO_HIP_CHECK(hipMemcpy(d->stepControl, kClear, sizeof(kClear), hipMemcpyHostToDevice));
-    static const char* const kWaits[] = {"q|k|v", "attention partials", "o_proj output", "down partials",
-                                         "layer output"};
-    const uint32_t which = words[kStepError];
-    return Fail(MUYO_E_STATE, "decoder: a persistent step gave up waiting for the %s hand-off; its output is void",
-                which >= 1 && which <= 5 ? kWaits[which - 1] : "(abandoned)");
-}
-}  // namespace
-
 extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_t position, uint32_t count,
                                            void* stream)
 {
@@ -1045,10 +859,6 @@ extern "C" int muyo_decoder_generate_async(MuyoDecoder* d, int32_t token, int32_
         return Fail(MUYO_E_RANGE, "decoder: at most %u steps per call", kIdsCapacity);
     }
     hipStream_t s = AsStream(stream);
-    if (d->persistent)
-    {
-        return GeneratePersistent(d, s, token, position, count);
-    }
     MUYO_HIP_CHECK(LaunchSetState(s, d->state, d->scratch, token, position, d->argBlocks));
     for (uint32_t i = 0; i < count; ++i)
     {
@@ -1087,11 +897,6 @@ extern "C" int muyo_decoder_generate(MuyoDecoder* d, int32_t token, int32_t posi
         return status;
     }
     MUYO_HIP_CHECK(hipStreamSynchronize(AsStream(stream)));
-    const int outcome = StepOutcome(d);
-    if (outcome != MUYO_OK)
-    {
-        return outcome;
-    }
     return ids != nullptr ? muyo_decoder_generated_ids(d, ids, count) : MUYO_OK;
 }
 
@@ -1112,31 +917,10 @@ extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
     {
         return 0;
     }
-    const uint32_t greedy = d->persistent ? 1u : 2u + (d->mergeInOProj || d->oProjGroups ? 5u : 6u) * d->config.layers;
+    const uint32_t greedy = 2u + (d->mergeInOProj || d->oProjGroups ? 5u : 6u) * d->config.layers;
     return greedy + (d->sampling ? SampleLaunches(d->config.vocab, d->sample, true) : 0u);
 }
 
-namespace
-{
-/// The next step re-records its launches (eagerly, then a fresh capture).
-void DropGraph(MuyoDecoder* d)
-{
-    for (int v = 0; v < 2; ++v)
-    {
-        if (d->exec[v] != nullptr)
-        {
-            (void)hipGraphExecDestroy(d->exec[v]);
-            d->exec[v] = nullptr;
-        }
-        if (d->graph[v] != nullptr)
-        {
-            (void)hipGraphDestroy(d->graph[v]);
-            d->graph[v] = nullptr;
-        }
-    }
-    d->warm = false;
-}
-}  // namespace
 
 extern "C" int muyo_decoder_set_sampler(MuyoDecoder* d, const MuyoSamplerParams* params)
 {
@@ -1472,32 +1256,4 @@ extern "C" int muyo_decoder_prefill(MuyoDecoder* d, const int32_t* tokens, uint3
         *next_token = next;
     }
     return MUYO_OK;
-}
-
-extern "C" int muyo_decoder_set_persistent(MuyoDecoder* d, int on)
-{
-    if (d == nullptr)
-    {
-        return Fail(MUYO_E_NULL, "decoder is NULL");
-    }
-    if (on != 0 && d->stepUnsupported != nullptr)
-    {
-        return Fail(MUYO_E_UNSUPPORTED, "decoder: no persistent step for this shape: %s", d->stepUnsupported);
-    }
-    MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
-    if (on != 0)
-    {
-        const int status = SetUpStep(d);
-        if (status != MUYO_OK)
-        {
-            return status;
-        }
-    }
-    d->persistent = on != 0;
-    return MUYO_OK;
-}
-
-extern "C" int muyo_decoder_persistent(const MuyoDecoder* d)
-{
-    return d != nullptr && d->persistent ? 1 : 0;
 }

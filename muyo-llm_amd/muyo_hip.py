@@ -166,8 +166,6 @@ _SIGNATURES = {
     "muyo_decoder_generate_async": (ctypes.c_int, [vp, i32, i32, u32, vp]),
     "muyo_decoder_generated_ids": (ctypes.c_int, [vp, vp, u32]),
     "muyo_decoder_launches_per_step": (u32, [vp]),
-    "muyo_decoder_set_persistent": (ctypes.c_int, [vp, ctypes.c_int]),
-    "muyo_decoder_persistent": (ctypes.c_int, [vp]),
     "muyo_decoder_set_state": (ctypes.c_int, [vp, i32, i32, vp]),
     "muyo_decoder_enqueue_kernel": (ctypes.c_int, [vp, u32, u32, vp]),
     "muyo_self_test": (ctypes.c_int, [ctypes.c_char_p]),
@@ -667,14 +665,6 @@ class Decoder:
 
     def launches_per_step(self) -> int:
         return int(self.lib.muyo_decoder_launches_per_step(self.handle))
-
-    def set_persistent(self, on: bool) -> None:
-        """One cooperative launch per token (where the shape allows) or the graph-replayed kernels."""
-        check(self.lib.muyo_decoder_set_persistent(self.handle, 1 if on else 0))
-
-    @property
-    def persistent(self) -> bool:
-        return bool(self.lib.muyo_decoder_persistent(self.handle))
 
     def set_state(self, token: int, position: int, stream: int = 0) -> None:
         check(self.lib.muyo_decoder_set_state(self.handle, token, position, stream))
