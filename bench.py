@@ -259,6 +259,103 @@ def time_kernels(mh, torch, shape, seed, rounds):
     return out
 
 
+def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
+    """Microseconds per launch of each per-layer kernel of the step (STEP_KINDS), each kind's
+    launches over every layer captured into one graph (torch's CUDAGraph around the decoder's
+    per-kernel launches) and replayed `reps` times: the kernels as the step's graph runs them,
+    minus their data dependence on the neighbouring kinds."""
+    stream = torch.cuda.Stream()
+    dec = mh.Decoder(mh.qwen2_config(**shape))
+    out = {}
+    try:
+        dec.fill_random(seed)
+        dec.fill_kv_random(position, seed + 1)
+        dec.set_state(9707, position, stream.cuda_stream)
+        for kind in STEP_KINDS:
+            for layer in range(shape["layers"]):
+                dec.enqueue_kernel(kind, layer, stream.cuda_stream)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for layer in range(shape["layers"]):
+                    dec.enqueue_kernel(kind, layer, stream.cuda_stream)
+            for _ in range(2):
+                graph.replay()
+            torch.cuda.synchronize()
+            b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                b.record(stream)
+                for _ in range(reps):
+                    graph.replay()
+                e.record(stream)
+            torch.cuda.synchronize()
+            out[kind.lower()] = 1000.0 * b.elapsed_time(e) / (reps * shape["layers"])
+            del graph
+    finally:
+        dec.close()
+    return out
+
+
+def floor_chain(byte_list, reps=20) -> dict:
+    """The streaming floor of a launch sequence (libmuyo_floor.so's muyo_floor_chain): each
+    launch only reads its algorithmic bytes from its own buffer region, chained in one hipGraph;
+    milliseconds per chain with 2, 3 and 4 workgroups of 512 threads per CU, and the best."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(ROOT / "muyo-llm_amd" / "libmuyo_floor.so"))
+    lib.muyo_floor_chain.restype = ctypes.c_int
+    lib.muyo_floor_chain.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.c_uint32, ctypes.POINTER(ctypes.c_double)]
+    arr = (ctypes.c_uint64 * len(byte_list))(*byte_list)
+    out = {}
+    for per_cu in (2, 3, 4):
+        ms = ctypes.c_double(0.0)
+        rc = lib.muyo_floor_chain(arr, len(byte_list), per_cu, reps, ctypes.byref(ms))
+        if rc != 0:
+            raise RuntimeError(f"muyo_floor_chain failed: hipError {rc}")
+        out[f"{per_cu}_per_cu_ms"] = round(ms.value, 5)
+    out["best_ms"] = min(v for k, v in out.items() if k.endswith("_ms"))
+    return out
+
+
+def floor_report(mh, torch, which: str) -> dict:
+    """The decode step beside its streaming floor. `which`: 05b (0.5B shape, cache rows
+    1014..1033, as the default bench line) or 7b (7B shape, rows 2032..2047).
+    chain: the step's launch sequence (embed, per layer qkv / attention / o_proj / gate_up / down,
+    LM head) with each launch's algorithmic bytes at the window's middle row, as pure streams;
+    phases: per kind, `layers` launches of its bytes as pure streams beside the step's own kernels
+    (time_phases), microseconds per launch."""
+    shape = dict(mh.QWEN25_05B if which == "05b" else mh.QWEN25_7B)
+    steps, warmup, centre = (20, 5, 1024) if which == "05b" else (16, 4, 2040)
+    seed = 20261201 if which == "05b" else 20261208
+    ms, positions, launches, _, median = time_decode(mh, torch, shape, centre, steps, warmup, seed)
+    position = positions[len(positions) // 2]
+    per_layer = [kernel_bytes(shape, kind.lower(), position) for kind in STEP_KINDS]
+    chain_bytes = [kernel_bytes(shape, "embed", position)] + per_layer * shape["layers"] + \
+        [kernel_bytes(shape, "lm_head", position)]
+    assert len(chain_bytes) == launches, (len(chain_bytes), launches)
+    chain = floor_chain(chain_bytes)
+    total = sum(chain_bytes)
+    step_bytes_mid = step_bytes(shape, position)
+    kernels = time_phases(mh, torch, shape, position, seed)
+    phases = {}
+    for kind, nbytes in zip(STEP_KINDS, per_layer):
+        stream_ms = floor_chain([nbytes] * shape["layers"])["best_ms"]
+        stream_us = 1000.0 * stream_ms / shape["layers"]
+        phases[kind.lower()] = {"bytes": nbytes, "stream_us": round(stream_us, 2),
+                                "kernel_us": round(kernels[kind.lower()], 2),
+                                "excess_us": round(kernels[kind.lower()] - stream_us, 2)}
+    return {
+        "shape": which, "positions": f"{positions[0]}..{positions[-1]}", "launches": launches,
+        "step_ms": round(ms, 5), "step_ms_median": round(median, 5),
+        "step_pct_of_peak": round(100 * step_bytes_mid / (ms * 1e-3) / 1e12 / 8, 1),
+        "chain_bytes": total, "chain": chain,
+        "chain_pct_of_peak": round(100 * total / (chain["best_ms"] * 1e-3) / 1e12 / 8, 1),
+        "step_over_chain": round(ms / chain["best_ms"], 3),
+        "phases": phases,
+    }
+
+
 def time_ops(mh, torch, reps: int = 10) -> dict:
     """Per-launch time of each per-op launcher at the batched shapes of the element-wise and
     reduction set (4096 rows at Qwen2.5-0.5B widths) and of the decode GEMV suite, through the C
@@ -733,6 +830,9 @@ def main() -> int:
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op launcher suite")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-7b", action="store_true", help="skip the 7B-shape secondary figure")
+    ap.add_argument("--floor", choices=["05b", "7b"],
+                    help="only the step beside its streaming floor (a chain of pure-read kernels with the step's "
+                         "launch count and bytes) and the per-phase kernels beside pure streams of their bytes")
     ap.add_argument("--kernel-only", choices=["lm_head", "copy", "step_05b", "step_7b"],
                     help="only launch one kernel back to back, or whole decode steps kernel by kernel "
                          "(0.5B shape from cache row 1024, 7B shape from row 2040), for rocprofv3")
@@ -770,6 +870,9 @@ def main() -> int:
     mh.load()
     if args.kernel_only:
         print(json.dumps(kernel_only(mh, torch, args.kernel_only, args.launches)), flush=True)
+        return 0
+    if args.floor:
+        print(json.dumps(floor_report(mh, torch, args.floor)), flush=True)
         return 0
     if args.ops_only:
         print(json.dumps({"kernels": time_ops(mh, torch, reps=3)}), flush=True)
