@@ -43,7 +43,6 @@ constexpr int kDirectThreads = 64;  // workgroup size of the register-direct GEM
 constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
 constexpr uint32_t kWideUnits = 2048;  // most units of a short-row GEMV launched a wave per unit
 constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
-constexpr uint32_t kMergeSlots = 512;  // (head, chunk) weights that prologue holds in LDS
 
 uint32_t CuCount()
 {
@@ -145,7 +144,7 @@ struct MergeStage
     const float* attnSum;
     const float* attnAcc;
     uint32_t heads, group, headDim, gridChunks;
-    static constexpr bool kCanDirect = false;  // the per-head weights are shared through LDS
+    static constexpr bool kCanDirect = false;  // the merged row is shared through LDS
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = false;
 
@@ -154,73 +153,58 @@ struct MergeStage
         return (static_cast<uint64_t>(h / group) * gridChunks + min(c, gridChunks - 1)) * group + h % group;
     }
 
+    /// Thread t owns channels 4t..4t+3 of the q dim (one head) and merges them on its own: every
+    /// (max, sum, P.V) slot of that head is requested at once (float4 P.V loads), the weights
+    /// 2^(m_c - M) are worked out per thread, and one barrier publishes the merged row.
     template <int kThreads, int kVec>
     __device__ void Run(float4* xs, uint32_t n) const
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
-        __shared__ float weight[kMergeSlots];
         const uint32_t nchunks = n / 8;
-        uint32_t items[kMergeItems];
-        float acc[kMergeItems][kChunks];
+        const uint32_t t = min(threadIdx.x, n / 4 - 1);
+        const uint32_t h = 4 * t / headDim;
+        const uint32_t d = 4 * t % headDim;
+        float m[kChunks];
+        float l[kChunks];
+        float4 a[kChunks];
 #pragma unroll
-        for (uint32_t k = 0; k < kMergeItems; ++k)
+        for (uint32_t c = 0; c < kChunks; ++c)
         {
-            items[k] = min(threadIdx.x + k * kBlock, n - 1);
-            const uint32_t h = items[k] / headDim;
+            const uint64_t slot = Slot(h, c);
+            m[c] = c < gridChunks ? attnMax[slot] : -INFINITY;
+            l[c] = attnSum[slot];
+            a[c] = *reinterpret_cast<const float4*>(attnAcc + slot * headDim + d);
+        }
+        float top = -INFINITY;
+#pragma unroll
+        for (uint32_t c = 0; c < kChunks; ++c)
+        {
+            top = fmaxf(top, m[c]);
+        }
+        float4 num = {0.0f, 0.0f, 0.0f, 0.0f};
+        float den = 0.0f;
+        if (top != -INFINITY)
+        {
 #pragma unroll
             for (uint32_t c = 0; c < kChunks; ++c)
             {
-                acc[k][c] = attnAcc[Slot(h, c) * headDim + items[k] % headDim];
+                const float e = exp2f(m[c] - top);  // 0 for neutral and absent slots
+                num.x = fmaf(e, a[c].x, num.x);
+                num.y = fmaf(e, a[c].y, num.y);
+                num.z = fmaf(e, a[c].z, num.z);
+                num.w = fmaf(e, a[c].w, num.w);
+                den = fmaf(e, l[c], den);
             }
         }
-        if (threadIdx.x < heads)
+        float4 out = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (den > 0.0f)
         {
-            const uint32_t h = threadIdx.x;
-            float m[kChunks];
-            float l[kChunks];
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                m[c] = c < gridChunks ? attnMax[Slot(h, c)] : -INFINITY;
-                l[c] = attnSum[Slot(h, c)];
-            }
-            float top = -INFINITY;
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                top = fmaxf(top, m[c]);
-            }
-            float den = 0.0f;
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                m[c] = top == -INFINITY ? 0.0f : exp2f(m[c] - top);  // 0 for neutral and absent slots
-                den = fmaf(m[c], l[c], den);
-            }
-            const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                weight[h * kChunks + c] = m[c] * inv;
-            }
+            out = float4{num.x / den, num.y / den, num.z / den, num.w / den};
         }
-        __syncthreads();
-        float* flat = reinterpret_cast<float*>(xs);
-#pragma unroll
-        for (uint32_t k = 0; k < kMergeItems; ++k)
+        if (4 * threadIdx.x < n)
         {
-            const uint32_t h = items[k] / headDim;
-            float out = 0.0f;
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                out = fmaf(weight[h * kChunks + c], acc[k][c], out);
-            }
-            const uint32_t item = threadIdx.x + k * kBlock;
-            if (item < n)
-            {
-                flat[SplitSlot(item, nchunks)] = out;
-            }
+            // Channels 4t..4t+3 are half of chunk t/2: its low float4 when t is even.
+            xs[(threadIdx.x & 1u) ? nchunks + threadIdx.x / 2 : threadIdx.x / 2] = out;
         }
         __syncthreads();
     }
@@ -1731,7 +1715,7 @@ uint32_t LmHeadBlocks(const DecodeDims& dims)
 bool MergeInOProj(const DecodeDims& dims)
 {
     const uint32_t qdim = dims.heads * dims.headDim;
-    return qdim <= kMergeItems * kBlock && dims.heads * kMergeAttnChunks <= kMergeSlots;
+    return qdim <= kMergeItems * kBlock && dims.headDim % 4 == 0;
 }
 
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
