@@ -13,10 +13,11 @@ rows 0..p read once as fp16, the appended rows written, activations as f32 once 
 reads or writes them. tok/s is reported beside it.
 
 roofline: the kernel with the largest share of the step's time, the fused gate/up (rms_norm
-prologue + 2 x 4864 x 896 fp16 GEMV + swiglu; 25.9 % of the step by rocprofv3's kernel trace),
-timed with HIP events on its stream while it rotates over the 24 layers' weights (420 MB, more
-than the 256 MB MALL); its HBM traffic and L2 hit rate come from the counter runs of the same
-kernel inside whole steps.
+prologue + 2 x 4864 x 896 fp16 GEMV + swiglu), timed with HIP events on its stream while it
+rotates over the 24 layers' weights (420 MB, more than the 256 MB MALL); its share of the step
+comes from this run's per-kind timing (phases_us: each kernel kind graph-replayed over the 24
+layers); its HBM traffic and L2 hit rate come from the counter runs of the same kernel inside
+whole steps (traffic_source names them).
 
 cpu_baseline: the reference's CPU path for the same workload (oracle/'s f32 step: HostMatVec-
 order f32 sums, gcc -O3) on one host core, the median of 10 single-step timings; the same with
@@ -48,6 +49,8 @@ MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core flop/s of MI355X
 # (profiles/decode_step_counters_0.5b.md: `--kernel-only step_05b`, `--summarize-counters`).
 GATE_UP_TRAFFIC_BYTES = 17_608_160
 GATE_UP_L2_HIT_RATE = 0.154
+GATE_UP_COUNTER_SOURCE = ("profiles/decode_step_counters_0.5b.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (each scaled "
+                          "by a 256 MiB device copy) and TCC_HIT/TCC_MISS over whole steps, gate/up rows")
 
 
 def step_bytes(c: dict, position: int) -> int:
@@ -892,6 +895,9 @@ def main() -> int:
     value = total_bytes / (ms * 1e-3 * args.steps) / 1e9
 
     kern = time_kernels(mh, torch, shape, seed, rounds=64)
+    # Each kernel kind of the step, graph-replayed over the 24 layers at the timed window's middle
+    # row: the roofline kernel's share of the step comes from these, not from a profile.
+    phases = time_phases(mh, torch, shape, positions[len(positions) // 2], seed)
     ops = {} if args.no_ops else time_ops(mh, torch)
     lm_gbs = lm_head_bytes(shape) / (kern["lm_head_ms"] * 1e-3) / 1e9
     gu_gbs = gate_up_bytes(shape) / (kern["gate_up_ms"] * 1e-3) / 1e9
@@ -955,9 +961,10 @@ def main() -> int:
             "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
             "traffic": GATE_UP_TRAFFIC_BYTES,
             "l2_hit_rate": GATE_UP_L2_HIT_RATE,
+            "traffic_source": GATE_UP_COUNTER_SOURCE,
             "launch_ms": round(kern["gate_up_ms"], 5),
             "bytes_per_launch": gate_up_bytes(shape),
-            "share_of_step": 0.259,
+            "share_of_step": round(phases["gate_up"] * shape["layers"] / (ms * 1000.0), 3),
             "note": "rotated over the 24 layers' weights (420 MB > MALL)",
         },
         "kernels": {
@@ -965,6 +972,7 @@ def main() -> int:
                         "bytes_per_launch": lm_head_bytes(shape), "frac": round(lm_gbs / HBM_PEAK_GBS, 4)},
             **ops,
         },
+        "phases_us": {k: round(v, 2) for k, v in phases.items()},
         "secondary": secondary,
         "greedy_ids_head": ids[:8],
     }

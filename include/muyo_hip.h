@@ -18,6 +18,12 @@
  *
  * Ownership: the caller owns every buffer passed to a launcher; launchers do not retain
  * pointers beyond the call. The decoder (below) owns the buffers it allocates.
+ *
+ * Threads and devices: launchers may be called from several host threads, on any device; each
+ * launches on the calling thread's current device. What they cache on the host (a device's CU
+ * count, a kernel's occupancy and its LDS opt-in) is kept per device and filled on first use
+ * under a lock. A decoder belongs to the device that was current when it was created and must
+ * be used with that device current, from one thread at a time.
  */
 #ifndef MUYO_HIP_H
 #define MUYO_HIP_H

@@ -24,6 +24,7 @@
 // and the next row's batch before the current row's reduction. Work that does not depend on the
 // dot products (the rope angle's cosine and sine) runs while the loads are in flight.
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 #include "common.hpp"
@@ -44,21 +45,35 @@ constexpr uint32_t kNoLimit = 0xFFFFFFFFu;
 constexpr uint32_t kWideUnits = 2048;  // most units of a short-row GEMV launched a wave per unit
 constexpr uint32_t kMergeItems = 4;    // q channels per thread in the o_proj merge prologue (q dim <= 1024)
 
+// Host-side launch caches are kept per device (the current device of the calling thread) and
+// are safe to use from several host threads: device attributes are read once per device, and
+// each GEMV kernel's occupancy and LDS opt-in are tracked per device under that kernel's lock.
+constexpr int kMaxDevices = 64;
+
+int CurrentDevice()
+{
+    int device = 0;
+    return hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices ? device : 0;
+}
+
+/// CUs of the current device, read once per device (threads racing on the first read store the
+/// same value).
 uint32_t CuCount()
 {
-    static uint32_t cus = 0;
-    if (cus == 0)
+    static std::atomic<uint32_t> cus[kMaxDevices];
+    const int device = CurrentDevice();
+    uint32_t count = cus[device].load(std::memory_order_relaxed);
+    if (count == 0)
     {
-        int device = 0;
-        int count = 0;
-        if (hipGetDevice(&device) != hipSuccess ||
-            hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || count <= 0)
+        int value = 0;
+        if (hipDeviceGetAttribute(&value, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || value <= 0)
         {
-            count = 256;
+            value = 256;
         }
-        cus = static_cast<uint32_t>(count);
+        count = static_cast<uint32_t>(value);
+        cus[device].store(count, std::memory_order_relaxed);
     }
-    return cus;
+    return count;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -781,6 +796,47 @@ struct ResidualEpi
     }
 };
 
+/// out[row] = (W[row] . x + bias0[row]) + bias1[row], each bias only when given: the per-op
+/// GEMV's FUSE0/FUSE1 in mul_mat_vec_base.glsl's order.
+struct BiasEpi
+{
+    static constexpr uint32_t kResidentRounds = 2;  // as the LM heads: long launches balance better
+    const uint16_t* w;
+    const float* bias0;
+    const float* bias1;
+    float* out;
+    uint32_t rows, cols;
+
+    __device__ uint32_t Units() const { return rows; }
+    __device__ const uint16_t* Row(uint32_t unit, int) const { return w + static_cast<uint64_t>(unit) * cols; }
+    struct Pre
+    {
+        float b0, b1;
+    };
+    __device__ Pre Prefetch(uint32_t unit) const
+    {
+        return Pre{bias0 != nullptr ? bias0[unit] : 0.0f, bias1 != nullptr ? bias1[unit] : 0.0f};
+    }
+    __device__ void Ready(Pre&) const {}
+    __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
+    {
+        float value = s[0];
+        if (bias0 != nullptr)
+        {
+            value += pre.b0;
+        }
+        if (bias1 != nullptr)
+        {
+            value += pre.b1;
+        }
+        out[unit] = value;
+    }
+    template <int kThreads>
+    __device__ void Tail(float, int32_t) const
+    {
+    }
+};
+
 struct GateUpEpi
 {
     // Two rounds of resident workgroups (7B gate/up 44.1 -> 43.0 us; the 0.5B one covers its
@@ -925,24 +981,32 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
                             uint32_t cols, const Stage& stage, const Epi& epi, GemvShape* shapeOut)
 {
     const auto kernel = kKernel;
-    // Cached per kernel (the statics belong to this instantiation).
-    static size_t residentLds = 0;
-    static uint32_t resident = 0;
-    if (resident == 0 || residentLds != lds)
+    // Per device, for this kernel instantiation: the resident workgroups at the last LDS size
+    // asked for, and the dynamic LDS the kernel has been opted in to (64 KB by default).
+    struct Cache
     {
-        resident = ResidentBlocks(kernel, kThreads, lds);
-        residentLds = lds;
+        std::mutex mutex;
+        uint32_t resident[kMaxDevices] = {};
+        size_t residentLds[kMaxDevices] = {};
+        size_t configured[kMaxDevices] = {};
+    };
+    static Cache cache;
+    std::lock_guard<std::mutex> lock(cache.mutex);
+    const int device = CurrentDevice();
+    if (cache.resident[device] == 0 || cache.residentLds[device] != lds)
+    {
+        cache.resident[device] = ResidentBlocks(kernel, kThreads, lds);
+        cache.residentLds[device] = lds;
     }
-    const uint32_t blocks =
-        std::max(1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, ResidentRounds<Epi>::value * resident}));
+    const uint32_t blocks = std::max(
+        1u, std::min({CeilDiv(units, unitsPerBlock), blockCap, ResidentRounds<Epi>::value * cache.resident[device]}));
     if (shapeOut != nullptr)
     {
         *shapeOut = GemvShape{blocks, unitsPerBlock};
         return hipSuccess;
     }
     // Opt in to more than the default 64 KB of dynamic LDS only when a launch needs it.
-    static size_t configured = 64 * 1024;
-    if (lds > configured)
+    if (lds > std::max<size_t>(64 * 1024, cache.configured[device]))
     {
         const hipError_t status = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -951,7 +1015,7 @@ hipError_t LaunchGemvKernel(hipStream_t s, uint32_t units, uint32_t unitsPerBloc
         {
             return status;
         }
-        configured = lds;
+        cache.configured[device] = lds;
     }
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, cols, stage, epi);
     return hipGetLastError();
@@ -1872,6 +1936,13 @@ hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x
     return LaunchFused<1>(s, rows, kNoLimit, cols, PlainStage{x}, epi);
 }
 
+hipError_t LaunchMatVecBias(hipStream_t s, const uint16_t* w, const float* x, const float* bias0, const float* bias1,
+                            float* out, uint32_t rows, uint32_t cols)
+{
+    BiasEpi epi{w, bias0, bias1, out, rows, cols};
+    return LaunchFused<1>(s, rows, kNoLimit, cols, PlainStage{x}, epi);
+}
+
 hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                               const uint16_t* wgate, const uint16_t* wup, float* act)
 {
@@ -2007,7 +2078,6 @@ static __device__ __align__(256) float scratch[kStaticScratchFloats];
 
 namespace
 {
-constexpr int kMaxDevices = 64;
 std::mutex g_scratchMutex;
 float* g_scratchAddress[kMaxDevices] = {};
 

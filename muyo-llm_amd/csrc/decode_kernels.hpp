@@ -136,6 +136,11 @@ hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols);
 
+/// out[row] = (W[row] . x + bias0[row]) + bias1[row] (null biases skipped) on the fused GEMV's
+/// launch shapes: W fp16 [rows][cols] with 16-byte aligned rows, x 16-byte aligned, cols % 8 == 0.
+hipError_t LaunchMatVecBias(hipStream_t s, const uint16_t* w, const float* x, const float* bias0, const float* bias1,
+                            float* out, uint32_t rows, uint32_t cols);
+
 hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                               const uint16_t* wgate, const uint16_t* wup, float* act);
 

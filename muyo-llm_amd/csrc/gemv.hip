@@ -13,6 +13,7 @@
 #include <algorithm>
 
 #include "common.hpp"
+#include "decode_kernels.hpp"
 #include "gemv_core.hpp"
 
 namespace muyo
@@ -447,7 +448,15 @@ int LaunchMatVec(const char* name, const LlamaMatVecPushConstants* pc, const Muy
     hipStream_t s = AsStream(stream);
 
     hipError_t status;
-    if (fast && sizeof(AT) == 2)
+    if (fast && sizeof(AT) == 2 && gy == 1 && pc->baseWorkGroupY == 0)
+    {
+        // One batch: the decode step's fused GEMV with its launch-shape choice (register-direct
+        // 64-thread workgroups for grids within the CUs, single-wave or whole-wave rows beyond).
+        status = LaunchMatVecBias(s, reinterpret_cast<const uint16_t*>(a), b,
+                                  (g.fusion & LLAMA_MAT_VEC_FUSION_BIAS0) ? fuse0 : nullptr,
+                                  (g.fusion & LLAMA_MAT_VEC_FUSION_BIAS1) ? fuse1 : nullptr, d, rows, g.ncols);
+    }
+    else if (fast && sizeof(AT) == 2)
     {
         status = DispatchFastF16(gy, lds, s, reinterpret_cast<const uint16_t*>(a), b, d, fuse0, fuse1, g);
     }

@@ -39,10 +39,16 @@ def test_decoder_weights_match_oracle_bits(mh, gpu, orc):
             assert np.array_equal(download(dec, kind, layer, arr), arr), (kind, layer)
 
 
-def test_decoder_small_steps_match_oracle(mh, gpu, orc):
-    dec, model = make_pair(mh, orc, SMALL, seed=11, kv_positions=30, kv_seed=12)
+@pytest.mark.parametrize("untied", [False, True], ids=["tied", "untied"])
+def test_decoder_small_steps_match_oracle(mh, gpu, orc, untied):
+    """12 steps fed back token by token. With the LM head tied to the embedding, a model this small
+    maps a token back to itself (17 at every step); the untied head makes the ids change, so the
+    token path (embedding row, rope position, cache rows of a new token) is exercised too."""
+    shape = dict(SMALL, untied_output=untied)
+    dec, model = make_pair(mh, orc, shape, seed=11, kv_positions=30, kv_seed=12)
     with dec:
         token = 17
+        seen = []
         for i in range(12):
             pos = 30 + i
             got = dec.step(token, pos)
@@ -52,6 +58,9 @@ def test_decoder_small_steps_match_oracle(mh, gpu, orc):
             assert worst(gpu_logits, logits) < 1e-4
             assert got == want, f"step {i}: gpu {got} oracle {want} (margin {top1 - top2:.3g})"
             token = got
+            seen.append(got)
+        if untied:
+            assert len(set(seen)) > 3, seen
         # The appended cache rows hold the same fp16 values (bit-exact up to last-bit rounding).
         for layer in range(SMALL["layers"]):
             for kind in ("KCACHE", "VCACHE"):
@@ -121,8 +130,9 @@ def test_decoder_odd_shapes_match_oracle(mh, gpu, orc, name):
 
 
 def test_decoder_graph_replay_matches_eager_steps(mh, gpu, orc):
-    """generate() (one hipGraph launch per token, ids fed back on the device) == step-by-step."""
-    cfg = mh.qwen2_config(**SMALL)
+    """generate() (one hipGraph launch per token, ids fed back on the device) == step-by-step, with
+    an untied LM head so the ids change from step to step."""
+    cfg = mh.qwen2_config(**SMALL, untied_output=True)
     with mh.Decoder(cfg) as dec:
         dec.fill_random(21)
         dec.fill_kv_random(10, 22)
@@ -135,6 +145,7 @@ def test_decoder_graph_replay_matches_eager_steps(mh, gpu, orc):
             token = dec.step(token, 10 + i)
             stepped.append(token)
     assert ids == again == stepped
+    assert len(set(ids)) > 1, ids
 
 
 @pytest.mark.parametrize("position", [128, 1024, 2016])
