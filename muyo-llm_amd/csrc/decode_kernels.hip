@@ -723,8 +723,7 @@ struct QkvEpi
     {
         // rope_neox (rope_funcs.glsl:76-114): theta = pos * theta_scale^j, pair (j, j + hd/2).
         const float theta = static_cast<float>(pre.pos) * pre.pow;
-        pre.cos = cosf(theta);
-        pre.sin = sinf(theta);
+        sincosf(theta, &pre.sin, &pre.cos);  // one range reduction for both
         asm volatile("" : "+v"(pre.cos), "+v"(pre.sin));
     }
 
@@ -1739,8 +1738,9 @@ __global__ __launch_bounds__(kBlock) void RopeAppendKernel(const float* __restri
         const uint32_t j = item % half;
         const float* src = head < heads ? q + head * headDim : k + (head - heads) * headDim;
         const float theta = static_cast<float>(pos) * powf(thetaScale, static_cast<float>(j));
-        const float c = cosf(theta);
-        const float s = sinf(theta);
+        float c;
+        float s;
+        sincosf(theta, &s, &c);
         const float x0 = src[j];
         const float x1 = src[j + half];
         const float o0 = x0 * c - x1 * s;

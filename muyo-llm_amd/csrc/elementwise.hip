@@ -234,8 +234,11 @@ __device__ __forceinline__ void RopeAngleWith(const LlamaRopePushConstants& p, f
     {
         theta = -theta;
     }
-    c = cosf(theta) * mscale;
-    s = sinf(theta) * mscale;
+    float cs;
+    float sn;
+    sincosf(theta, &sn, &cs);  // one range reduction for both
+    c = cs * mscale;
+    s = sn * mscale;
 }
 
 __device__ __forceinline__ void RopeAngle(const LlamaRopePushConstants& p, const float* __restrict__ ff, uint32_t iw,

@@ -341,8 +341,9 @@ __global__ __launch_bounds__(256) void RopeSplitAppendKernel(const float* __rest
         const float s0 = value(head * headDim + j);
         const float s1 = value(head * headDim + j + half);
         const float theta = static_cast<float>(pos) * ropePow[j];
-        const float c = cosf(theta);
-        const float sn = sinf(theta);
+        float c;
+        float sn;
+        sincosf(theta, &sn, &c);
         const float o0 = s0 * c - s1 * sn;
         const float o1 = s0 * sn + s1 * c;
         if (head < heads)
@@ -426,8 +427,7 @@ __global__ __launch_bounds__(256) void RopeSplitAppendQuadKernel(const float* __
         for (int e = 0; e < 4; ++e)
         {
             const float theta = static_cast<float>(pos) * power[e];
-            c[e] = cosf(theta);
-            sn[e] = sinf(theta);
+            sincosf(theta, &sn[e], &c[e]);
         }
         float o0[4];
         float o1[4];
