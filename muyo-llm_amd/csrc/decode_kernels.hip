@@ -78,6 +78,13 @@ uint32_t CuCount()
 
 // ------------------------------------------------------------------------------------------------
 // Activation staging policies (each fills the LDS split layout and ends synchronised).
+//
+// A norm stage (kNorm) stages x * w, the rms_norm weight applied but not the row's factor
+// rsqrt(mean(x^2) + eps): the kernels multiply their row sums by that factor after the dot, so
+// the norm's reduction overlaps the weight stream instead of standing between the activation's
+// arrival and the first product. Run returns the factor (1 without a norm); Direct returns this
+// lane's part of sum(x^2) (0 without a norm), which the kernel reduces with its dot products.
+// The column-quarter kernel (FusedMatVecColumns) keeps a prologue of its own that scales x.
 
 struct PlainStage
 {
@@ -85,15 +92,16 @@ struct PlainStage
     static constexpr bool kCanDirect = true;  // see DirectStage
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = true;  // any column range stages on its own
+    static constexpr bool kNorm = false;
     template <int kLpr, int kCpl, class Between>
-    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
+    __device__ float Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
     {
-        LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, 0.0f, lir, xlo, xhi, between);
+        return LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, lir, xlo, xhi, between);
     }
     template <int kThreads, int kVec>
-    __device__ void Run(float4* xs, uint32_t n) const
+    __device__ float Run(float4* xs, uint32_t n) const
     {
-        StageSplit<kThreads, kVec, false>(x, nullptr, n, 0.0f, xs);
+        return StageSplit<kThreads, kVec, false>(x, nullptr, n, 0.0f, xs);
     }
 };
 
@@ -105,15 +113,16 @@ struct NormStage
     static constexpr bool kCanDirect = true;
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = false;  // the norm needs the whole row
+    static constexpr bool kNorm = true;
     template <int kLpr, int kCpl, class Between>
-    __device__ void Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
+    __device__ float Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
     {
-        LoadActivationDirect<kLpr, kCpl, true>(x, w, n, eps, lir, xlo, xhi, between);
+        return LoadActivationDirect<kLpr, kCpl, true>(x, w, n, lir, xlo, xhi, between);
     }
     template <int kThreads, int kVec>
-    __device__ void Run(float4* xs, uint32_t n) const
+    __device__ float Run(float4* xs, uint32_t n) const
     {
-        StageSplit<kThreads, kVec, true>(x, w, n, eps, xs);
+        return StageSplit<kThreads, kVec, true>(x, w, n, eps, xs);
     }
 };
 
@@ -130,10 +139,11 @@ struct PartsNormStage
     float* sum;
     static constexpr bool kCanDirect = false;  // the sum is stored once, through the staging path
     static constexpr bool kDirect = false;
+    static constexpr bool kNorm = true;
     template <int kThreads, int kVec>
-    __device__ void Run(float4* xs, uint32_t n) const
+    __device__ float Run(float4* xs, uint32_t n) const
     {
-        StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr);
+        return StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr);
     }
 };
 
@@ -162,6 +172,7 @@ struct MergeStage
     static constexpr bool kCanDirect = false;  // the merged row is shared through LDS
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = false;
+    static constexpr bool kNorm = false;
 
     __device__ uint64_t Slot(uint32_t h, uint32_t c) const
     {
@@ -172,7 +183,7 @@ struct MergeStage
     /// (max, sum, P.V) slot of that head is requested at once (float4 P.V loads), the weights
     /// 2^(m_c - M) are worked out per thread, and one barrier publishes the merged row.
     template <int kThreads, int kVec>
-    __device__ void Run(float4* xs, uint32_t n) const
+    __device__ float Run(float4* xs, uint32_t n) const
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
         const uint32_t nchunks = n / 8;
@@ -222,6 +233,7 @@ struct MergeStage
             xs[(threadIdx.x & 1u) ? nchunks + threadIdx.x / 2 : threadIdx.x / 2] = out;
         }
         __syncthreads();
+        return 1.0f;
     }
 };
 
@@ -290,25 +302,34 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
         }
         float4 xlo[kCpl];
         float4 xhi[kCpl];
+        // A directly staged norm leaves each lane its part of sum(x^2), reduced over the segment
+        // with every unit's row sums (one more value in the same lane permutes).
+        constexpr bool kLaneNorm = Stage::kDirect && Stage::kNorm;
+        float scale = 1.0f;
+        float squares = 0.0f;
         // The epilogue's own work (Ready) runs while the weights and the activation are in flight.
         if constexpr (Stage::kDirect)
         {
-            stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] { epi.Ready(pre); });
+            squares = stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] { epi.Ready(pre); });
         }
         else
         {
             epi.Ready(pre);
-            stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols);
+            scale = stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols);
             LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
         }
         for (; first < units; first += stride)
         {
             const uint32_t unit = first + unitInWave;
-            float sums[kNr];
+            float sums[kNr + (kLaneNorm ? 1 : 0)];
 #pragma unroll
             for (int r = 0; r < kNr; ++r)
             {
                 sums[r] = unit < units ? DotRegisters<kLpr, kCpl>(w[r], xlo, xhi, nchunks, lir) : 0.0f;
+            }
+            if constexpr (kLaneNorm)
+            {
+                sums[kNr] = squares;
             }
             // The next unit's rows go out before this unit's reduction and epilogue; with a single
             // buffer per wave the other resident waves keep the memory busy meanwhile.
@@ -321,9 +342,19 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
             }
             // Every lane of the segment ends with the unit's row sums.
             GroupSumN<kLpr>(sums);
+            if constexpr (kLaneNorm)
+            {
+                scale = NormScale(sums[kNr], cols, stage.eps);
+            }
+            float rowSums[kNr];
+#pragma unroll
+            for (int r = 0; r < kNr; ++r)
+            {
+                rowSums[r] = Stage::kNorm ? sums[r] * scale : sums[r];
+            }
             if (unit < units && lir == 0)
             {
-                epi.Finish(unit, sums, pre, bestValue, bestIndex);
+                epi.Finish(unit, rowSums, pre, bestValue, bestIndex);
             }
             pre = next;
         }
@@ -338,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
             LoadBatch<kLpr, kCpl>(epi.Row(first + unitInWave, part), 0, nchunks, lir, w);
             epi.Ready(pre);
         }
-        stage.template Run<kBlock, kStageVec>(xs, cols);
+        const float scale = stage.template Run<kBlock, kStageVec>(xs, cols);
         const float4* lo = xs;
         const float4* hi = xs + nchunks;
         for (; first < units; first += stride)
@@ -361,6 +392,10 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
             // Every lane of a segment holds its row's sum; the unit's second row sits in the
             // partner segment.
             dot = GroupSum<kLpr>(dot);
+            if constexpr (Stage::kNorm)
+            {
+                dot *= scale;
+            }
             float sums[kNr];
             sums[0] = dot;
             if constexpr (kNr == 2)
@@ -390,6 +425,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
     float bestValue = -INFINITY;
     int32_t bestIndex = 0x7FFFFFFF;
     uint32_t parity = 0;
+    float scale = 1.0f;  // the rms_norm factor of a norm stage
     auto finish = [&](uint32_t unit, float dot, const typename Epi::Pre& pre) {
         dot = GroupSum<kWave>(dot);
         if ((threadIdx.x & (kWave - 1)) == 0)
@@ -400,6 +436,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         if (threadIdx.x == 0)
         {
             float sums[1] = {(partial[parity][0] + partial[parity][1]) + (partial[parity][2] + partial[parity][3])};
+            if constexpr (Stage::kNorm)
+            {
+                sums[0] *= scale;
+            }
             epi.Finish(unit, sums, pre, bestValue, bestIndex);
         }
         parity ^= 1u;
@@ -416,7 +456,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecBlockRow(uint32_t cols, Sta
         LoadBatch<kBlock, kCpl>(epi.Row(unit, 0), 0, nchunks, lir, wa);
         epi.Ready(pa);
     }
-    stage.template Run<kBlock, kStageVec>(xs, cols);
+    scale = stage.template Run<kBlock, kStageVec>(xs, cols);
     const float4* lo = xs;
     const float4* hi = xs + nchunks;
     for (; unit < units; unit += 2 * gridDim.x)
@@ -473,12 +513,12 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stag
     }
     float4 xlo[kCpl];
     float4 xhi[kCpl];
-    LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, 0.0f, lane, xlo, xhi);
+    LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, lane, xlo, xhi);
     float4 glo[kCpl];
     float4 ghi[kCpl];
-    if constexpr (!Stage::kElementwise)
+    if constexpr (Stage::kNorm)
     {
-        LoadActivationDirect<kWave, kCpl, false>(stage.w + 8 * begin, nullptr, 8 * span, 0.0f, lane, glo, ghi);
+        LoadActivationDirect<kWave, kCpl, false>(stage.w + 8 * begin, nullptr, 8 * span, lane, glo, ghi);
     }
     // Every unit at once; past the last unit (the grid's last workgroup only) a slot reloads it.
     half8 w[kUnits][kNr][kCpl];
@@ -495,25 +535,17 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stag
     // The activation quarter and the norm weights are requested before the weights: loads
     // complete in order, so the norm's sum and barrier run while the weights stream (7B QKV
     // 8.3 -> 8.0 us). The scheduling barrier keeps the compiler from moving the norm above the
-    // weight loads.
+    // weight loads. Here the row's factor is applied to x before the dot, in that shadow: taken
+    // to the row sums instead, its square root and division land after the weights (7B-shape
+    // QKV 7.77 -> 7.97 us).
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (!Stage::kElementwise)
+    if constexpr (Stage::kNorm)
     {
-        // rms_norm over the whole row: (scale * x) * w with scale = rsqrt(mean(x^2) + eps).
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < kCpl; ++i)
         {
-            float part = 0.0f;
-            part = fmaf(xlo[i].x, xlo[i].x, part);
-            part = fmaf(xlo[i].y, xlo[i].y, part);
-            part = fmaf(xlo[i].z, xlo[i].z, part);
-            part = fmaf(xlo[i].w, xlo[i].w, part);
-            part = fmaf(xhi[i].x, xhi[i].x, part);
-            part = fmaf(xhi[i].y, xhi[i].y, part);
-            part = fmaf(xhi[i].z, xhi[i].z, part);
-            part = fmaf(xhi[i].w, xhi[i].w, part);
-            ss += lane + i * kWave < span ? part : 0.0f;
+            ss += lane + i * kWave < span ? SquaresOf(xlo[i], xhi[i]) : 0.0f;
         }
         ss = GroupSum<kWave>(ss);
         if (lane == 0)
@@ -521,8 +553,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecColumns(uint32_t cols, Stag
             squares[waveId] = ss;
         }
         __syncthreads();
-        const float total = (squares[0] + squares[1]) + (squares[2] + squares[3]);
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(cols) + stage.eps);
+        const float scale = NormScale((squares[0] + squares[1]) + (squares[2] + squares[3]), cols, stage.eps);
 #pragma unroll
         for (int i = 0; i < kCpl; ++i)
         {
@@ -631,14 +662,15 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
     }
     float4 xlo[kCpl];
     float4 xhi[kCpl];
+    float scale = 1.0f;  // the rms_norm factor of a norm stage
     if constexpr (Stage::kElementwise)
     {
         // Each wave reads its own quarter of x straight into registers: one latency, no LDS.
-        LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, 0.0f, lane, xlo, xhi);
+        LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, lane, xlo, xhi);
     }
     else
     {
-        stage.template Run<kBlock, kStageVec>(xs, cols);
+        scale = stage.template Run<kBlock, kStageVec>(xs, cols);
         LoadActivation<kWave, kCpl>(xs + begin, xs + nchunks + begin, span, lane, xlo, xhi);
     }
     for (uint32_t k = 0; k < count; k += 2)
@@ -665,6 +697,10 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
     {
         const uint32_t k = threadIdx.x;
         float sums[1] = {(partial[k][0] + partial[k][1]) + (partial[k][2] + partial[k][3])};
+        if constexpr (Stage::kNorm)
+        {
+            sums[0] *= scale;
+        }
         epi.Finish(rowOf(k), sums, pre, bestValue, bestIndex);
     }
     epi.template Tail<kBlock>(bestValue, bestIndex);

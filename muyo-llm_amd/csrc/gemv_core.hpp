@@ -70,6 +70,34 @@ __device__ __forceinline__ float DotBatch(const half8 (&w)[kCpl], uint32_t base,
     return (a[0] + a[1]) + (a[2] + a[3]);
 }
 
+/// Sum of the squares of one chunk's 8 values, in element order.
+__device__ __forceinline__ float SquaresOf(const float4& lo, const float4& hi)
+{
+    float part = 0.0f;
+    part = fmaf(lo.x, lo.x, part);
+    part = fmaf(lo.y, lo.y, part);
+    part = fmaf(lo.z, lo.z, part);
+    part = fmaf(lo.w, lo.w, part);
+    part = fmaf(hi.x, hi.x, part);
+    part = fmaf(hi.y, hi.y, part);
+    part = fmaf(hi.z, hi.z, part);
+    part = fmaf(hi.w, hi.w, part);
+    return part;
+}
+
+__device__ __forceinline__ float4 MulF4(const float4& a, const float4& b)
+{
+    return float4{a.x * b.x, a.y * b.y, a.z * b.z, a.w * b.w};
+}
+
+/// The rms_norm factor of a row of n values whose squares sum to ss: rsqrt(mean(x^2) + eps), as
+/// shaders/llama/rms_norm.comp:100 computes it. The fused GEMVs with a staged or direct norm multiply their row
+/// sums by it after the dot: W . ((x * w) * scale) computed as (W . (x * w)) * scale.
+__device__ __forceinline__ float NormScale(float ss, uint32_t n, float eps)
+{
+    return 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
+}
+
 /// This lane's activation chunks (chunk lir + i*kLpr, clamped), read from LDS once and kept in
 /// registers: a lane meets the same columns in every row it processes.
 template <int kLpr, int kCpl>
@@ -86,22 +114,23 @@ __device__ __forceinline__ void LoadActivation(const float4* __restrict__ lo, co
     }
 }
 
-/// This lane's activation chunks (chunk lir + i*kLpr, clamped) read straight from global memory
-/// into registers, for rows that one kLpr-lane segment covers (kLpr * kCpl >= n/8): no LDS and
-/// no workgroup barrier. With kNorm the chunks are scaled in place by rsqrt(mean(x^2) + eps) * w
-/// in rms_norm.comp:122's order (scale * x) * w; the sum of squares is the segment's, which
-/// holds every element of the row once.
 struct NoOp
 {
     __device__ void operator()() const {}
 };
 
+/// This lane's activation chunks (chunk lir + i*kLpr, clamped) read straight from global memory
+/// into registers, for rows that one kLpr-lane segment covers (kLpr * kCpl >= n/8): no LDS and
+/// no workgroup barrier. With kNorm the chunks become x * w (the rms_norm weight) and the return
+/// value is this lane's part of sum(x^2): the caller reduces it over the segment together with
+/// its dot products and multiplies the row sums by rsqrt(mean(x^2) + eps) at the end, so the
+/// norm's reduction runs beside the dot instead of before it. Without kNorm it returns 0.
 /// `between` runs once the loads are issued and before the norm waits for them (work that
 /// overlaps their latency).
 template <int kLpr, int kCpl, bool kNorm, class Between = NoOp>
-__device__ __forceinline__ void LoadActivationDirect(const float* __restrict__ x, const float* __restrict__ w,
-                                                     uint32_t n, float eps, uint32_t lir, float4 (&xlo)[kCpl],
-                                                     float4 (&xhi)[kCpl], Between between = Between{})
+__device__ __forceinline__ float LoadActivationDirect(const float* __restrict__ x, const float* __restrict__ w,
+                                                      uint32_t n, uint32_t lir, float4 (&xlo)[kCpl],
+                                                      float4 (&xhi)[kCpl], Between between = Between{})
 {
     const uint32_t nchunks = n / 8;
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -121,38 +150,22 @@ __device__ __forceinline__ void LoadActivationDirect(const float* __restrict__ x
         }
     }
     between();
+    float ss = 0.0f;
     if constexpr (kNorm)
     {
-        float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < kCpl; ++i)
         {
-            float part = 0.0f;
-            part = fmaf(xlo[i].x, xlo[i].x, part);
-            part = fmaf(xlo[i].y, xlo[i].y, part);
-            part = fmaf(xlo[i].z, xlo[i].z, part);
-            part = fmaf(xlo[i].w, xlo[i].w, part);
-            part = fmaf(xhi[i].x, xhi[i].x, part);
-            part = fmaf(xhi[i].y, xhi[i].y, part);
-            part = fmaf(xhi[i].z, xhi[i].z, part);
-            part = fmaf(xhi[i].w, xhi[i].w, part);
-            ss += lir + i * kLpr < nchunks ? part : 0.0f;
+            ss += lir + i * kLpr < nchunks ? SquaresOf(xlo[i], xhi[i]) : 0.0f;
         }
-        ss = GroupSum<kLpr>(ss);
-        const float scale = 1.0f / sqrtf(ss / static_cast<float>(n) + eps);
 #pragma unroll
         for (int i = 0; i < kCpl; ++i)
         {
-            xlo[i].x = (scale * xlo[i].x) * glo[i].x;
-            xlo[i].y = (scale * xlo[i].y) * glo[i].y;
-            xlo[i].z = (scale * xlo[i].z) * glo[i].z;
-            xlo[i].w = (scale * xlo[i].w) * glo[i].w;
-            xhi[i].x = (scale * xhi[i].x) * ghi[i].x;
-            xhi[i].y = (scale * xhi[i].y) * ghi[i].y;
-            xhi[i].z = (scale * xhi[i].z) * ghi[i].z;
-            xhi[i].w = (scale * xhi[i].w) * ghi[i].w;
+            xlo[i] = MulF4(xlo[i], glo[i]);
+            xhi[i] = MulF4(xhi[i], ghi[i]);
         }
     }
+    return ss;
 }
 
 /// One loaded single-batch row against the activation in registers (chunks past the row add
@@ -212,16 +225,19 @@ __device__ __forceinline__ float RowDot(const uint16_t* __restrict__ row, uint32
 
 /// Stage an n-float activation (n % 8 == 0) into LDS in the split chunk layout with unrolled,
 /// independent float4 loads (kVec per thread per round), so staging costs one memory latency.
-/// With kNorm the values are scaled by rsqrt(mean(x^2) + eps) * w in the order (scale * x) * w
-/// of rms_norm.comp:122; that path holds x and w in registers and needs n/4 <= kVec * threads.
+/// With kNorm the staged values are x * w (the rms_norm weight) and the return value is the
+/// row's rms_norm factor NormScale(sum(x^2)), which the caller applies to its row sums after the
+/// dot; that path holds x and w in registers and needs n/4 <= kVec * threads. The sum of
+/// squares meets across the waves through the same barrier that publishes the staged row.
+/// Without kNorm it returns 1.
 /// With kNorm, x may also be `parts` (at most kMaxStageParts) consecutive vectors of n floats
 /// whose sum (added in order) is the activation; `sumOut`, when set, receives that sum. Ends
 /// with the block synchronised.
 constexpr uint32_t kMaxStageParts = 4;
 
 template <int kBlockThreads, int kVec, bool kNorm>
-__device__ __forceinline__ void StageSplit(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
-                                           float eps, float4* xs, uint32_t parts = 1, float* sumOut = nullptr)
+__device__ __forceinline__ float StageSplit(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
+                                            float eps, float4* xs, uint32_t parts = 1, float* sumOut = nullptr)
 {
     constexpr int kWaveCount = kBlockThreads / kWave;
     const uint32_t n4 = n / 4;
@@ -315,35 +331,40 @@ __device__ __forceinline__ void StageSplit(const float* __restrict__ x, const fl
                 ss = fmaf(v[k].w, v[k].w, ss);
             }
         }
-        ss = GroupSum<kWave>(ss);
-        if ((threadIdx.x & (kWave - 1)) == 0)
-        {
-            partial[threadIdx.x / kWave] = ss;
-        }
-        __syncthreads();
-        float total = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kWaveCount; ++k)
-        {
-            total += partial[k];
-        }
-        const float scale = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
+        // The products go to LDS while the sum of squares is reduced; one barrier publishes both.
 #pragma unroll
         for (int k = 0; k < kVec; ++k)
         {
             const uint32_t i = threadIdx.x + k * kBlockThreads;
             if (i < n4)
             {
-                float4 o;
-                o.x = (scale * v[k].x) * g[k].x;
-                o.y = (scale * v[k].y) * g[k].y;
-                o.z = (scale * v[k].z) * g[k].z;
-                o.w = (scale * v[k].w) * g[k].w;
-                xs[(i & 1u) ? nchunks + (i >> 1) : (i >> 1)] = o;
+                xs[(i & 1u) ? nchunks + (i >> 1) : (i >> 1)] = MulF4(v[k], g[k]);
             }
+        }
+        ss = GroupSum<kWave>(ss);
+        if constexpr (kWaveCount == 1)
+        {
+            __syncthreads();
+            return NormScale(ss, n, eps);
+        }
+        else
+        {
+            if ((threadIdx.x & (kWave - 1)) == 0)
+            {
+                partial[threadIdx.x / kWave] = ss;
+            }
+            __syncthreads();
+            float total = 0.0f;
+#pragma unroll
+            for (int k = 0; k < kWaveCount; ++k)
+            {
+                total += partial[k];
+            }
+            return NormScale(total, n, eps);
         }
     }
     __syncthreads();
+    return 1.0f;
 }
 
 /// (lanes per row, chunks per lane per batch) for a row of `nchunks` 16-byte chunks, with at
