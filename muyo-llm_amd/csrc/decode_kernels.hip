@@ -1639,23 +1639,104 @@ __global__ __launch_bounds__(128) void AttentionMergeKernel(DecodeScratch sc, fl
     }
 }
 
-/// o_proj split by kv group, with the attention merge in its prologue. Workgroup (b, g) owns
-/// group g's query heads, the W_o columns [g * gw, (g + 1) * gw) with gw = group * headDim
-/// (at most 1024), and rows b * 4 + w + k * 4 * gridDim.x (k < kRows) for its wave w. Every
-/// thread requests its merge operands, then its wave's row slices; the workgroup merges the
-/// group's chunk partials (AttentionMergeKernel's arithmetic, four channels per thread) into LDS
-/// while the weights are in flight (loads complete in order, so operands requested after the
-/// weights would wait for them: 8.8 -> 8.0 us at the 7B widths). The rows' dots go to
-/// parts[g][row], group 0 adding the residual; the next kernel's prologue sums the groups. A
-/// workgroup reads one group's partials instead of every head's, so the merge costs each
-/// workgroup gridChunks * gw floats.
-template <int kRows>
-__global__ __launch_bounds__(kBlock) void OProjGroupKernel(const uint16_t* __restrict__ wo, DecodeScratch sc,
-                                                           const float* __restrict__ residual,
-                                                           float* __restrict__ parts, uint32_t hidden,
-                                                           uint32_t qdim, uint32_t group, uint32_t headDim,
-                                                           uint32_t gridChunks)
+/// Sums eight values over the 64 lanes of a wave, leaving lane L the total of value L & 7 (a
+/// reduce-scatter: three halving exchanges inside each octet of lanes, then three full ones), in
+/// about a third of the lane permutes of eight separate sums.
+template <int kCtrl>
+__device__ __forceinline__ float DppMove(float x)
 {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), kCtrl, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float ScatterSum8(const float (&v)[8])
+{
+    const uint32_t lane = __lane_id();
+    // Partner L ^ 7 (row_half_mirror): lanes with bit 2 set keep values 4..7, the others 0..3.
+    const bool b2 = (lane & 4u) != 0;
+    float u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const float keep = b2 ? v[i + 4] : v[i];
+        const float send = b2 ? v[i] : v[i + 4];
+        u[i] = keep + DppMove<0x141>(send);
+    }
+    // Partner L ^ 2 (quad_perm [2,3,0,1]), split by bit 1.
+    const bool b1 = (lane & 2u) != 0;
+    float t[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+    {
+        const float keep = b1 ? u[i + 2] : u[i];
+        const float send = b1 ? u[i] : u[i + 2];
+        t[i] = keep + DppMove<0x4E>(send);
+    }
+    // Partner L ^ 1 (quad_perm [1,0,3,2]), split by bit 0: lane L now holds value L & 7 of its octet.
+    const bool b0 = (lane & 1u) != 0;
+    float r = (b0 ? t[1] : t[0]) + DppMove<0xB1>(b0 ? t[0] : t[1]);
+    // The octets: L ^ 8 (row_ror:8), L ^ 16 and L ^ 32 (row and half swaps).
+    r += DppMove<0x128>(r);
+    const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+    r = __uint_as_float(rows[0]) + __uint_as_float(rows[1]);
+    const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(r), __float_as_uint(r), false, false);
+    return __uint_as_float(halves[0]) + __uint_as_float(halves[1]);
+}
+
+constexpr int kOProjThreads = 512;
+constexpr uint32_t kOProjWaves = kOProjThreads / kWave;
+
+/// kCh consecutive floats, loaded and stored as one access.
+template <int kCh>
+struct Channels;
+template <>
+struct Channels<1>
+{
+    float v[1];
+    __device__ static Channels Load(const float* p) { return Channels{{*p}}; }
+    __device__ void Store(float* p) const { *p = v[0]; }
+};
+template <>
+struct Channels<2>
+{
+    float v[2];
+    __device__ static Channels Load(const float* p)
+    {
+        const float2 x = *reinterpret_cast<const float2*>(p);
+        return Channels{{x.x, x.y}};
+    }
+    __device__ void Store(float* p) const { *reinterpret_cast<float2*>(p) = float2{v[0], v[1]}; }
+};
+template <>
+struct Channels<4>
+{
+    float v[4];
+    __device__ static Channels Load(const float* p)
+    {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        return Channels{{x.x, x.y, x.z, x.w}};
+    }
+    __device__ void Store(float* p) const { *reinterpret_cast<float4*>(p) = float4{v[0], v[1], v[2], v[3]}; }
+};
+
+/// o_proj split by kv group, with the attention merge in its prologue. Workgroup (b, g) of 512
+/// threads owns group g's query heads, the W_o columns [g * gw, (g + 1) * gw) with gw = group *
+/// headDim (at most 1024), and rows b * 8 + w + k * 8 * gridDim.x (k < kRows <= 8) for its wave w.
+/// Wave h merges query head h (group <= 8, kCh = headDim / 64 channels per lane): lane c turns
+/// chunk c's (max, sum) into its weight 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c', and every lane
+/// adds its channels of the chunks' P.V rows with those weights, read from lane c, so the
+/// exponentials and the division run once per chunk rather than once per channel. The merge
+/// operands are requested before the weight rows (loads complete in order) and merged into LDS
+/// while the rows are in flight. The rows' dots, reduced by ScatterSum8, go to parts[g][row],
+/// group 0 adding the residual; the next kernel's prologue sums the groups. A workgroup reads one
+/// group's partials instead of every head's: gridChunks * gw floats.
+template <int kRows, int kCh>
+__global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t* __restrict__ wo, DecodeScratch sc,
+                                                                  const float* __restrict__ residual,
+                                                                  float* __restrict__ parts, uint32_t hidden,
+                                                                  uint32_t qdim, uint32_t group, uint32_t headDim,
+                                                                  uint32_t gridChunks)
+{
+    static_assert(kRows >= 1 && kRows <= 8, "ScatterSum8 reduces eight rows");
     constexpr int kCpl = 2;
     __shared__ float4 xs[2 * kWave * kCpl];
     const uint32_t g = blockIdx.y;
@@ -1663,88 +1744,72 @@ __global__ __launch_bounds__(kBlock) void OProjGroupKernel(const uint16_t* __res
     const uint32_t nchunks = gw / 8;
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = threadIdx.x / kWave;
-    const uint32_t stride = kWaves * gridDim.x;
-    const uint32_t first = blockIdx.x * kWaves + wave;
-    // Merge operands first: thread t owns channels 4t..4t+3 of the group (one head).
-    const uint32_t t = threadIdx.x;
-    const uint32_t tc = min(t, gw / 4 - 1);
-    const uint32_t hh = 4 * tc / headDim;
-    const uint32_t d = 4 * tc % headDim;
-    float m[kMaxAttnChunks];
-    float l[kMaxAttnChunks];
-    float4 a[kMaxAttnChunks];
+    const uint32_t stride = kOProjWaves * gridDim.x;
+    const uint32_t first = blockIdx.x * kOProjWaves + wave;
+    // Merge operands first. Waves past the group's heads repeat the last head's (unused) loads,
+    // which keeps the loads out of branches.
+    const uint32_t hh = min(wave, group - 1);
+    const uint64_t headBase = static_cast<uint64_t>(g) * gridChunks * group + hh;  // slot of chunk 0
+    const uint32_t lc = min(lane, gridChunks - 1);
+    float m = sc.attnMax[headBase + static_cast<uint64_t>(lc) * group];
+    const float l = sc.attnSum[headBase + static_cast<uint64_t>(lc) * group];
+    Channels<kCh> a[kMaxAttnChunks];
 #pragma unroll
     for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
     {
-        const uint32_t cc = min(c, gridChunks - 1);
-        const uint64_t slot = (static_cast<uint64_t>(g) * gridChunks + cc) * group + hh;
-        m[c] = c < gridChunks ? sc.attnMax[slot] : -INFINITY;
-        l[c] = sc.attnSum[slot];
-        a[c] = *reinterpret_cast<const float4*>(sc.attnAcc + slot * headDim + d);
+        const uint64_t slot = headBase + static_cast<uint64_t>(min(c, gridChunks - 1)) * group;
+        a[c] = Channels<kCh>::Load(sc.attnAcc + slot * headDim + lane * kCh);
     }
     half8 w[kRows][kCpl];
-    float res[kRows];
 #pragma unroll
     for (int k = 0; k < kRows; ++k)
     {
         const uint32_t row = min(first + k * stride, hidden - 1);
         LoadBatch<kWave, kCpl>(wo + static_cast<uint64_t>(row) * qdim + g * gw, 0, nchunks, lane, w[k]);
-        res[k] = g == 0 ? residual[row] : 0.0f;
     }
+    // Lane k < kRows stores row first + k * stride.
+    const uint32_t myRow = first + (lane & 7u) * stride;
+    const float res = g == 0 ? residual[min(myRow, hidden - 1)] : 0.0f;
     {
-        float top = -INFINITY;
+        m = lane < gridChunks ? m : -INFINITY;
+        const float top = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(GroupMax<16>(m))));
+        const float e = top == -INFINITY || m == -INFINITY ? 0.0f : exp2f(m - top);
+        const float den = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(GroupSum<16>(e * l))));
+        const float weight = den > 0.0f ? e / den : 0.0f;
+        Channels<kCh> out{};
 #pragma unroll
         for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
         {
-            top = fmaxf(top, m[c]);
-        }
-        float4 num = {0.0f, 0.0f, 0.0f, 0.0f};
-        float den = 0.0f;
-        if (top != -INFINITY)
-        {
+            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), c));
 #pragma unroll
-            for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+            for (int j = 0; j < kCh; ++j)
             {
-                const float e = exp2f(m[c] - top);
-                num.x = fmaf(e, a[c].x, num.x);
-                num.y = fmaf(e, a[c].y, num.y);
-                num.z = fmaf(e, a[c].z, num.z);
-                num.w = fmaf(e, a[c].w, num.w);
-                den = fmaf(e, l[c], den);
+                out.v[j] = fmaf(wc, a[c].v[j], out.v[j]);
             }
         }
-        float4 out = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (den > 0.0f)
+        if (wave < group)
         {
-            out = float4{num.x / den, num.y / den, num.z / den, num.w / den};
-        }
-        if (4 * t < gw)
-        {
-            xs[(t & 1u) ? nchunks + t / 2 : t / 2] = out;
+            // Channel ch of the group sits in chunk ch / 8: its low float4 for ch % 8 < 4.
+            const uint32_t ch = hh * headDim + lane * kCh;
+            const uint32_t pos = ch % 8;
+            const uint32_t at = pos < 4 ? 4 * (ch / 8) + pos : 4 * nchunks + 4 * (ch / 8) + pos - 4;
+            out.Store(reinterpret_cast<float*>(xs) + at);
         }
     }
     __syncthreads();
     float4 xlo[kCpl];
     float4 xhi[kCpl];
     LoadActivation<kWave, kCpl>(xs, xs + nchunks, nchunks, lane, xlo, xhi);
-    float sums[kRows];
+    float sums[8];
 #pragma unroll
-    for (int k = 0; k < kRows; ++k)
+    for (int k = 0; k < 8; ++k)
     {
-        sums[k] = DotRegisters<kWave, kCpl>(w[k], xlo, xhi, nchunks, lane);
+        sums[k] = k < kRows ? DotRegisters<kWave, kCpl>(w[k < kRows ? k : 0], xlo, xhi, nchunks, lane) : 0.0f;
     }
-    GroupSumN<kWave>(sums);
-    if (lane == 0)
+    const float total = ScatterSum8(sums);
+    if (lane < static_cast<uint32_t>(kRows) && myRow < hidden)
     {
-#pragma unroll
-        for (int k = 0; k < kRows; ++k)
-        {
-            const uint32_t row = first + k * stride;
-            if (row < hidden)
-            {
-                parts[static_cast<uint64_t>(g) * hidden + row] = res[k] + sums[k];
-            }
-        }
+        parts[static_cast<uint64_t>(g) * hidden + myRow] = res + total;
     }
 }
 
@@ -1913,19 +1978,38 @@ hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16
 bool OProjInGroups(const DecodeDims& dims)
 {
     const uint32_t gw = dims.heads / dims.kvHeads * dims.headDim;
-    return !MergeInOProj(dims) && gw <= 2 * kWave * 8 && gw % 8 == 0 && dims.headDim % 4 == 0 &&
-           dims.kvHeads <= kMaxStageParts;
+    // A wave merges one head (at most eight a workgroup) with 1, 2 or 4 channels per lane.
+    const uint32_t group = dims.heads / dims.kvHeads;
+    const uint32_t channels = dims.headDim / kWave;
+    return !MergeInOProj(dims) && gw <= 2 * kWave * 8 && group <= kOProjWaves && dims.headDim % kWave == 0 &&
+           (channels == 1 || channels == 2 || channels == 4) && dims.kvHeads <= kMaxStageParts;
 }
 
-template <int kRows>
+template <int kRows, int kCh>
 hipError_t LaunchOProjGroupsT(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
                               const float* residual, float* parts)
 {
-    const dim3 grid(CeilDiv(dims.hidden, kWaves * kRows), dims.kvHeads);
-    hipLaunchKernelGGL(OProjGroupKernel<kRows>, grid, dim3(kBlock), 0, s, wo, scratch, residual, parts, dims.hidden,
+    const dim3 grid(CeilDiv(dims.hidden, kOProjWaves * kRows), dims.kvHeads);
+    const auto kernel = &OProjGroupKernel<kRows, kCh>;
+    hipLaunchKernelGGL(kernel, grid, dim3(kOProjThreads), 0, s, wo, scratch, residual, parts, dims.hidden,
                        dims.heads * dims.headDim, dims.heads / dims.kvHeads, dims.headDim,
                        AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks));
     return hipGetLastError();
+}
+
+template <int kRows>
+hipError_t LaunchOProjGroupsRows(hipStream_t s, const DecodeDims& dims, const uint16_t* wo,
+                                 const DecodeScratch& scratch, const float* residual, float* parts)
+{
+    switch (dims.headDim / kWave)
+    {
+        case 1:
+            return LaunchOProjGroupsT<kRows, 1>(s, dims, wo, scratch, residual, parts);
+        case 2:
+            return LaunchOProjGroupsT<kRows, 2>(s, dims, wo, scratch, residual, parts);
+        default:
+            return LaunchOProjGroupsT<kRows, 4>(s, dims, wo, scratch, residual, parts);
+    }
 }
 
 hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
@@ -1935,26 +2019,27 @@ hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16
     {
         return hipErrorInvalidValue;
     }
-    // About two workgroups per CU: the rows of each group spread over 2 * CUs / groups workgroups.
-    const uint32_t waves = std::max(1u, 2 * CuCount() * kWaves / dims.kvHeads);
+    // About one workgroup (eight waves) per CU: the rows of each group spread over CUs / groups
+    // workgroups.
+    const uint32_t waves = std::max(1u, CuCount() * kOProjWaves / dims.kvHeads);
     const uint32_t perWave = CeilDiv(dims.hidden, waves);
     if (perWave <= 1)
     {
-        return LaunchOProjGroupsT<1>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<1>(s, dims, wo, scratch, residual, parts);
     }
     if (perWave <= 2)
     {
-        return LaunchOProjGroupsT<2>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<2>(s, dims, wo, scratch, residual, parts);
     }
     if (perWave <= 4)
     {
-        return LaunchOProjGroupsT<4>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<4>(s, dims, wo, scratch, residual, parts);
     }
     if (perWave <= 7)
     {
-        return LaunchOProjGroupsT<7>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<7>(s, dims, wo, scratch, residual, parts);
     }
-    return LaunchOProjGroupsT<8>(s, dims, wo, scratch, residual, parts);
+    return LaunchOProjGroupsRows<8>(s, dims, wo, scratch, residual, parts);
 }
 
 hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const float* parts, const float* normW,
