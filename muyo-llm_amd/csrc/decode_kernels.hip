@@ -1426,6 +1426,7 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     constexpr int kSlices = kBlock / kRC;  // keys of a block, side by side
     constexpr int kR = static_cast<int>(kAttnBlocksPerRound);
     static_assert(kSlices == 2048 / kHd, "slice count must match AttnSlices");
+    static_assert(kHd <= kBlock, "one thread per channel in the final sums");
     __shared__ float waveMax[kWaves];
     __shared__ float waveSum[kWaves];
     __shared__ float combine[kWaves][kHd];
@@ -1489,23 +1490,30 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         // blocks interleave instead of each waiting on its own previous step.
         float s[kR];
         bool valid[kR];
+        bool any = false;
 #pragma unroll
         for (int k = 0; k < kR; ++k)
         {
-            valid[k] = b0 + k < mine && keyOf(b0 + k) < keys;
+            // Blocks past this chunk's hold keys past the last (block * chunks + chunk >= blocks).
+            valid[k] = keyOf(b0 + k) < keys;
+            any = any || valid[k];
             s[k] = DotChunk(kk[k], q0, q1, 0.0f);
         }
         GroupSumN<kRC>(s);
+        if (!any)
+        {
+            return;  // no valid key for this slice in this round
+        }
         float top = m;
 #pragma unroll
         for (int k = 0; k < kR; ++k)
         {
             s[k] = valid[k] ? s[k] * sl : -INFINITY;
             top = fmaxf(top, s[k]);
-        }
-        if (top == -INFINITY)
-        {
-            return;  // no valid key for this slice in this round
+            if (!valid[k])
+            {
+                vv[k] = half8{};  // 0 * NaN would be NaN
+            }
         }
         const float factor = exp2f(m - top);  // 0 while m is still -inf
         m = top;
@@ -1516,10 +1524,6 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         {
             p[k] = valid[k] ? exp2f(s[k] - top) : 0.0f;
             psum += p[k];
-            if (!valid[k])
-            {
-                vv[k] = half8{};  // 0 * NaN would be NaN
-            }
         }
         l = fmaf(l, factor, psum);
 #pragma unroll
@@ -1583,8 +1587,10 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         }
     }
     __syncthreads();
-    for (uint32_t d = threadIdx.x; d < kHd; d += kBlock)
+    // Thread d < kHd sums channel d; thread 0 also the chunk's max and sum.
+    if (threadIdx.x < kHd)
     {
+        const uint32_t d = threadIdx.x;
         float sum = combine[0][d];
 #pragma unroll
         for (int w = 1; w < kWaves; ++w)
@@ -1592,17 +1598,17 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
             sum += combine[w][d];
         }
         sc.attnAcc[slot * kHd + d] = sum;
-    }
-    if (threadIdx.x == 0)
-    {
-        float sum = waveSum[0];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w)
+        if (d == 0)
         {
-            sum += waveSum[w];
+            float total = waveSum[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w)
+            {
+                total += waveSum[w];
+            }
+            sc.attnMax[slot] = top;
+            sc.attnSum[slot] = total;
         }
-        sc.attnMax[slot] = top;
-        sc.attnSum[slot] = sum;
     }
 }
 
