@@ -164,16 +164,16 @@ __device__ __forceinline__ void GroupSumN(float (&v)[N])
 #undef MUYO_GROUP_SUM_LEVEL
 }
 
-/// Sums eight values over the 64 lanes of a wave, leaving lane L the total of value L & 7 (a
-/// reduce-scatter: three halving exchanges inside each octet of lanes, then three full ones), in
-/// about a third of the lane permutes of eight separate sums.
 template <int kCtrl>
 __device__ __forceinline__ float DppMove(float x)
 {
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(x), __float_as_int(x), kCtrl, 0xF, 0xF, false));
 }
 
-__device__ __forceinline__ float ScatterSum8(const float (&v)[8])
+/// Sums eight values over each octet of lanes (lanes 8o .. 8o + 7), leaving lane L the octet's
+/// total of value L & 7: a reduce-scatter of three halving exchanges, 7 lane permutes where eight
+/// separate octet sums take 24.
+__device__ __forceinline__ float OctetScatter8(const float (&v)[8])
 {
     const uint32_t lane = __lane_id();
     // Partner L ^ 7 (row_half_mirror): lanes with bit 2 set keep values 4..7, the others 0..3.
@@ -196,11 +196,18 @@ __device__ __forceinline__ float ScatterSum8(const float (&v)[8])
         const float send = b1 ? u[i] : u[i + 2];
         t[i] = keep + DppMove<0x4E>(send);
     }
-    // Partner L ^ 1 (quad_perm [1,0,3,2]), split by bit 0: lane L now holds value L & 7 of its octet.
+    // Partner L ^ 1 (quad_perm [1,0,3,2]), split by bit 0.
     const bool b0 = (lane & 1u) != 0;
-    float r = (b0 ? t[1] : t[0]) + DppMove<0xB1>(b0 ? t[0] : t[1]);
-    // The octets: L ^ 8 (row_ror:8), L ^ 16 and L ^ 32 (row and half swaps).
-    r += DppMove<0x128>(r);
+    return (b0 ? t[1] : t[0]) + DppMove<0xB1>(b0 ? t[0] : t[1]);
+}
+
+/// Sums eight values over the 64 lanes of a wave, leaving lane L the total of value L & 7: the
+/// octet reduce-scatter, then three full exchanges (L ^ 8, L ^ 16, L ^ 32). About a third of the
+/// lane permutes of eight separate sums.
+__device__ __forceinline__ float ScatterSum8(const float (&v)[8])
+{
+    float r = OctetScatter8(v);
+    r += DppMove<0x128>(r);  // row_ror:8
     const auto rows = __builtin_amdgcn_permlane16_swap(__float_as_uint(r), __float_as_uint(r), false, false);
     r = __uint_as_float(rows[0]) + __uint_as_float(rows[1]);
     const auto halves = __builtin_amdgcn_permlane32_swap(__float_as_uint(r), __float_as_uint(r), false, false);

@@ -1392,6 +1392,26 @@ __global__ __launch_bounds__(kBlock) void FinalizeKernel(DecodeState* state, con
 // neutral partial (-inf, 0, 0), so the merge needs no position either.
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+template <int kLane>
+__device__ __forceinline__ float FromOctetLane(float v)
+{
+    // ds_swizzle bit mode: source lane (L & 0x18) | kLane within each 32 lanes.
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x18 | (kLane << 5)));
+}
+
+/// out[k] = v of lane k of this lane's octet, for k < 8.
+__device__ __forceinline__ void OctetBroadcast8(float v, float (&out)[8])
+{
+    out[0] = FromOctetLane<0>(v);
+    out[1] = FromOctetLane<1>(v);
+    out[2] = FromOctetLane<2>(v);
+    out[3] = FromOctetLane<3>(v);
+    out[4] = FromOctetLane<4>(v);
+    out[5] = FromOctetLane<5>(v);
+    out[6] = FromOctetLane<6>(v);
+    out[7] = FromOctetLane<7>(v);
+}
 // kAttnBlocksPerRound (decode_kernels.hpp) key blocks per lane per round: 2048 keys of a 2048-row
 // cache in one round with the long grids.
 
@@ -1485,31 +1505,35 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     // Online softmax over one round of blocks b0 .. b0 + kR - 1. Keys past the position and
     // blocks past this chunk's are masked; their rows may hold anything, so their V is zeroed as
     // well as weighted by 0.
+    static_assert(kR == 8, "the scores' reduce-scatter gives each lane of an octet one of eight blocks");
     auto consume = [&](uint32_t b0) {
-        // Dot products first, then their lane sums level by level, so the permutes of the
-        // blocks interleave instead of each waiting on its own previous step.
         float s[kR];
         bool valid[kR];
-        bool any = false;
 #pragma unroll
         for (int k = 0; k < kR; ++k)
         {
             // Blocks past this chunk's hold keys past the last (block * chunks + chunk >= blocks).
             valid[k] = keyOf(b0 + k) < keys;
-            any = any || valid[k];
             s[k] = DotChunk(kk[k], q0, q1, 0.0f);
         }
-        GroupSumN<kRC>(s);
-        if (!any)
+        // Reduce-scatter the slice's partial dot products: lane L ends with the score of block
+        // L % 8 (both octets of a 16-lane slice hold all eight), so the max, the exponential
+        // and the sum run once per block instead of once per lane and block.
+        float sj = OctetScatter8(s);
+        if constexpr (kRC == 16)
         {
-            return;  // no valid key for this slice in this round
+            sj += DppMove<0x128>(sj);  // the slice's other octet (row_ror:8)
         }
-        float top = m;
+        const uint32_t j = threadIdx.x & 7u;
+        sj = keyOf(b0 + j) < keys ? sj * sl : -INFINITY;
+        const float top = fmaxf(m, GroupMax<8>(sj));
+        if (top == -INFINITY)
+        {
+            return;  // no valid key for this slice yet
+        }
 #pragma unroll
         for (int k = 0; k < kR; ++k)
         {
-            s[k] = valid[k] ? s[k] * sl : -INFINITY;
-            top = fmaxf(top, s[k]);
             if (!valid[k])
             {
                 vv[k] = half8{};  // 0 * NaN would be NaN
@@ -1517,15 +1541,11 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
         }
         const float factor = exp2f(m - top);  // 0 while m is still -inf
         m = top;
+        const float pj = exp2f(sj - top);  // masked keys: exp2(-inf) = 0
+        l = fmaf(l, factor, GroupSum<8>(pj));
+        // Every lane takes block k's weight from lane k of its octet.
         float p[kR];
-        float psum = 0.0f;
-#pragma unroll
-        for (int k = 0; k < kR; ++k)
-        {
-            p[k] = valid[k] ? exp2f(s[k] - top) : 0.0f;
-            psum += p[k];
-        }
-        l = fmaf(l, factor, psum);
+        OctetBroadcast8(pj, p);
 #pragma unroll
         for (int c = 0; c < 8; ++c)
         {
