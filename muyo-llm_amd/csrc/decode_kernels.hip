@@ -158,6 +158,24 @@ struct DirectStage : Base
     static constexpr bool kDirect = true;
 };
 
+/// out[k] = v of lane k of this lane's group of lanes, for k < kCount: ds_swizzle bit mode
+/// within each 32 lanes, source (L & kAnd) | k (kAnd 0x10: 16-lane groups, 0: 32-lane groups).
+template <int kAnd, int kK>
+__device__ __forceinline__ float FromGroupLane(float v)
+{
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), kAnd | (kK << 5)));
+}
+
+template <int kAnd, uint32_t kCount, int kK = 0>
+__device__ __forceinline__ void HeadLaneBroadcast(float v, float (&out)[kCount])
+{
+    if constexpr (kK < static_cast<int>(kCount))
+    {
+        out[kK] = FromGroupLane<kAnd, kK>(v);
+        HeadLaneBroadcast<kAnd, kCount, kK + 1>(v, out);
+    }
+}
+
 /// The attention output, merged from the chunk partials: out[h][d] = sum_c 2^(m_c - M) acc_c /
 /// sum_c 2^(m_c - M) l_c (flash-decoding's combine, maxima in log2 units). Every slot of the
 /// grid (at most kChunks) takes part; chunks without keys hold the neutral partial, so no
@@ -179,53 +197,51 @@ struct MergeStage
         return (static_cast<uint64_t>(h / group) * gridChunks + min(c, gridChunks - 1)) * group + h % group;
     }
 
-    /// Thread t owns channels 4t..4t+3 of the q dim (one head) and merges them on its own: every
-    /// (max, sum, P.V) slot of that head is requested at once (float4 P.V loads), the weights
-    /// 2^(m_c - M) are worked out per thread, and one barrier publishes the merged row.
+    /// Thread t owns channels 4t..4t+3 of the q dim, so a head is headDim / 4 consecutive lanes
+    /// (16 or 32). Lane c < kChunks of a head's lanes turns chunk c's (max, sum) into its weight
+    /// 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c' and every lane adds its channels of the chunks' P.V
+    /// rows with those weights, read from lane c by ds_swizzle: the exponentials and the division
+    /// run once per chunk, not once per channel. One barrier publishes the merged row.
     template <int kThreads, int kVec>
     __device__ float Run(float4* xs, uint32_t n) const
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
+        static_assert(kChunks <= 16, "a head's first 16 lanes weigh the chunks");
         const uint32_t nchunks = n / 8;
         const uint32_t t = min(threadIdx.x, n / 4 - 1);
         const uint32_t h = 4 * t / headDim;
         const uint32_t d = 4 * t % headDim;
-        float m[kChunks];
-        float l[kChunks];
+        const uint32_t c = t % (headDim / 4);  // this lane's chunk, when below gridChunks
         float4 a[kChunks];
 #pragma unroll
-        for (uint32_t c = 0; c < kChunks; ++c)
+        for (uint32_t k = 0; k < kChunks; ++k)
         {
-            const uint64_t slot = Slot(h, c);
-            m[c] = c < gridChunks ? attnMax[slot] : -INFINITY;
-            l[c] = attnSum[slot];
-            a[c] = *reinterpret_cast<const float4*>(attnAcc + slot * headDim + d);
+            a[k] = *reinterpret_cast<const float4*>(attnAcc + Slot(h, k) * headDim + d);
         }
-        float top = -INFINITY;
-#pragma unroll
-        for (uint32_t c = 0; c < kChunks; ++c)
+        const float mc = c < gridChunks && c < kChunks ? attnMax[Slot(h, c)] : -INFINITY;
+        const float lc = attnSum[Slot(h, min(c, kChunks - 1))];
+        // Lanes 0..15 of each head hold its chunks (the rest -inf), so 16-lane groups suffice.
+        const float top = GroupMax<16>(mc);
+        const float e = top == -INFINITY || mc == -INFINITY ? 0.0f : exp2f(mc - top);
+        const float den = GroupSum<16>(e * lc);
+        const float weight = den > 0.0f ? e / den : 0.0f;
+        float wk[kChunks];
+        if (headDim == 64)
         {
-            top = fmaxf(top, m[c]);
+            HeadLaneBroadcast<0x10, kChunks>(weight, wk);
         }
-        float4 num = {0.0f, 0.0f, 0.0f, 0.0f};
-        float den = 0.0f;
-        if (top != -INFINITY)
+        else
         {
-#pragma unroll
-            for (uint32_t c = 0; c < kChunks; ++c)
-            {
-                const float e = exp2f(m[c] - top);  // 0 for neutral and absent slots
-                num.x = fmaf(e, a[c].x, num.x);
-                num.y = fmaf(e, a[c].y, num.y);
-                num.z = fmaf(e, a[c].z, num.z);
-                num.w = fmaf(e, a[c].w, num.w);
-                den = fmaf(e, l[c], den);
-            }
+            HeadLaneBroadcast<0x00, kChunks>(weight, wk);
         }
         float4 out = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (den > 0.0f)
+#pragma unroll
+        for (uint32_t k = 0; k < kChunks; ++k)
         {
-            out = float4{num.x / den, num.y / den, num.z / den, num.w / den};
+            out.x = fmaf(wk[k], a[k].x, out.x);
+            out.y = fmaf(wk[k], a[k].y, out.y);
+            out.z = fmaf(wk[k], a[k].z, out.z);
+            out.w = fmaf(wk[k], a[k].w, out.w);
         }
         if (4 * threadIdx.x < n)
         {
