@@ -81,8 +81,10 @@ __device__ __forceinline__ uint16_t FloatToHalfBits(float value)
 /// The value held by a lane of the other half of this lane's group of 2*kStep consecutive lanes.
 /// Meant for butterfly reductions in which, before step kStep, every lane of each kStep-lane
 /// half already holds the same value: the partner lane then need not be lane ^ kStep, so the
-/// steps inside a 16-lane row use DPP (quad permutes, then the half-row and row mirrors), the
-/// step across rows a swizzle, and the step across the wave's halves two lane reads.
+/// steps inside a 16-lane row use DPP (quad permutes, then the half-row and row mirrors). The
+/// steps across rows and across the wave's halves are lane ^ 16 and lane ^ 32 exchanges
+/// (v_permlane16_swap, v_permlane32_swap): VALU operations, where an LDS swizzle or two lane
+/// reads would wait on the LDS pipe or a scalar register.
 template <int kStep>
 __device__ __forceinline__ int PartnerLane(int value)
 {
@@ -105,13 +107,17 @@ __device__ __forceinline__ int PartnerLane(int value)
     }
     else if constexpr (kStep == 16)
     {
-        return __builtin_amdgcn_ds_swizzle(value, 0x401F);  // bit mode: lane ^ 16 within 32 lanes
+        // Rows 2r and 2r + 1 exchange: the pair holds (even row's, odd row's) value per lane.
+        const auto rows = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(value), static_cast<unsigned>(value),
+                                                           false, false);
+        return static_cast<int>((__lane_id() & 16u) != 0 ? rows[0] : rows[1]);
     }
     else
     {
-        const int low = __builtin_amdgcn_readlane(value, 0);
-        const int high = __builtin_amdgcn_readlane(value, 32);
-        return (__lane_id() < 32) ? high : low;
+        // The wave's halves exchange: the pair holds (low half's, high half's) value per lane.
+        const auto halves = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(value),
+                                                             static_cast<unsigned>(value), false, false);
+        return static_cast<int>((__lane_id() & 32u) != 0 ? halves[0] : halves[1]);
     }
 }
 
