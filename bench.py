@@ -113,6 +113,15 @@ def enqueue_step(dec, shape, stream) -> None:
     dec.enqueue_kernel("LM_HEAD", 0, stream)
 
 
+def settle(torch) -> None:
+    """Waits until the device is idle and then a little longer. Freeing a large device buffer (an
+    earlier decoder's arena, torch's cache) starts work in the driver that keeps HBM busy for a
+    while afterwards: a 7B-shape step measured 2.563 ms before such a free, 2.628 ms within
+    0.25 s after freeing 15 GB and 2.563 ms again from 0.5 s on. Timed regions start after it."""
+    torch.cuda.synchronize()
+    time.sleep(0.75)
+
+
 def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
     """Returns (ms per step, positions timed, decoder launches per step, generated ids, median ms
     per step over 16 runs of the same positions). `sampler`: keyword
@@ -132,7 +141,7 @@ def time_decode(mh, torch, shape, position, steps, warmup, seed, sampler=None):
         warm_ids = dec.generated_ids(warmup)
         first = start + warmup
         begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
+        settle(torch)
         begin.record(stream)
         dec.generate_async(warm_ids[-1], first, steps, stream.cuda_stream)
         end.record(stream)
@@ -173,14 +182,12 @@ def prefill_flops(c: dict, prompt: int) -> int:
 def time_prefill(mh, torch, shape, prompt, reps, seed):
     """Milliseconds per muyo_decoder_prefill of `prompt` tokens at row 0 (a synchronous call:
     host clock around it, token upload and next-token readback included)."""
-    import time
-
     tokens = [(7919 * i + 13) % shape["vocab"] for i in range(prompt)]
     dec = mh.Decoder(mh.qwen2_config(**shape))
     try:
         dec.fill_random(seed)
         first = dec.prefill(tokens, 0)
-        torch.cuda.synchronize()
+        settle(torch)
         begin = time.perf_counter()
         for _ in range(reps):
             again = dec.prefill(tokens, 0)
@@ -198,7 +205,7 @@ def library_gemm(torch, m, n, k, reps=10):
     w = torch.randn(n, k, device="cuda", dtype=torch.float16)
     for _ in range(2):
         torch.matmul(x, w.t())
-    torch.cuda.synchronize()
+    settle(torch)
     b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     b.record()
     for _ in range(reps):
@@ -240,7 +247,7 @@ def time_kernels(mh, torch, shape, seed, rounds):
         for _ in range(3):
             dec.enqueue_kernel("LM_HEAD", 0, s)
         b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
+        settle(torch)
         b.record(stream)
         for _ in range(rounds):
             dec.enqueue_kernel("LM_HEAD", 0, s)
@@ -274,6 +281,7 @@ def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
         dec.fill_random(seed)
         dec.fill_kv_random(position, seed + 1)
         dec.set_state(9707, position, stream.cuda_stream)
+        settle(torch)
         for kind in STEP_KINDS:
             for layer in range(shape["layers"]):
                 dec.enqueue_kernel(kind, layer, stream.cuda_stream)
@@ -299,7 +307,7 @@ def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
     return out
 
 
-def floor_chain(byte_list, reps=20) -> dict:
+def floor_chain(torch, byte_list, reps=20) -> dict:
     """The streaming floor of a launch sequence (libmuyo_floor.so's muyo_floor_chain): each
     launch only reads its algorithmic bytes from its own buffer region, chained in one hipGraph;
     milliseconds per chain with 2, 3 and 4 workgroups of 512 threads per CU, and the best."""
@@ -312,6 +320,7 @@ def floor_chain(byte_list, reps=20) -> dict:
     arr = (ctypes.c_uint64 * len(byte_list))(*byte_list)
     out = {}
     for per_cu in (2, 3, 4):
+        settle(torch)  # the previous chain's (or decoder's) freed buffer
         ms = ctypes.c_double(0.0)
         rc = lib.muyo_floor_chain(arr, len(byte_list), per_cu, reps, ctypes.byref(ms))
         if rc != 0:
@@ -337,13 +346,13 @@ def floor_report(mh, torch, which: str) -> dict:
     chain_bytes = [kernel_bytes(shape, "embed", position)] + per_layer * shape["layers"] + \
         [kernel_bytes(shape, "lm_head", position)]
     assert len(chain_bytes) == launches, (len(chain_bytes), launches)
-    chain = floor_chain(chain_bytes)
+    chain = floor_chain(torch, chain_bytes)
     total = sum(chain_bytes)
     step_bytes_mid = step_bytes(shape, position)
     kernels = time_phases(mh, torch, shape, position, seed)
     phases = {}
     for kind, nbytes in zip(STEP_KINDS, per_layer):
-        stream_ms = floor_chain([nbytes] * shape["layers"])["best_ms"]
+        stream_ms = floor_chain(torch, [nbytes] * shape["layers"])["best_ms"]
         stream_us = 1000.0 * stream_ms / shape["layers"]
         phases[kind.lower()] = {"bytes": nbytes, "stream_us": round(stream_us, 2),
                                 "kernel_us": round(kernels[kind.lower()], 2),
