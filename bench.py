@@ -368,6 +368,35 @@ def floor_report(mh, torch, which: str) -> dict:
     }
 
 
+def launch_floor_report(mh, which: str) -> dict:
+    """What a kernel boundary costs (muyo-llm_amd/launch_floor, a child process): empty kernels
+    replayed from hipGraphs of 122 and 1952 kernels; empty kernels dispatched from an AQL queue with
+    system, agent or no fence scopes; and the decode step's launch sequence (`which`: 05b at cache
+    row 1024, 7b at row 2040, each launch's algorithmic bytes as in `floor_report`) read by
+    pure-stream kernels with agent or no fences, and with an 896-float activation handed from launch
+    to launch in five coherence schemes (times in microseconds per chain)."""
+    import subprocess
+
+    shape = dict(mh.QWEN25_05B if which == "05b" else mh.QWEN25_7B)
+    position = 1024 if which == "05b" else 2040
+    per_layer = [kernel_bytes(shape, kind.lower(), position) for kind in STEP_KINDS]
+    chain = [kernel_bytes(shape, "embed", position)] + per_layer * shape["layers"] + \
+        [kernel_bytes(shape, "lm_head", position)]
+    tool = ROOT / "muyo-llm_amd" / "launch_floor"
+    code = ROOT / "muyo-llm_amd" / "launch_floor_kernels.co"
+    run = subprocess.run([str(tool), str(code)], input="\n".join(str(b) for b in chain), capture_output=True,
+                         text=True, timeout=300)
+    if run.returncode != 0:
+        raise RuntimeError(f"launch_floor failed ({run.returncode}): {run.stderr.strip()}")
+    out = json.loads(run.stdout)
+    stream = out["aql_stream_us"]
+    agent = min(stream["agent"], stream["agent_again"])
+    none = min(stream["none"], stream["none_again"])
+    return {"shape": which, "position": position, "launches": len(chain), "chain_bytes": sum(chain), **out,
+            "fences_us_per_chain": round(agent - none, 1),
+            "fences_us_per_launch": round((agent - none) / len(chain), 3)}
+
+
 def time_ops(mh, torch, reps: int = 10) -> dict:
     """Per-launch time of each per-op launcher at the batched shapes of the element-wise and
     reduction set (4096 rows at Qwen2.5-0.5B widths) and of the decode GEMV suite, through the C
@@ -845,6 +874,10 @@ def main() -> int:
     ap.add_argument("--floor", choices=["05b", "7b"],
                     help="only the step beside its streaming floor (a chain of pure-read kernels with the step's "
                          "launch count and bytes) and the per-phase kernels beside pure streams of their bytes")
+    ap.add_argument("--launch-floor", choices=["05b", "7b"],
+                    help="only the kernel-boundary measurements (muyo-llm_amd/launch_floor): hipGraph and raw AQL "
+                         "chains of empty kernels by fence scope, and the step's launch sequence as pure streams and "
+                         "with activation hand-offs under each fence and coherence scheme")
     ap.add_argument("--kernel-only", choices=["lm_head", "copy", "step_05b", "step_7b"],
                     help="only launch one kernel back to back, or whole decode steps kernel by kernel "
                          "(0.5B shape from cache row 1024, 7B shape from row 2040), for rocprofv3")
@@ -874,9 +907,13 @@ def main() -> int:
               "path is single-GPU by design and multi-GPU figures are not produced.", file=sys.stderr)
         return 2
 
-    import torch
-
     import muyo_hip as mh
+
+    if args.launch_floor:
+        print(json.dumps(launch_floor_report(mh, args.launch_floor)), flush=True)
+        return 0
+
+    import torch
 
     torch.cuda.set_device(0)
     mh.load()
