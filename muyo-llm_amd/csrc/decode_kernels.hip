@@ -98,10 +98,10 @@ struct PlainStage
     {
         return LoadActivationDirect<kLpr, kCpl, false>(x, nullptr, n, lir, xlo, xhi, between);
     }
-    template <int kThreads, int kVec>
-    __device__ float Run(float4* xs, uint32_t n) const
+    template <int kThreads, int kVec, class Between = NoOp>
+    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
-        return StageSplit<kThreads, kVec, false>(x, nullptr, n, 0.0f, xs);
+        return StageSplit<kThreads, kVec, false>(x, nullptr, n, 0.0f, xs, 1, nullptr, between);
     }
 };
 
@@ -119,10 +119,10 @@ struct NormStage
     {
         return LoadActivationDirect<kLpr, kCpl, true>(x, w, n, lir, xlo, xhi, between);
     }
-    template <int kThreads, int kVec>
-    __device__ float Run(float4* xs, uint32_t n) const
+    template <int kThreads, int kVec, class Between = NoOp>
+    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
-        return StageSplit<kThreads, kVec, true>(x, w, n, eps, xs);
+        return StageSplit<kThreads, kVec, true>(x, w, n, eps, xs, 1, nullptr, between);
     }
 };
 
@@ -140,10 +140,11 @@ struct PartsNormStage
     static constexpr bool kCanDirect = false;  // the sum is stored once, through the staging path
     static constexpr bool kDirect = false;
     static constexpr bool kNorm = true;
-    template <int kThreads, int kVec>
-    __device__ float Run(float4* xs, uint32_t n) const
+    template <int kThreads, int kVec, class Between = NoOp>
+    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
-        return StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr);
+        return StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr,
+                                                between);
     }
 };
 
@@ -202,10 +203,14 @@ struct MergeStage
     /// 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c' and every lane adds its channels of the chunks' P.V
     /// rows with those weights, read from lane c by ds_swizzle: the exponentials and the division
     /// run once per chunk, not once per channel. One barrier publishes the merged row.
-    template <int kThreads, int kVec>
-    __device__ float Run(float4* xs, uint32_t n) const
+    /// `between` (a kernel's weight loads) runs first: at these widths the weights are two
+    /// chunks a lane and arrive ahead of the partials anyway (requested after the partials,
+    /// o_proj took 4.6 us instead of 4.0).
+    template <int kThreads, int kVec, class Between = NoOp>
+    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
+        between();
         static_assert(kChunks <= 16, "a head's first 16 lanes weigh the chunks");
         const uint32_t nchunks = n / 8;
         const uint32_t t = min(threadIdx.x, n / 4 - 1);
@@ -301,7 +306,7 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
 
     if constexpr (kSingle)
     {
-        // Weights do not depend on the activation: start streaming them before it is staged.
+        // Weights do not depend on the activation: they stream while it is staged.
         half8 w[kNr][kCpl];
         typename Epi::Pre pre{};
         auto load = [&](uint32_t unit) {
@@ -311,11 +316,13 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
                 LoadBatch<kLpr, kCpl>(epi.Row(unit, r), 0, nchunks, lir, w[r]);
             }
         };
-        if (first + unitInWave < units)
-        {
-            pre = epi.Prefetch(first + unitInWave);
-            load(first + unitInWave);
-        }
+        // Branch-free (a wave without a unit loads the last unit's rows and drops them), so the
+        // waits for loads issued before these can count them.
+        auto loadFirst = [&] {
+            const uint32_t unit = min(first + unitInWave, units - 1);
+            pre = epi.Prefetch(unit);
+            load(unit);
+        };
         float4 xlo[kCpl];
         float4 xhi[kCpl];
         // A directly staged norm leaves each lane its part of sum(x^2), reduced over the segment
@@ -326,12 +333,18 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
         // The epilogue's own work (Ready) runs while the weights and the activation are in flight.
         if constexpr (Stage::kDirect)
         {
+            loadFirst();
             squares = stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] { epi.Ready(pre); });
         }
         else
         {
-            epi.Ready(pre);
-            scale = stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols);
+            // The staging policy issues the activation's loads first and the weights' right after
+            // (Run's `between`), so the activation, which loads complete in order, is staged while
+            // the weights stream.
+            scale = stage.template Run<kThreads, StageVecFor<kLpr, kCpl, kThreads>()>(xs, cols, [&] {
+                loadFirst();
+                epi.Ready(pre);
+            });
             LoadActivation<kLpr, kCpl>(xs, xs + nchunks, nchunks, lir, xlo, xhi);
         }
         for (; first < units; first += stride)

@@ -233,11 +233,16 @@ __device__ __forceinline__ float RowDot(const uint16_t* __restrict__ row, uint32
 /// With kNorm, x may also be `parts` (at most kMaxStageParts) consecutive vectors of n floats
 /// whose sum (added in order) is the activation; `sumOut`, when set, receives that sum. Ends
 /// with the block synchronised.
+/// `between` runs once the staging loads are issued and before any of them is used (with kNorm;
+/// without, before the loads): a kernel issues its weight rows there, so that the activation,
+/// requested first, arrives first (loads complete in order) and is staged while the weights are
+/// in flight. Scheduling barriers keep the compiler from moving either group of loads across.
 constexpr uint32_t kMaxStageParts = 4;
 
-template <int kBlockThreads, int kVec, bool kNorm>
+template <int kBlockThreads, int kVec, bool kNorm, class Between = NoOp>
 __device__ __forceinline__ float StageSplit(const float* __restrict__ x, const float* __restrict__ w, uint32_t n,
-                                            float eps, float4* xs, uint32_t parts = 1, float* sumOut = nullptr)
+                                            float eps, float4* xs, uint32_t parts = 1, float* sumOut = nullptr,
+                                            Between between = Between{})
 {
     constexpr int kWaveCount = kBlockThreads / kWave;
     const uint32_t n4 = n / 4;
@@ -245,6 +250,7 @@ __device__ __forceinline__ float StageSplit(const float* __restrict__ x, const f
     const float4* x4 = reinterpret_cast<const float4*>(x);
     if constexpr (!kNorm)
     {
+        between();
         for (uint32_t first = 0; first < n4; first += kVec * kBlockThreads)
         {
             float4 v[kVec];
@@ -278,10 +284,10 @@ __device__ __forceinline__ float StageSplit(const float* __restrict__ x, const f
             v[k] = x4[i];
             g[k] = w4[i];
         }
+        // Every part's loads go out before any is added: one latency for all of them.
+        float4 more[kMaxStageParts - 1][kVec];
         if (parts > 1)
         {
-            // Every part's loads go out before any is added: one latency for all of them.
-            float4 more[kMaxStageParts - 1][kVec];
 #pragma unroll
             for (uint32_t p = 1; p < kMaxStageParts; ++p)
             {
@@ -291,6 +297,12 @@ __device__ __forceinline__ float StageSplit(const float* __restrict__ x, const f
                     more[p - 1][k] = x4[min(p, parts - 1) * n4 + min(threadIdx.x + k * kBlockThreads, n4 - 1)];
                 }
             }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
+        if (parts > 1)
+        {
 #pragma unroll
             for (uint32_t p = 1; p < kMaxStageParts; ++p)
             {
