@@ -203,14 +203,12 @@ struct MergeStage
     /// 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c' and every lane adds its channels of the chunks' P.V
     /// rows with those weights, read from lane c by ds_swizzle: the exponentials and the division
     /// run once per chunk, not once per channel. One barrier publishes the merged row.
-    /// `between` (a kernel's weight loads) runs first: at these widths the weights are two
-    /// chunks a lane and arrive ahead of the partials anyway (requested after the partials,
-    /// o_proj took 4.6 us instead of 4.0).
+    /// `between` (a kernel's weight loads) runs once the partials are requested, so the merge
+    /// runs while the weights stream.
     template <int kThreads, int kVec, class Between = NoOp>
     __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
         static_assert(kThreads == kBlock, "the merge spreads the q dim over kBlock threads");
-        between();
         static_assert(kChunks <= 16, "a head's first 16 lanes weigh the chunks");
         const uint32_t nchunks = n / 8;
         const uint32_t t = min(threadIdx.x, n / 4 - 1);
@@ -223,8 +221,12 @@ struct MergeStage
         {
             a[k] = *reinterpret_cast<const float4*>(attnAcc + Slot(h, k) * headDim + d);
         }
-        const float mc = c < gridChunks && c < kChunks ? attnMax[Slot(h, c)] : -INFINITY;
+        const float mcLoaded = attnMax[Slot(h, min(c, kChunks - 1))];
         const float lc = attnSum[Slot(h, min(c, kChunks - 1))];
+        __builtin_amdgcn_sched_barrier(0);
+        between();
+        __builtin_amdgcn_sched_barrier(0);
+        const float mc = c < gridChunks && c < kChunks ? mcLoaded : -INFINITY;
         // Lanes 0..15 of each head hold its chunks (the rest -inf), so 16-lane groups suffice.
         const float top = GroupMax<16>(mc);
         const float e = top == -INFINITY || mc == -INFINITY ? 0.0f : exp2f(mc - top);
