@@ -692,7 +692,7 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
     half8 wa[kCpl];
     half8 wb[kCpl];
     auto load = [&](uint32_t k, half8(&w)[kCpl]) {
-        LoadBatch<kWave, kCpl>(epi.Row(rowOf(k), 0) + 8 * begin, 0, span, lane, w);
+        LoadBatch<kWave, kCpl>(epi.Row(min(rowOf(k), units - 1), 0) + 8 * begin, 0, span, lane, w);
     };
     auto dot = [&](uint32_t k, const half8(&w)[kCpl], const float4(&xlo)[kCpl], const float4(&xhi)[kCpl]) {
         const float d = GroupSum<kWave>(DotRegisters<kWave, kCpl>(w, xlo, xhi, span, lane));
@@ -701,14 +701,12 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
             partial[k][waveId] = d;
         }
     };
-    if (count > 0)
-    {
-        load(0, wa);
-    }
-    if (threadIdx.x < count)
-    {
-        epi.Ready(pre);
-    }
+    // The activation quarter first, then two rows, each buffer refilled as soon as its row is
+    // consumed. Loads complete in order, so a row's dot then waits only for that row. No load sits
+    // under a branch: the steady loop runs only while both refill rows exist and the tail's loads
+    // are straight-line, so the compiler's waits count every load (loads under a branch had it
+    // wait for the next row before using the current one). Rows are clamped into the matrix, so
+    // a workgroup with a single row reloads it (an L2 hit).
     float4 xlo[kCpl];
     float4 xhi[kCpl];
     float scale = 1.0f;  // the rms_norm factor of a norm stage
@@ -716,28 +714,47 @@ __global__ __launch_bounds__(kBlock) void FusedMatVecSplitRows(uint32_t cols, St
     {
         // Each wave reads its own quarter of x straight into registers: one latency, no LDS.
         LoadActivationDirect<kWave, kCpl, false>(stage.x + 8 * begin, nullptr, 8 * span, lane, xlo, xhi);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    else
+    load(0, wa);
+    load(min(1u, count - 1), wb);
+    __builtin_amdgcn_sched_barrier(0);
+    if (threadIdx.x < count)
+    {
+        epi.Ready(pre);
+    }
+    if constexpr (!Stage::kElementwise)
     {
         scale = stage.template Run<kBlock, kStageVec>(xs, cols);
         LoadActivation<kWave, kCpl>(xs + begin, xs + nchunks + begin, span, lane, xlo, xhi);
     }
-    for (uint32_t k = 0; k < count; k += 2)
+    uint32_t k = 0;
+    for (; k + 3 < count; k += 2)
     {
-        if (k + 1 < count)
-        {
-            load(k + 1, wb);
-        }
         dot(k, wa, xlo, xhi);
-        if (k + 1 >= count)
-        {
-            break;
-        }
-        if (k + 2 < count)
-        {
-            load(k + 2, wa);
-        }
+        load(k + 2, wa);
+        __builtin_amdgcn_sched_barrier(0);
         dot(k + 1, wb, xlo, xhi);
+        load(k + 3, wb);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint32_t left = count - k;  // 1, 2 or 3 rows (0 only for a workgroup without rows)
+    if (left == 3)
+    {
+        dot(k, wa, xlo, xhi);
+        load(k + 2, wa);
+        __builtin_amdgcn_sched_barrier(0);
+        dot(k + 1, wb, xlo, xhi);
+        dot(k + 2, wa, xlo, xhi);
+    }
+    else if (left == 2)
+    {
+        dot(k, wa, xlo, xhi);
+        dot(k + 1, wb, xlo, xhi);
+    }
+    else if (left == 1)
+    {
+        dot(k, wa, xlo, xhi);
     }
     __syncthreads();
     float bestValue = -INFINITY;
