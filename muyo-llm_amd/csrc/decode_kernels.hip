@@ -1510,18 +1510,24 @@ __global__ __launch_bounds__(kBlock) void AttentionChunk(const float* __restrict
     const half8* vBase = reinterpret_cast<const half8*>(vc + static_cast<uint64_t>(g) * maxSeq * kHd) + part;
     auto keyOf = [&](uint32_t block) { return (block * chunks + chunk) * kSlices + slice; };
 
-    // Round 0 before the position: this chunk's first kR blocks, clamped into the cache.
+    // Round 0 before the position: q, then this chunk's first kR blocks of K, then of V, clamped
+    // into the cache. Loads complete in order, so the scores wait only for q and K while the V
+    // rows are still arriving.
+    const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + h) * kHd) + part * 2;
+    const float4 q0 = qh[0];
+    const float4 q1 = qh[1];
     half8 kk[kR], vv[kR];
 #pragma unroll
     for (int k = 0; k < kR; ++k)
     {
-        const uint32_t key = min(keyOf(k), maxSeq - 1);
-        kk[k] = kBase[static_cast<uint64_t>(key) * kRC];
-        vv[k] = vBase[static_cast<uint64_t>(key) * kRC];
+        kk[k] = kBase[static_cast<uint64_t>(min(keyOf(k), maxSeq - 1)) * kRC];
     }
-    const float4* qh = reinterpret_cast<const float4*>(q + (static_cast<uint64_t>(g) * group + h) * kHd) + part * 2;
-    const float4 q0 = qh[0];
-    const float4 q1 = qh[1];
+#pragma unroll
+    for (int k = 0; k < kR; ++k)
+    {
+        vv[k] = vBase[static_cast<uint64_t>(min(keyOf(k), maxSeq - 1)) * kRC];
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const int32_t pos = *position;
     // Positions outside the cache are refused on the host; here they leave every chunk neutral.
     const uint32_t keys = pos >= 0 && static_cast<uint32_t>(pos) < maxSeq ? static_cast<uint32_t>(pos) + 1 : 0;
@@ -1816,9 +1822,12 @@ __global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t
         const uint32_t row = min(first + k * stride, hidden - 1);
         LoadBatch<kWave, kCpl>(wo + static_cast<uint64_t>(row) * qdim + g * gw, 0, nchunks, lane, w[k]);
     }
-    // Lane k < kRows stores row first + k * stride.
+    // Lane k < kRows stores row first + k * stride. Every group loads the residual (group 0 adds
+    // it): a load under a branch would leave the merge's waits unable to count it.
     const uint32_t myRow = first + (lane & 7u) * stride;
-    const float res = g == 0 ? residual[min(myRow, hidden - 1)] : 0.0f;
+    const float resLoaded = residual[min(myRow, hidden - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+    const float res = g == 0 ? resLoaded : 0.0f;
     {
         m = lane < gridChunks ? m : -INFINITY;
         const float top = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(GroupMax<16>(m))));
