@@ -335,8 +335,13 @@ __global__ __launch_bounds__(kThreads) void FusedMatVec(uint32_t cols, Stage sta
         // The epilogue's own work (Ready) runs while the weights and the activation are in flight.
         if constexpr (Stage::kDirect)
         {
-            loadFirst();
-            squares = stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] { epi.Ready(pre); });
+            // The activation (an L2 hit for all but the first workgroups of an XCD) is requested
+            // first and the weights right after it, so the norm's products run while the weights
+            // stream rather than after the activation has queued behind them.
+            squares = stage.template Direct<kLpr, kCpl>(cols, lir, xlo, xhi, [&] {
+                loadFirst();
+                epi.Ready(pre);
+            });
         }
         else
         {

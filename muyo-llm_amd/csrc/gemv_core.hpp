@@ -125,8 +125,9 @@ struct NoOp
 /// value is this lane's part of sum(x^2): the caller reduces it over the segment together with
 /// its dot products and multiplies the row sums by rsqrt(mean(x^2) + eps) at the end, so the
 /// norm's reduction runs beside the dot instead of before it. Without kNorm it returns 0.
-/// `between` runs once the loads are issued and before the norm waits for them (work that
-/// overlaps their latency).
+/// `between` runs once the loads are issued and before the norm waits for them: work that
+/// overlaps their latency, or a kernel's weight loads, which then arrive after the activation
+/// (loads complete in order). Scheduling barriers keep either side from moving across.
 template <int kLpr, int kCpl, bool kNorm, class Between = NoOp>
 __device__ __forceinline__ float LoadActivationDirect(const float* __restrict__ x, const float* __restrict__ w,
                                                       uint32_t n, uint32_t lir, float4 (&xlo)[kCpl],
@@ -149,7 +150,9 @@ __device__ __forceinline__ float LoadActivationDirect(const float* __restrict__ 
             ghi[i] = w4[2 * c + 1];
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
     between();
+    __builtin_amdgcn_sched_barrier(0);
     float ss = 0.0f;
     if constexpr (kNorm)
     {
