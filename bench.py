@@ -5,19 +5,21 @@ Workload: one greedy decode step of a Qwen2.5-0.5B-shaped model (24 layers, hidd
 4864, 14/2 heads, head_dim 64, tied vocab 151936), fp16 weights N(0, 0.02) from the portable
 seeded generator, fp16 KV cache pre-filled with N(0, 1), steps centred on cache position 1024.
 A "step" is one token: embed -> 24 x (norm+QKV+rope+append, attention, o_proj+residual,
-norm+gate/up+swiglu, down+residual) -> norm + LM head + argmax, replayed as one hipGraph with the
-greedy id fed back on the device. Inputs are resident in HBM before the timed region.
+norm+gate/up+swiglu+down+residual) -> norm + LM head + argmax, replayed as one hipGraph with the
+greedy id fed back on the device; the feed-forward block is one launch in layers 0..22 and two
+(gate/up, down) in layer 23. Inputs are resident in HBM before the timed region.
 
 value = algorithmic HBM bytes of the timed steps / time (GB/s): every weight once as fp16, the KV
 rows 0..p read once as fp16, the appended rows written, activations as f32 once per kernel that
 reads or writes them. tok/s is reported beside it.
 
-roofline: the kernel with the largest share of the step's time, the fused gate/up (rms_norm
-prologue + 2 x 4864 x 896 fp16 GEMV + swiglu), timed with HIP events on its stream while it
-rotates over the 24 layers' weights (420 MB, more than the 256 MB MALL); its share of the step
-comes from this run's per-kind timing (phases_us: each kernel kind graph-replayed over the 24
-layers); its HBM traffic and L2 hit rate come from the counter runs of the same kernel inside
-whole steps (traffic_source names them).
+roofline: the kernel with the largest share of the step's time, the one-launch feed-forward
+block (rms_norm + 2 x 4864 x 896 gate/up GEMV + swiglu + 896 x 4864 down GEMV, added into the
+hidden state's partial vectors), timed with HIP events on its stream while it rotates over the
+23 fused layers' weights (601 MB, more than the 256 MB MALL); its share of the step comes from
+this run's per-kind timing (phases_us: each kernel kind graph-replayed over the layers it runs
+in); its HBM traffic and L2 hit rate come from the counter runs of the same kernel inside whole
+steps (traffic_source names them).
 
 cpu_baseline: the reference's CPU path for the same workload (oracle/'s f32 step: HostMatVec-
 order f32 sums, gcc -O3) on one host core, the median of 10 single-step timings; the same with
@@ -43,14 +45,14 @@ sys.path.insert(0, str(ROOT / "muyo-llm_amd"))
 METRIC = "F16 GEMV+norm HBM GB/s (% of MI355X peak); Qwen2.5-0.5B-shape decode tok/s"
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core flop/s of MI355X
-# HBM bytes per gate/up launch (0.5B shape) from rocprofv3 FETCH_SIZE / WRITE_SIZE, each scaled by
-# what the counter reads for a 256 MiB device copy, and its L2 hit rate (TCC_HIT_sum /
-# (TCC_HIT_sum + TCC_MISS_sum)), over whole steps launched kernel by kernel
+# HBM bytes per launch of the one-launch feed-forward block (0.5B shape) from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE, each scaled by what the counter reads for a 256 MiB device copy, and its L2 hit rate
+# (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)), over whole steps launched kernel by kernel
 # (profiles/decode_step_counters_0.5b.md: `--kernel-only step_05b`, `--summarize-counters`).
-GATE_UP_TRAFFIC_BYTES = 17_605_209
-GATE_UP_L2_HIT_RATE = 0.155
-GATE_UP_COUNTER_SOURCE = ("profiles/decode_step_counters_0.5b.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (each scaled "
-                          "by a 256 MiB device copy) and TCC_HIT/TCC_MISS over whole steps, gate/up rows")
+FFN_TRAFFIC_BYTES = None
+FFN_L2_HIT_RATE = None
+FFN_COUNTER_SOURCE = ("profiles/decode_step_counters_0.5b.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (each scaled "
+                      "by a 256 MiB device copy) and TCC_HIT/TCC_MISS over whole steps, ffn rows")
 
 
 def step_bytes(c: dict, position: int) -> int:
@@ -76,7 +78,37 @@ def gate_up_bytes(c: dict) -> int:
     return 2 * 2 * c["ffn"] * c["hidden"] + 4 * c["hidden"] * 2 + 4 * c["ffn"]
 
 
+def ffn_bytes(c: dict) -> int:
+    """The one-launch feed-forward block: gate, up and down weights once, the input and the norm
+    weight read, the hidden state's new value written once."""
+    return 3 * 2 * c["ffn"] * c["hidden"] + 4 * c["hidden"] * 3
+
+
 STEP_KINDS = ("QKV", "ATTENTION", "O_PROJ", "GATE_UP", "DOWN")
+
+
+def ffn_fused(c: dict) -> bool:
+    """True when the decoder runs the feed-forward block as one launch (MUYO_KERNEL_FFN) in every
+    layer but the last: hidden sizes up to 1024 whose o_proj is not split by kv group, which holds
+    for the 0.5B shape and not for the 7B one (the decoder's own test; launch counts are checked
+    against muyo_decoder_launches_per_step where a decoder is at hand)."""
+    return c["hidden"] <= 1024 and c["layers"] >= 2
+
+
+def layer_kinds(c: dict, layer: int) -> tuple:
+    """The kernels of layer `layer` in the step's launch order."""
+    if ffn_fused(c) and layer + 1 < c["layers"]:
+        return ("QKV", "ATTENTION", "O_PROJ", "FFN")
+    return STEP_KINDS
+
+
+def kind_layers(c: dict) -> dict:
+    """Per kernel kind, the layers whose step runs it; GATE_UP and DOWN are also timed over every
+    layer in their two-launch form, for comparison."""
+    out = {kind: list(range(c["layers"])) for kind in STEP_KINDS}
+    if ffn_fused(c):
+        out["FFN"] = list(range(c["layers"] - 1))
+    return out
 
 
 def kernel_bytes(c: dict, kind: str, position: int) -> int:
@@ -99,16 +131,25 @@ def kernel_bytes(c: dict, kind: str, position: int) -> int:
         "o_proj": 2 * h * q + partials + 4 * h + (4 * h if merged else parts),
         "gate_up": 4 * f * h + (8 * h if merged else parts + 8 * h) + 4 * f,
         "down": 2 * h * f + 4 * f + 8 * h,
+        "ffn": ffn_bytes(c),
         "lm_head": lm_head_bytes(c),
     }
     return table[kind]
+
+
+def chain_bytes_of(c: dict, position: int) -> list:
+    """Algorithmic bytes of each launch of one step, in launch order."""
+    seq = [kernel_bytes(c, "embed", position)]
+    for layer in range(c["layers"]):
+        seq += [kernel_bytes(c, kind.lower(), position) for kind in layer_kinds(c, layer)]
+    return seq + [kernel_bytes(c, "lm_head", position)]
 
 
 def enqueue_step(dec, shape, stream) -> None:
     """One decode step launched kernel by kernel (the graph's sequence, enqueued eagerly)."""
     dec.enqueue_kernel("EMBED", 0, stream)
     for layer in range(shape["layers"]):
-        for kind in STEP_KINDS:
+        for kind in layer_kinds(shape, layer):
             dec.enqueue_kernel(kind, layer, stream)
     dec.enqueue_kernel("LM_HEAD", 0, stream)
 
@@ -236,7 +277,8 @@ def prefill_line(mh, torch, shape, prompt, reps, seed, decode_ms):
 
 
 def time_kernels(mh, torch, shape, seed, rounds):
-    """Per-launch ms of the LM-head kernel and of the gate/up kernel rotated over all layers."""
+    """Per-launch ms of the LM-head kernel and of the roofline kernel (the one-launch feed-forward
+    block where the decoder runs it, else gate/up) rotated over the layers that run it."""
     stream = torch.cuda.current_stream()
     s = stream.cuda_stream
     dec = mh.Decoder(mh.qwen2_config(**shape))
@@ -254,26 +296,29 @@ def time_kernels(mh, torch, shape, seed, rounds):
         e.record(stream)
         torch.cuda.synchronize()
         out["lm_head_ms"] = b.elapsed_time(e) / rounds
-        for layer in range(shape["layers"]):
-            dec.enqueue_kernel("GATE_UP", layer, s)
+        kind = "FFN" if ffn_fused(shape) else "GATE_UP"
+        layers = kind_layers(shape)[kind]
+        for layer in layers:
+            dec.enqueue_kernel(kind, layer, s)
         torch.cuda.synchronize()
         b.record(stream)
         for _ in range(max(1, rounds // 4)):
-            for layer in range(shape["layers"]):
-                dec.enqueue_kernel("GATE_UP", layer, s)
+            for layer in layers:
+                dec.enqueue_kernel(kind, layer, s)
         e.record(stream)
         torch.cuda.synchronize()
-        out["gate_up_ms"] = b.elapsed_time(e) / (max(1, rounds // 4) * shape["layers"])
+        out["roofline_kind"] = kind
+        out["roofline_ms"] = b.elapsed_time(e) / (max(1, rounds // 4) * len(layers))
     finally:
         dec.close()
     return out
 
 
 def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
-    """Microseconds per launch of each per-layer kernel of the step (STEP_KINDS), each kind's
-    launches over every layer captured into one graph (torch's CUDAGraph around the decoder's
-    per-kernel launches) and replayed `reps` times: the kernels as the step's graph runs them,
-    minus their data dependence on the neighbouring kinds."""
+    """Microseconds per launch of each per-layer kernel kind (kind_layers), each kind's launches
+    over its layers captured into one graph (torch's CUDAGraph around the decoder's per-kernel
+    launches) and replayed `reps` times: the kernels as the step's graph runs them, minus their
+    data dependence on the neighbouring kinds."""
     stream = torch.cuda.Stream()
     dec = mh.Decoder(mh.qwen2_config(**shape))
     out = {}
@@ -282,13 +327,13 @@ def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
         dec.fill_kv_random(position, seed + 1)
         dec.set_state(9707, position, stream.cuda_stream)
         settle(torch)
-        for kind in STEP_KINDS:
-            for layer in range(shape["layers"]):
+        for kind, layers in kind_layers(shape).items():
+            for layer in layers:
                 dec.enqueue_kernel(kind, layer, stream.cuda_stream)
             torch.cuda.synchronize()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
-                for layer in range(shape["layers"]):
+                for layer in layers:
                     dec.enqueue_kernel(kind, layer, stream.cuda_stream)
             for _ in range(2):
                 graph.replay()
@@ -300,7 +345,7 @@ def time_phases(mh, torch, shape, position, seed, reps=20) -> dict:
                     graph.replay()
                 e.record(stream)
             torch.cuda.synchronize()
-            out[kind.lower()] = 1000.0 * b.elapsed_time(e) / (reps * shape["layers"])
+            out[kind.lower()] = 1000.0 * b.elapsed_time(e) / (reps * len(layers))
             del graph
     finally:
         dec.close()
@@ -333,27 +378,26 @@ def floor_chain(torch, byte_list, reps=20) -> dict:
 def floor_report(mh, torch, which: str) -> dict:
     """The decode step beside its streaming floor. `which`: 05b (0.5B shape, cache rows
     1014..1033, as the default bench line) or 7b (7B shape, rows 2032..2047).
-    chain: the step's launch sequence (embed, per layer qkv / attention / o_proj / gate_up / down,
-    LM head) with each launch's algorithmic bytes at the window's middle row, as pure streams;
-    phases: per kind, `layers` launches of its bytes as pure streams beside the step's own kernels
-    (time_phases), microseconds per launch."""
+    chain: the step's launch sequence (embed, per layer qkv / attention / o_proj and the
+    feed-forward launch or launches, LM head) with each launch's algorithmic bytes at the window's
+    middle row, as pure streams; phases: per kind, as many launches of its bytes as pure streams
+    as the kind has layers, beside the step's own kernels (time_phases), microseconds per launch."""
     shape = dict(mh.QWEN25_05B if which == "05b" else mh.QWEN25_7B)
     steps, warmup, centre = (20, 5, 1024) if which == "05b" else (16, 4, 2040)
     seed = 20261201 if which == "05b" else 20261208
     ms, positions, launches, _, median = time_decode(mh, torch, shape, centre, steps, warmup, seed)
     position = positions[len(positions) // 2]
-    per_layer = [kernel_bytes(shape, kind.lower(), position) for kind in STEP_KINDS]
-    chain_bytes = [kernel_bytes(shape, "embed", position)] + per_layer * shape["layers"] + \
-        [kernel_bytes(shape, "lm_head", position)]
+    chain_bytes = chain_bytes_of(shape, position)
     assert len(chain_bytes) == launches, (len(chain_bytes), launches)
     chain = floor_chain(torch, chain_bytes)
     total = sum(chain_bytes)
     step_bytes_mid = step_bytes(shape, position)
     kernels = time_phases(mh, torch, shape, position, seed)
     phases = {}
-    for kind, nbytes in zip(STEP_KINDS, per_layer):
-        stream_ms = floor_chain(torch, [nbytes] * shape["layers"])["best_ms"]
-        stream_us = 1000.0 * stream_ms / shape["layers"]
+    for kind, layers in kind_layers(shape).items():
+        nbytes = kernel_bytes(shape, kind.lower(), position)
+        stream_ms = floor_chain(torch, [nbytes] * len(layers))["best_ms"]
+        stream_us = 1000.0 * stream_ms / len(layers)
         phases[kind.lower()] = {"bytes": nbytes, "stream_us": round(stream_us, 2),
                                 "kernel_us": round(kernels[kind.lower()], 2),
                                 "excess_us": round(kernels[kind.lower()] - stream_us, 2)}
@@ -379,9 +423,7 @@ def launch_floor_report(mh, which: str) -> dict:
 
     shape = dict(mh.QWEN25_05B if which == "05b" else mh.QWEN25_7B)
     position = 1024 if which == "05b" else 2040
-    per_layer = [kernel_bytes(shape, kind.lower(), position) for kind in STEP_KINDS]
-    chain = [kernel_bytes(shape, "embed", position)] + per_layer * shape["layers"] + \
-        [kernel_bytes(shape, "lm_head", position)]
+    chain = chain_bytes_of(shape, position)
     tool = ROOT / "muyo-llm_amd" / "launch_floor"
     code = ROOT / "muyo-llm_amd" / "launch_floor_kernels.co"
     run = subprocess.run([str(tool), str(code)], input="\n".join(str(b) for b in chain), capture_output=True,
@@ -685,6 +727,8 @@ def step_kind(name: str, previous: str | None) -> str | None:
         return "o_proj"
     if "GateUpEpi" in name:
         return "gate_up"
+    if "FfnFused" in name:
+        return "ffn"
     if "LmHeadEpi" in name:
         return "lm_head"
     if "ResidualEpi" in name:
@@ -751,14 +795,16 @@ def summarize_counters(root: pathlib.Path, which: str) -> str:
     hits = counter_means("hit", {"TCC_HIT_sum", "TCC_MISS_sum"})
     steps = len(durations["lm_head"])
     per_step = {"embed": 1, "qkv": shape["layers"], "attention": shape["layers"], "merge": shape["layers"],
-                "o_proj": shape["layers"], "gate_up": shape["layers"], "down": shape["layers"], "lm_head": 1}
+                "o_proj": shape["layers"], "lm_head": 1}
+    for kind in ("GATE_UP", "DOWN", "FFN"):
+        per_step[kind.lower()] = sum(kind in layer_kinds(shape, layer) for layer in range(shape["layers"]))
     lines = [f"fetch scale {fetch_scale:.4f}, write scale {write_scale:.4f} (256 MiB copy); {steps} steps",
              "",
              "| kernel | launches/step | avg µs | µs/step | share | algorithmic bytes | counter bytes | "
              "counter/alg | GB/s (alg) | % of 8 TB/s | L2 hit rate |",
              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
     total = sum(per_step[k] * sum(v) / len(v) for k, v in durations.items())
-    for k in ("embed", "qkv", "attention", "merge", "o_proj", "gate_up", "down", "lm_head"):
+    for k in ("embed", "qkv", "attention", "merge", "o_proj", "ffn", "gate_up", "down", "lm_head"):
         if k not in durations:
             continue
         us = sum(durations[k]) / len(durations[k])
@@ -946,7 +992,10 @@ def main() -> int:
     phases = time_phases(mh, torch, shape, positions[len(positions) // 2], seed)
     ops = {} if args.no_ops else time_ops(mh, torch)
     lm_gbs = lm_head_bytes(shape) / (kern["lm_head_ms"] * 1e-3) / 1e9
-    gu_gbs = gate_up_bytes(shape) / (kern["gate_up_ms"] * 1e-3) / 1e9
+    assert ffn_fused(shape) and kern["roofline_kind"] == "FFN", kern["roofline_kind"]
+    assert launches == len(chain_bytes_of(shape, positions[0])), launches
+    ffn_gbs = ffn_bytes(shape) / (kern["roofline_ms"] * 1e-3) / 1e9
+    ffn_layers = len(kind_layers(shape)["FFN"])
 
     secondary = {}
     # The same decode with the device sampler after every step (the reference's sampling options
@@ -999,19 +1048,21 @@ def main() -> int:
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 1),
         "bytes_per_step": total_bytes // args.steps,
         "roofline": {
-            "kernel": "FusedMatVec<16,7,2,true,NormStage,GateUpEpi,64> (ffn_norm + gate/up 2x4864x896 + swiglu)",
+            "kernel": "FfnFusedKernel (ffn_norm + gate/up 2x4864x896 + swiglu + down 896x4864 from transposed "
+                      "weights, added into the hidden state's partial vectors)",
             "bound": "hbm",
-            "achieved": round(gu_gbs, 1),
+            "achieved": round(ffn_gbs, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-            "traffic": GATE_UP_TRAFFIC_BYTES,
-            "l2_hit_rate": GATE_UP_L2_HIT_RATE,
-            "traffic_source": GATE_UP_COUNTER_SOURCE,
-            "launch_ms": round(kern["gate_up_ms"], 5),
-            "bytes_per_launch": gate_up_bytes(shape),
-            "share_of_step": round(phases["gate_up"] * shape["layers"] / (ms * 1000.0), 3),
-            "note": "rotated over the 24 layers' weights (420 MB > MALL)",
+            "frac": round(ffn_gbs / HBM_PEAK_GBS, 4),
+            "traffic": FFN_TRAFFIC_BYTES,
+            "l2_hit_rate": FFN_L2_HIT_RATE,
+            "traffic_source": FFN_COUNTER_SOURCE,
+            "launch_ms": round(kern["roofline_ms"], 5),
+            "bytes_per_launch": ffn_bytes(shape),
+            "share_of_step": round(phases["ffn"] * ffn_layers / (ms * 1000.0), 3),
+            "note": f"rotated over the {ffn_layers} fused layers' weights "
+                    f"({ffn_layers * ffn_bytes(shape) / 1e6:.0f} MB > MALL)",
         },
         "kernels": {
             "lm_head": {"GB/s": round(lm_gbs, 1), "launch_ms": round(kern["lm_head_ms"], 5),

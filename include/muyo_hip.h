@@ -303,7 +303,11 @@ enum
     MUYO_KERNEL_O_PROJ = 3,    /* [attention merge +] o_proj GEMV + residual */
     MUYO_KERNEL_GATE_UP = 4,   /* rms_norm + gate/up GEMV + swiglu */
     MUYO_KERNEL_DOWN = 5,      /* down GEMV + residual */
-    MUYO_KERNEL_LM_HEAD = 6    /* rms_norm + tied LM head + per-workgroup argmax partials */
+    MUYO_KERNEL_LM_HEAD = 6,   /* rms_norm + tied LM head + per-workgroup argmax partials */
+    MUYO_KERNEL_FFN = 7        /* rms_norm + gate/up + swiglu + down in one launch, on decoders with a
+                                  hidden size of at most 1024 and layers other than the last (the
+                                  step's own feed-forward launch there; GATE_UP and DOWN still run
+                                  the two-launch form) */
 };
 
 /* Set the device-side token and position (stream-ordered) without running a step. */

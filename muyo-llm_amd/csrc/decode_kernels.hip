@@ -16,6 +16,9 @@
 //   GateUpSwiGlu   : rms_norm prologue (summing the o_proj group parts) -> gate and up GEMV
 //                    rows -> silu(g)*u
 //   Down           : down GEMV + residual add
+//   (FfnFused      : gate/up, swiglu and down in one launch on decoders with a hidden size of at
+//                    most 1024: each workgroup's slice of the down product is added with atomics
+//                    into partial vectors of the hidden state, which the next layer sums)
 //   LmHeadArgMax   : final rms_norm prologue -> tied LM head -> logits + per-workgroup argmax
 //
 // GEMV core (gemv_core.hpp): a wave64 splits into segments of LPR lanes, each segment streaming
@@ -26,6 +29,7 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
@@ -146,6 +150,41 @@ struct PartsNormStage
         return StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr,
                                                 between);
     }
+};
+
+/// NormStage over a hidden state held as kResidualParts partial vectors laid end to end (the fused
+/// feed-forward kernel's output): x = ((p0 + p1) + p2) + ..., rms_norm applied as NormStage does.
+struct SumNormStage
+{
+    const float* parts;  // [kResidualParts][n]
+    const float* w;
+    float eps;
+    static constexpr bool kCanDirect = true;
+    static constexpr bool kDirect = false;
+    static constexpr bool kElementwise = false;
+    static constexpr bool kNorm = true;
+    static constexpr bool kSumsParts = true;  // the column-quarter kernel reads a single vector
+    template <int kLpr, int kCpl, class Between>
+    __device__ float Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
+    {
+        return LoadActivationDirectParts<kLpr, kCpl, kResidualParts>(parts, w, n, lir, xlo, xhi, between);
+    }
+    template <int kThreads, int kVec, class Between = NoOp>
+    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
+    {
+        return StageSplit<kThreads, kVec, true, Between, kResidualParts>(parts, w, n, eps, xs, kResidualParts,
+                                                                         nullptr, between);
+    }
+};
+
+/// True for a stage whose activation is a sum of partial vectors.
+template <class Stage, class = void>
+struct SumsParts : std::false_type
+{
+};
+template <class Stage>
+struct SumsParts<Stage, std::void_t<decltype(Stage::kSumsParts)>> : std::bool_constant<Stage::kSumsParts>
+{
 };
 
 /// A staging policy applied by every lane to its own activation chunks, straight from global
@@ -902,6 +941,63 @@ struct ResidualEpi
     }
 };
 
+/// ResidualEpi for the decoders whose feed-forward block is one launch. The residual is either a
+/// single vector (inParts 1) or kResidualParts partial vectors laid end to end, added in order
+/// (p0 + p1) + ... before the dot; with `parts` set the output also seeds the feed-forward
+/// kernel's partial vectors: parts[0][row] = out[row], the other parts' rows zero. The residual
+/// may be `parts` itself: each row is read and written only by the lanes that own it.
+struct ResidualPartsEpi
+{
+    const uint16_t* w;
+    const float* residual;
+    float* out;
+    float* parts;
+    uint32_t rows, cols, inParts;
+
+    __device__ uint32_t Units() const { return rows; }
+    __device__ const uint16_t* Row(uint32_t unit, int) const { return w + static_cast<uint64_t>(unit) * cols; }
+    struct Pre
+    {
+        float v[kResidualParts];
+    };
+    /// Branch-free: with a single residual vector every load reads it (cache hits).
+    __device__ Pre Prefetch(uint32_t unit) const
+    {
+        Pre p;
+#pragma unroll
+        for (uint32_t k = 0; k < kResidualParts; ++k)
+        {
+            p.v[k] = residual[min(k, inParts - 1) * static_cast<uint64_t>(rows) + unit];
+        }
+        return p;
+    }
+    __device__ void Ready(Pre&) const {}
+    __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float&, int32_t&) const
+    {
+        float res = pre.v[0];
+#pragma unroll
+        for (uint32_t k = 1; k < kResidualParts; ++k)
+        {
+            res += k < inParts ? pre.v[k] : 0.0f;
+        }
+        const float value = res + s[0];
+        out[unit] = value;
+        if (parts != nullptr)
+        {
+            parts[unit] = value;
+#pragma unroll
+            for (uint32_t k = 1; k < kResidualParts; ++k)
+            {
+                parts[k * static_cast<uint64_t>(rows) + unit] = 0.0f;
+            }
+        }
+    }
+    template <int kThreads>
+    __device__ void Tail(float, int32_t) const
+    {
+    }
+};
+
 /// out[row] = (W[row] . x + bias0[row]) + bias1[row], each bias only when given: the per-op
 /// GEMV's FUSE0/FUSE1 in mul_mat_vec_base.glsl's order.
 struct BiasEpi
@@ -1188,13 +1284,17 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
         // Units past one round of resident waves: column quarters with several units per
         // workgroup put the whole matrix in flight at once (rows of 257..512 chunks, where a
         // quarter is two chunks per lane).
-        if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
+        // (Not for an activation summed from partial vectors: the column kernel reads one vector.)
+        if constexpr (!SumsParts<Stage>::value)
         {
-            const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
-                                                                        shapeOut);
-            if (status != hipErrorNotSupported)
+            if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
             {
-                return status;
+                const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
+                                                                            shapeOut);
+                if (status != hipErrorNotSupported)
+                {
+                    return status;
+                }
             }
         }
     }
@@ -1316,6 +1416,158 @@ hipError_t LaunchFused(hipStream_t s, uint32_t units, uint32_t blockCap, uint32_
 #undef MUYO_BLOCK_ROW_CASE
     }
     return hipErrorInvalidValue;
+}
+
+// ------------------------------------------------------------------------------------------------
+// Feed-forward block in one launch (hidden <= 1024).
+//
+// Workgroup b owns the kFfnUnits intermediate units from kFfnUnits * b: wave w the units w,
+// w + 4, ... . Every wave reads the activation (x * rms_norm weight) straight into registers,
+// 64 lanes x 2 chunks covering a row of up to 1024 floats, and its units' gate and up rows; at the
+// same time the workgroup requests its units' rows of the transposed down matrix (downT, one
+// contiguous row of `hidden` weights per unit), so one launch streams all three matrices and the
+// down rows arrive while the gate/up dots run. The units' swiglu values meet in LDS. Threads
+// t < 2 * hidden/8 then own chunk t mod (hidden/8) of every other unit's down row, the two halves
+// meet in LDS, and the workgroup adds its partial down product into partial vector
+// b mod kResidualParts with one atomic add per element. Every workgroup adds to every element, so
+// the adds to one address serialise at the memory: spreading them over kResidualParts vectors
+// keeps that cost under the kernel's streaming time.
+constexpr uint32_t kFfnUnits = 19;      // 4864 / 19 = 256 workgroups at the 0.5B shape, one per CU
+constexpr uint32_t kFfnMaxChunks = 128;  // hidden <= 1024
+
+__global__ __launch_bounds__(kBlock) void FfnFusedKernel(const float* __restrict__ x, const float* __restrict__ normW,
+                                                         const uint16_t* __restrict__ wgate,
+                                                         const uint16_t* __restrict__ wup,
+                                                         const uint16_t* __restrict__ downT, float* parts,
+                                                         uint32_t hidden, uint32_t ffn, float eps)
+{
+    constexpr uint32_t kPerWave = (kFfnUnits + kWaves - 1) / kWaves;
+    constexpr uint32_t kPerHalf = (kFfnUnits + 1) / 2;
+    __shared__ float act[kFfnUnits];
+    __shared__ float4 upper[kFfnMaxChunks][2];
+    __shared__ float total[8 * kFfnMaxChunks];
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & (kWave - 1);
+    const uint32_t wave = t / kWave;
+    const uint32_t nchunks = hidden / 8;
+    const uint32_t base = blockIdx.x * kFfnUnits;
+    // Down rows: half h (0 or 1) takes units h, h + 2, ...; threads past 2 * nchunks load a copy
+    // of half 1's rows (cache hits) and drop it, which keeps every load branch-free.
+    const uint32_t chunk = t % nchunks;
+    const uint32_t half = min(t / nchunks, 1u);
+    const bool owner = t < 2 * nchunks;
+    auto unitRow = [&](uint32_t j) { return min(base + min(j, kFfnUnits - 1), ffn - 1); };
+    half8 g[kPerWave][2];
+    half8 u[kPerWave][2];
+    half8 d[kPerHalf];
+    float4 xlo[2];
+    float4 xhi[2];
+    // The activation first, then the gate/up rows, then the down rows: loads complete in order,
+    // so the norm and the gate/up dots wait only for what they use.
+    const float squares = LoadActivationDirect<kWave, 2, true>(x, normW, hidden, lane, xlo, xhi, [&] {
+#pragma unroll
+        for (uint32_t k = 0; k < kPerWave; ++k)
+        {
+            const uint64_t row = unitRow(wave + kWaves * k);
+            LoadBatch<kWave, 2>(wgate + row * hidden, 0, nchunks, lane, g[k]);
+            LoadBatch<kWave, 2>(wup + row * hidden, 0, nchunks, lane, u[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kPerHalf; ++k)
+        {
+            const uint64_t row = unitRow(half + 2 * k);
+            d[k] = __builtin_nontemporal_load(reinterpret_cast<const half8*>(downT + row * hidden) + chunk);
+        }
+    });
+    float sums[2 * kPerWave + 1];
+#pragma unroll
+    for (uint32_t k = 0; k < kPerWave; ++k)
+    {
+        sums[2 * k] = DotRegisters<kWave, 2>(g[k], xlo, xhi, nchunks, lane);
+        sums[2 * k + 1] = DotRegisters<kWave, 2>(u[k], xlo, xhi, nchunks, lane);
+    }
+    sums[2 * kPerWave] = squares;
+    GroupSumN<kWave>(sums);
+    const float scale = NormScale(sums[2 * kPerWave], hidden, eps);
+#pragma unroll
+    for (uint32_t k = 0; k < kPerWave; ++k)
+    {
+        const uint32_t j = wave + kWaves * k;
+        if (j < kFfnUnits && lane == 0)
+        {
+            const float gv = sums[2 * k] * scale;
+            const float uv = sums[2 * k + 1] * scale;
+            // A unit past the matrix (the last workgroup's) weighs nothing: its clamped row is a
+            // copy of the last one.
+            act[j] = base + j < ffn ? gv / (1.0f + expf(-gv)) * uv : 0.0f;  // as GateUpEpi
+        }
+    }
+    __syncthreads();
+    float acc[8] = {};
+#pragma unroll
+    for (uint32_t k = 0; k < kPerHalf; ++k)
+    {
+        const uint32_t j = half + 2 * k;
+        const float a = j < kFfnUnits ? act[min(j, kFfnUnits - 1)] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+        {
+            acc[e] = fmaf(a, static_cast<float>(d[k][e]), acc[e]);
+        }
+    }
+    if (owner && half == 1)
+    {
+        upper[chunk][0] = float4{acc[0], acc[1], acc[2], acc[3]};
+        upper[chunk][1] = float4{acc[4], acc[5], acc[6], acc[7]};
+    }
+    __syncthreads();
+    if (owner && half == 0)
+    {
+        const float4 lo = upper[chunk][0];
+        const float4 hi = upper[chunk][1];
+        const float other[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+        {
+            total[8 * chunk + e] = acc[e] + other[e];
+        }
+    }
+    __syncthreads();
+    // Consecutive lanes add consecutive elements: each wave's atomics cover whole cache lines.
+    float* dst = parts + (blockIdx.x % kResidualParts) * static_cast<uint64_t>(hidden);
+    for (uint32_t i = t; i < hidden; i += kBlock)
+    {
+        __hip_atomic_fetch_add(dst + i, total[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+/// dst[c][r] = src[r][c], through 64 x 64 tiles in LDS.
+__global__ __launch_bounds__(kBlock) void TransposeF16Kernel(const uint16_t* __restrict__ src,
+                                                             uint16_t* __restrict__ dst, uint32_t rows,
+                                                             uint32_t cols)
+{
+    __shared__ uint16_t tile[64][66];
+    const uint32_t r0 = blockIdx.y * 64;
+    const uint32_t c0 = blockIdx.x * 64;
+    for (uint32_t i = threadIdx.x; i < 64 * 64; i += kBlock)
+    {
+        const uint32_t r = i / 64;
+        const uint32_t c = i % 64;
+        if (r0 + r < rows && c0 + c < cols)
+        {
+            tile[r][c] = src[static_cast<uint64_t>(r0 + r) * cols + c0 + c];
+        }
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < 64 * 64; i += kBlock)
+    {
+        const uint32_t c = i / 64;
+        const uint32_t r = i % 64;
+        if (r0 + r < rows && c0 + c < cols)
+        {
+            dst[static_cast<uint64_t>(c0 + c) * rows + r0 + r] = tile[r][c];
+        }
+    }
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1974,12 +2226,20 @@ hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch
 
 hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                                const uint16_t* wqkv, const float* bias, const DecodeState* state, float* qOut,
-                               uint16_t* kcache, uint16_t* vcache)
+                               uint16_t* kcache, uint16_t* vcache, uint32_t xParts)
 {
     QkvEpi epi{wqkv,       bias,         state,        qOut,         kcache,
                vcache,     dims.ropePow, dims.hidden,  dims.heads,   dims.kvHeads,
                dims.headDim, dims.maxSeq};
     const uint32_t units = (dims.heads + 2 * dims.kvHeads) * dims.headDim / 2;
+    if (xParts == kResidualParts)
+    {
+        return LaunchFused<2>(s, units, kNoLimit, dims.hidden, SumNormStage{x, normW, dims.eps}, epi);
+    }
+    if (xParts != 1)
+    {
+        return hipErrorInvalidValue;
+    }
     return LaunchFused<2>(s, units, kNoLimit, dims.hidden, NormStage{x, normW, dims.eps}, epi);
 }
 
@@ -2021,12 +2281,11 @@ hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const Dec
     return hipGetLastError();
 }
 
-hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
-                             const float* residual, float* out)
+template <class Epi>
+hipError_t LaunchOProjMergedT(hipStream_t s, const DecodeDims& dims, const DecodeScratch& scratch, const Epi& epi)
 {
     const uint32_t qdim = dims.heads * dims.headDim;
     const uint32_t chunks = AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks);
-    ResidualEpi epi{wo, residual, out, dims.hidden, qdim};
     if (chunks <= kShortAttnChunks)
     {
         MergeStage<kShortAttnChunks> stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads,
@@ -2036,6 +2295,38 @@ hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16
     MergeStage<kMergeAttnChunks> stage{scratch.attnMax, scratch.attnSum, scratch.attnAcc, dims.heads,
                                        dims.heads / dims.kvHeads, dims.headDim, chunks};
     return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, stage, epi);
+}
+
+hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
+                             const float* residual, float* out, uint32_t residualParts, float* parts)
+{
+    const uint32_t qdim = dims.heads * dims.headDim;
+    if (residualParts == 1 && parts == nullptr)
+    {
+        return LaunchOProjMergedT(s, dims, scratch, ResidualEpi{wo, residual, out, dims.hidden, qdim});
+    }
+    if (residualParts != 1 && residualParts != kResidualParts)
+    {
+        return hipErrorInvalidValue;
+    }
+    return LaunchOProjMergedT(s, dims, scratch,
+                              ResidualPartsEpi{wo, residual, out, parts, dims.hidden, qdim, residualParts});
+}
+
+hipError_t LaunchOProjPlain(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const float* attn,
+                            const float* residual, float* out, uint32_t residualParts, float* parts)
+{
+    const uint32_t qdim = dims.heads * dims.headDim;
+    if (residualParts == 1 && parts == nullptr)
+    {
+        return LaunchMatVecResidual(s, wo, attn, residual, out, dims.hidden, qdim);
+    }
+    if (residualParts != 1 && residualParts != kResidualParts)
+    {
+        return hipErrorInvalidValue;
+    }
+    return LaunchFused<1>(s, dims.hidden, kNoLimit, qdim, PlainStage{attn},
+                          ResidualPartsEpi{wo, residual, out, parts, dims.hidden, qdim, residualParts});
 }
 
 bool OProjInGroups(const DecodeDims& dims)
@@ -2132,6 +2423,35 @@ hipError_t LaunchGateUpSwiGlu(hipStream_t s, const DecodeDims& dims, const float
 {
     GateUpEpi epi{wgate, wup, act, dims.ffn, dims.hidden};
     return LaunchFused<2>(s, dims.ffn, kNoLimit, dims.hidden, NormStage{x, normW, dims.eps}, epi);
+}
+
+bool FfnFusable(const DecodeDims& dims)
+{
+    return dims.hidden >= 8 && dims.hidden <= 8 * kFfnMaxChunks && dims.hidden % 8 == 0 && dims.ffn >= 1 &&
+           !OProjInGroups(dims);
+}
+
+hipError_t LaunchFfnFused(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
+                          const uint16_t* wgate, const uint16_t* wup, const uint16_t* downT, float* parts)
+{
+    if (!FfnFusable(dims))
+    {
+        return hipErrorInvalidValue;
+    }
+    hipLaunchKernelGGL(FfnFusedKernel, dim3(CeilDiv(dims.ffn, kFfnUnits)), dim3(kBlock), 0, s, x, normW, wgate, wup,
+                       downT, parts, dims.hidden, dims.ffn, dims.eps);
+    return hipGetLastError();
+}
+
+hipError_t LaunchTransposeF16(hipStream_t s, const uint16_t* src, uint16_t* dst, uint32_t rows, uint32_t cols)
+{
+    if (rows == 0 || cols == 0)
+    {
+        return hipSuccess;
+    }
+    hipLaunchKernelGGL(TransposeF16Kernel, dim3(CeilDiv(cols, 64u), CeilDiv(rows, 64u)), dim3(kBlock), 0, s, src,
+                       dst, rows, cols);
+    return hipGetLastError();
 }
 
 hipError_t LaunchLmHeadArgMax(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,

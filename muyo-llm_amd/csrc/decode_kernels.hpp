@@ -55,6 +55,10 @@ struct DecodeScratch
 };
 
 constexpr uint32_t kArgMaxBlocks = 2048;
+/// Partial vectors the fused feed-forward kernel adds its down projection into (atomically); the
+/// layer's output is their sum. Fewer vectors mean more atomic adds to each address, which
+/// serialise: at the 0.5B shape the kernel takes 7.7 us with 8, 8.3 with 4, 12.7 with 1.
+constexpr uint32_t kResidualParts = 8;
 constexpr uint32_t kMaxAttnChunks = 16;    // attention chunks per kv head, at most
 constexpr uint32_t kMergeAttnChunks = 8;   // the same when o_proj's prologue merges the partials
 constexpr uint32_t kShortAttnChunks = 4;   // the same while every chunk's keys fit its first round
@@ -108,17 +112,40 @@ hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* st
 hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, uint32_t argBlocks,
                           int32_t* ids, uint32_t idsCap);
 
+/// `xParts` 1: x is the hidden state; kResidualParts: x holds that many partial vectors (the
+/// fused feed-forward kernel's output) whose sum is the hidden state.
 hipError_t LaunchQkvRopeAppend(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
                                const uint16_t* wqkv, const float* bias, const DecodeState* state, float* qOut,
-                               uint16_t* kcache, uint16_t* vcache);
+                               uint16_t* kcache, uint16_t* vcache, uint32_t xParts = 1);
 
 hipError_t LaunchAttention(hipStream_t s, const DecodeDims& dims, const float* q, const uint16_t* kcache,
                            const uint16_t* vcache, const int32_t* position, const DecodeScratch& scratch);
 
 hipError_t LaunchAttentionMerge(hipStream_t s, const DecodeDims& dims, const DecodeScratch& scratch, float* out);
 
+/// out = residual + W_o . merged attention. `residualParts` 1 or kResidualParts (as
+/// LaunchQkvRopeAppend's xParts); `parts`, when set, also receives out as the partial vectors
+/// the fused feed-forward kernel adds into: parts[0] = out, parts[1..] = 0.
 hipError_t LaunchOProjMerged(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
-                             const float* residual, float* out);
+                             const float* residual, float* out, uint32_t residualParts = 1, float* parts = nullptr);
+
+/// The same with the attention output already merged (`attn`, heads * headDim floats).
+hipError_t LaunchOProjPlain(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const float* attn,
+                            const float* residual, float* out, uint32_t residualParts, float* parts);
+
+/// True when the decoder runs gate/up, swiglu and down as one launch (FfnFused): a hidden size
+/// of at most 1024 and o_proj not split by kv group.
+bool FfnFusable(const DecodeDims& dims);
+
+/// The feed-forward block in one launch: rms_norm(x) . gate/up,
+/// swiglu, and the down projection from its transposed weights downT [ffn][hidden], added with
+/// atomics into `parts` ([kResidualParts][hidden], holding the residual as o_proj left it). The
+/// order of the atomic adds varies from run to run, so the sum does in its last bits.
+hipError_t LaunchFfnFused(hipStream_t s, const DecodeDims& dims, const float* x, const float* normW,
+                          const uint16_t* wgate, const uint16_t* wup, const uint16_t* downT, float* parts);
+
+/// dst[c][r] = src[r][c] for an fp16 matrix of `rows` x `cols`.
+hipError_t LaunchTransposeF16(hipStream_t s, const uint16_t* src, uint16_t* dst, uint32_t rows, uint32_t cols);
 
 /// True when o_proj runs split by kv group with the attention merge in its prologue (models
 /// whose q dim is too wide for MergeInOProj but whose group is at most 1024 channels wide).

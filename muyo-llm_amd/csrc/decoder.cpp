@@ -107,6 +107,14 @@ struct MuyoDecoder
     uint32_t argBlocks = 0;     // LM-head workgroups = argmax partials per step
     bool mergeInOProj = false;  // o_proj's prologue merges the attention partials
     bool oProjGroups = false;   // o_proj runs per kv group, merging that group's partials
+    // Feed-forward block in one launch (FfnFused) for every layer but the last: its down product
+    // lands in kResidualParts partial vectors of the hidden state (resParts), which the next
+    // layer's QKV and o_proj sum. It reads the down weights transposed (downT, one copy per fused
+    // layer), rebuilt before the next step whenever the down weights may have changed.
+    bool ffnFused = false;
+    float* resParts = nullptr;       // [kResidualParts][hidden]
+    std::vector<TensorSlot> downT;   // per fused layer: [ffn][hidden] fp16
+    bool downTStale = true;
 
     // Sampling (muyo_decoder_set_sampler): off = greedy from the LM head's argmax partials.
     bool sampling = false;
@@ -236,11 +244,21 @@ hipError_t EnqueueEmbed(MuyoDecoder* d, hipStream_t s)
                            kIdsCapacity, d->config.hidden, d->config.vocab);
 }
 
+/// The hidden state entering layer l: a single vector for layer 0 (the embedding) and on
+/// decoders without the fused feed-forward block; otherwise the previous layer's partial vectors.
+uint32_t LayerInputParts(const MuyoDecoder* d, uint32_t l) { return d->ffnFused && l > 0 ? kResidualParts : 1; }
+
+/// True when layer l's feed-forward block is the one-launch FfnFused (all layers but the last,
+/// whose output the LM head reads as one vector).
+bool LayerFfnFused(const MuyoDecoder* d, uint32_t l) { return d->ffnFused && l + 1 < d->config.layers; }
+
 hipError_t EnqueueQkv(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* x)
 {
-    return LaunchQkvRopeAppend(s, d->dims, x, d->At<float>(d->Layer(l, kAttnNorm)), d->At<uint16_t>(d->Layer(l, kQkv)),
-                               d->At<float>(d->Layer(l, kQkvBias)), d->state, d->q,
-                               d->At<uint16_t>(d->Layer(l, kKCache)), d->At<uint16_t>(d->Layer(l, kVCache)));
+    const uint32_t parts = LayerInputParts(d, l);
+    return LaunchQkvRopeAppend(s, d->dims, parts > 1 ? d->resParts : x, d->At<float>(d->Layer(l, kAttnNorm)),
+                               d->At<uint16_t>(d->Layer(l, kQkv)), d->At<float>(d->Layer(l, kQkvBias)), d->state,
+                               d->q, d->At<uint16_t>(d->Layer(l, kKCache)), d->At<uint16_t>(d->Layer(l, kVCache)),
+                               parts);
 }
 
 hipError_t EnqueueAttention(MuyoDecoder* d, hipStream_t s, uint32_t l)
@@ -257,6 +275,18 @@ hipError_t EnqueueAttention(MuyoDecoder* d, hipStream_t s, uint32_t l)
 hipError_t EnqueueOProj(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* residual, float* out)
 {
     const uint16_t* wo = d->At<uint16_t>(d->Layer(l, kOut));
+    if (d->ffnFused)
+    {
+        // The residual is the layer's input; the output also seeds the fused block's parts.
+        const uint32_t parts = LayerInputParts(d, l);
+        const float* res = parts > 1 ? d->resParts : residual;
+        float* seed = LayerFfnFused(d, l) ? d->resParts : nullptr;
+        if (d->mergeInOProj)
+        {
+            return LaunchOProjMerged(s, d->dims, wo, d->scratch, res, out, parts, seed);
+        }
+        return LaunchOProjPlain(s, d->dims, wo, d->attnOut, res, out, parts, seed);
+    }
     if (d->mergeInOProj)
     {
         return LaunchOProjMerged(s, d->dims, wo, d->scratch, residual, out);
@@ -280,6 +310,35 @@ hipError_t EnqueueGateUp(MuyoDecoder* d, hipStream_t s, uint32_t l, float* x)
     }
     return LaunchGateUpSwiGlu(s, d->dims, x, d->At<float>(d->Layer(l, kFfnNorm)), d->At<uint16_t>(d->Layer(l, kGate)),
                               d->At<uint16_t>(d->Layer(l, kUp)), d->act);
+}
+
+/// Layer l's gate/up, swiglu and down in one launch, into the partial vectors o_proj seeded.
+hipError_t EnqueueFfn(MuyoDecoder* d, hipStream_t s, uint32_t l)
+{
+    return LaunchFfnFused(s, d->dims, d->xMid, d->At<float>(d->Layer(l, kFfnNorm)),
+                          d->At<uint16_t>(d->Layer(l, kGate)), d->At<uint16_t>(d->Layer(l, kUp)),
+                          d->At<uint16_t>(d->downT[l]), d->resParts);
+}
+
+/// Rebuilds the transposed down weights of the fused layers when the down weights may have
+/// changed since the last build (queued on `s`, before any step that reads them).
+hipError_t PrepareDerived(MuyoDecoder* d, hipStream_t s)
+{
+    if (!d->ffnFused || !d->downTStale)
+    {
+        return hipSuccess;
+    }
+    for (uint32_t l = 0; l + 1 < d->config.layers; ++l)
+    {
+        const hipError_t status = LaunchTransposeF16(s, d->At<uint16_t>(d->Layer(l, kDown)), d->At<uint16_t>(d->downT[l]),
+                                                     d->config.hidden, d->config.feedForward);
+        if (status != hipSuccess)
+        {
+            return status;
+        }
+    }
+    d->downTStale = false;
+    return hipSuccess;
 }
 
 hipError_t EnqueueDown(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* residual, float* out)
@@ -318,6 +377,14 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
         if ((status = EnqueueOProj(d, s, l, x, d->xMid)) != hipSuccess)
         {
             return LaunchFailed(status, "o_proj", l);
+        }
+        if (LayerFfnFused(d, l))
+        {
+            if ((status = EnqueueFfn(d, s, l)) != hipSuccess)
+            {
+                return LaunchFailed(status, "ffn", l);
+            }
+            continue;
         }
         if ((status = EnqueueGateUp(d, s, l, d->xMid)) != hipSuccess)
         {
@@ -408,6 +475,7 @@ int CaptureStep(MuyoDecoder* d, int variant, uint32_t chunks)
 /// two hipGraphLaunch calls (no synchronisation, no capture).
 int RunStep(MuyoDecoder* d, hipStream_t s, int32_t position)
 {
+    MUYO_HIP_CHECK(PrepareDerived(d, s));
     const uint32_t longChunks = d->dims.attnChunks;
     const int variant =
         d->mergeInOProj && static_cast<uint32_t>(position) < ShortAttnKeys(d->config.headDim) ? 1 : 0;
@@ -479,6 +547,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->mergeInOProj = MergeInOProj(d->dims);
     d->dims.attnChunks = d->mergeInOProj ? kMergeAttnChunks : kMaxAttnChunks;
     d->oProjGroups = OProjInGroups(d->dims);
+    d->ffnFused = FfnFusable(d->dims) && c.layers >= 2;
 
     // Arena layout: embedding, output norm, logits, then each layer's tensors, then activations
     // and scratch. Every tensor starts on a 256-byte boundary.
@@ -515,6 +584,15 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot attnOut = place(qdim * 4);
     const TensorSlot oParts = place(static_cast<size_t>(c.kvHeads) * c.hidden * 4);
     const TensorSlot act = place(static_cast<size_t>(c.feedForward) * 4);
+    const TensorSlot resParts = place(d->ffnFused ? static_cast<size_t>(kResidualParts) * c.hidden * 4 : 0);
+    if (d->ffnFused)
+    {
+        d->downT.resize(c.layers - 1);
+        for (TensorSlot& slot : d->downT)
+        {
+            slot = place(static_cast<size_t>(c.feedForward) * c.hidden * 2);
+        }
+    }
     const TensorSlot state = place(sizeof(DecodeState));
     const TensorSlot ids = place(kIdsCapacity * 4);
     const size_t small = c.kvHeads * chunks * group;
@@ -581,6 +659,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->attnOut = d->At<float>(attnOut);
     d->oParts = d->At<float>(oParts);
     d->act = d->At<float>(act);
+    d->resParts = d->ffnFused ? d->At<float>(resParts) : nullptr;
     d->state = d->At<DecodeState>(state);
     d->ids = d->At<int32_t>(ids);
     d->scratch.attnMax = d->At<float>(attnMax);
@@ -695,6 +774,10 @@ extern "C" int muyo_decoder_tensor(MuyoDecoder* d, uint32_t kind, uint32_t layer
     {
         return status;
     }
+    if (kind == MUYO_TENSOR_FFN_DOWN && device_ptr != nullptr)
+    {
+        d->downTStale = true;  // the caller may write through the pointer
+    }
     if (device_ptr != nullptr)
     {
         *device_ptr = d->arena + slot.offset;
@@ -718,6 +801,10 @@ extern "C" int muyo_decoder_upload(MuyoDecoder* d, uint32_t kind, uint32_t layer
     {
         return Fail(MUYO_E_RANGE, "decoder_upload: %llu bytes given, tensor holds %zu",
                     static_cast<unsigned long long>(bytes), slot.bytes);
+    }
+    if (kind == MUYO_TENSOR_FFN_DOWN)
+    {
+        d->downTStale = true;
     }
     MUYO_HIP_CHECK(hipMemcpyAsync(d->arena + slot.offset, host, bytes, hipMemcpyHostToDevice, d->stream));
     MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
@@ -791,6 +878,7 @@ extern "C" int muyo_decoder_fill_random(MuyoDecoder* d, uint64_t seed)
             }
         }
     }
+    d->downTStale = true;
     if (status == MUYO_OK)
     {
         MUYO_HIP_CHECK(hipStreamSynchronize(d->stream));
@@ -917,7 +1005,11 @@ extern "C" uint32_t muyo_decoder_launches_per_step(const MuyoDecoder* d)
     {
         return 0;
     }
-    const uint32_t greedy = 2u + (d->mergeInOProj || d->oProjGroups ? 5u : 6u) * d->config.layers;
+    uint32_t greedy = 2u + (d->mergeInOProj || d->oProjGroups ? 5u : 6u) * d->config.layers;
+    if (d->ffnFused)
+    {
+        greedy -= d->config.layers - 1;  // one launch for gate/up and down in every layer but the last
+    }
     return greedy + (d->sampling ? SampleLaunches(d->config.vocab, d->sample, true) : 0u);
 }
 
@@ -995,7 +1087,11 @@ extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint
         return Fail(MUYO_E_RANGE, "decoder_enqueue_kernel: layer %u out of range", layer);
     }
     hipStream_t s = AsStream(stream);
-    hipError_t status;
+    hipError_t status = PrepareDerived(d, s);
+    if (status != hipSuccess)
+    {
+        return HipStatus(status, "decoder_enqueue_kernel");
+    }
     switch (kernel)
     {
         case MUYO_KERNEL_EMBED:
@@ -1015,6 +1111,13 @@ extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint
             break;
         case MUYO_KERNEL_DOWN:
             status = EnqueueDown(d, s, layer, d->xMid, d->xB);
+            break;
+        case MUYO_KERNEL_FFN:
+            if (!LayerFfnFused(d, layer))
+            {
+                return Fail(MUYO_E_UNSUPPORTED, "decoder_enqueue_kernel: layer %u runs gate/up and down apart", layer);
+            }
+            status = EnqueueFfn(d, s, layer);
             break;
         case MUYO_KERNEL_LM_HEAD:
             status = EnqueueLmHead(d, s, d->xA);

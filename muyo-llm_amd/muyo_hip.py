@@ -128,7 +128,7 @@ FUSION_BIAS0, FUSION_BIAS1 = 0x1, 0x2
 ROPE_NEOX = 2
 GLU_SPLIT = 2
 
-KERNEL = dict(EMBED=0, QKV=1, ATTENTION=2, O_PROJ=3, GATE_UP=4, DOWN=5, LM_HEAD=6)
+KERNEL = dict(EMBED=0, QKV=1, ATTENTION=2, O_PROJ=3, GATE_UP=4, DOWN=5, LM_HEAD=6, FFN=7)
 
 TENSOR = dict(
     TOKEN_EMBD=0, OUTPUT_NORM=1, ATTN_NORM=2, ATTN_QKV=3, ATTN_QKV_B=4, ATTN_OUTPUT=5, FFN_NORM=6,

@@ -72,6 +72,37 @@ def test_decoder_small_steps_match_oracle(mh, gpu, orc, untied):
                 assert diff.max() <= 2e-3 * (1 + np.abs(orc.half_to_float(ref[:, 30:42])).max())
 
 
+def test_fused_ffn_follows_new_down_weights(mh, gpu, orc):
+    """On a decoder whose feed-forward block is one launch (hidden 256), that launch reads its own
+    transposed copy of the down weights. New down weights, uploaded or written through the
+    tensor's device pointer, are picked up by the next step: the logits follow the oracle on the
+    new weights (std 0.05 instead of 0.02, far past the 1e-3 bar had the old copy been read)."""
+    dec, model = make_pair(mh, orc, SMALL, seed=51, kv_positions=20, kv_seed=52)
+    shape = (SMALL["hidden"], SMALL["ffn"])
+    state = {"token": 5, "pos": 20}
+
+    def check(label):
+        for i in range(3):
+            got = dec.step(state["token"], state["pos"])
+            want, logits, _ = model.step(state["token"], state["pos"])
+            gpu_logits = download(dec, "LOGITS", 0, np.empty(SMALL["vocab"], np.float32))
+            assert close(gpu_logits, logits, 1e-3) == 0, f"{label} step {i}"
+            assert got == want, f"{label} step {i}"
+            state["token"], state["pos"] = got, state["pos"] + 1
+
+    with dec:
+        check("initial weights")
+        new = orc.normal_f16(shape[0] * shape[1], 54, 0.0, 0.05).reshape(shape)
+        model.t[("FFN_DOWN", 0)][...] = new
+        dec.upload("FFN_DOWN", 0, np.ascontiguousarray(new))
+        check("after an upload")
+        ptr, nbytes = dec.tensor("FFN_DOWN", 0)
+        assert mh.load().muyo_fill_normal_f16(ptr, nbytes // 2, 55, 0.0, 0.05, None) == 0
+        gpu.cuda.synchronize()
+        model.t[("FFN_DOWN", 0)][...] = orc.normal_f16(shape[0] * shape[1], 55, 0.0, 0.05).reshape(shape)
+        check("after a write through the pointer")
+
+
 # Shapes off the two Qwen sizes: a full GQA group of 8 with head_dim 128 (q dim 1024, merged in
 # o_proj), q dims past 1024 (o_proj split by kv group: four groups of 5 heads at head_dim 64, two
 # of 6 at 128), eight kv heads (more group parts than gate/up's prologue adds up: a separate merge
@@ -106,9 +137,11 @@ ODD_SHAPES = {
 }
 
 
-# Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel).
+# Launches per greedy step: embed + LM head, and five kernels a layer (six with a merge kernel);
+# with a hidden size of at most 1024 and o_proj not split by kv group, gate/up and down are one
+# launch in every layer but the last.
 ODD_LAUNCHES = {"group8_hd128": 2 + 5, "qdim1280_hd64": 2 + 5 * 2, "hidden_1536_short_cache": 2 + 5,
-                "kv8_merge_kernel": 2 + 6 * 2, "grouped_rows1": 2 + 5, "grouped_rows4": 2 + 5,
+                "kv8_merge_kernel": 2 + 6 * 2 - 1, "grouped_rows1": 2 + 5, "grouped_rows4": 2 + 5,
                 "grouped_rows8": 2 + 5, "wide_rows_few_units": 2 + 5, "long_cache_32k_hd64": 2 + 5,
                 "long_cache_16k_grouped_hd128": 2 + 5}
 
@@ -239,4 +272,5 @@ def test_decoder_rejects_out_of_range(mh, gpu):
         assert lib.muyo_decoder_generate_async(dec.handle, SMALL["vocab"], 0, 1, 0) == mh.MUYO_E_RANGE
         assert lib.muyo_decoder_generate_async(dec.handle, 0, SMALL["max_seq"] - 2, 3, 0) == mh.MUYO_E_RANGE
         assert lib.muyo_decoder_generate_async(dec.handle, 0, -1, 1, 0) == mh.MUYO_E_RANGE
-        assert dec.launches_per_step() == 2 + 5 * SMALL["layers"]
+        # Gate/up and down in one launch in every layer but the last (hidden 256).
+        assert dec.launches_per_step() == 2 + 5 * SMALL["layers"] - (SMALL["layers"] - 1)
