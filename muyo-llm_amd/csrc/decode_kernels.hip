@@ -29,7 +29,6 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
-#include <type_traits>
 
 #include "common.hpp"
 #include "decode_kernels.hpp"
@@ -154,37 +153,25 @@ struct PartsNormStage
 
 /// NormStage over a hidden state held as kResidualParts partial vectors laid end to end (the fused
 /// feed-forward kernel's output): x = ((p0 + p1) + p2) + ..., rms_norm applied as NormStage does.
+/// Always staged through LDS: every lane summing its own chunks of all the parts (the direct
+/// path) reads them once per wave, and at the 0.5B QKV shape those reads made the step 12 us
+/// slower than one workgroup of four waves sharing one staged copy (two waves per copy: 13 us
+/// slower than that; eight: 21 us).
 struct SumNormStage
 {
     const float* parts;  // [kResidualParts][n]
     const float* w;
     float eps;
-    static constexpr bool kCanDirect = true;
+    static constexpr bool kCanDirect = false;
     static constexpr bool kDirect = false;
     static constexpr bool kElementwise = false;
     static constexpr bool kNorm = true;
-    static constexpr bool kSumsParts = true;  // the column-quarter kernel reads a single vector
-    template <int kLpr, int kCpl, class Between>
-    __device__ float Direct(uint32_t n, uint32_t lir, float4 (&xlo)[kCpl], float4 (&xhi)[kCpl], Between between) const
-    {
-        return LoadActivationDirectParts<kLpr, kCpl, kResidualParts>(parts, w, n, lir, xlo, xhi, between);
-    }
     template <int kThreads, int kVec, class Between = NoOp>
     __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
     {
         return StageSplit<kThreads, kVec, true, Between, kResidualParts>(parts, w, n, eps, xs, kResidualParts,
                                                                          nullptr, between);
     }
-};
-
-/// True for a stage whose activation is a sum of partial vectors.
-template <class Stage, class = void>
-struct SumsParts : std::false_type
-{
-};
-template <class Stage>
-struct SumsParts<Stage, std::void_t<decltype(Stage::kSumsParts)>> : std::bool_constant<Stage::kSumsParts>
-{
 };
 
 /// A staging policy applied by every lane to its own activation chunks, straight from global
@@ -1284,17 +1271,13 @@ hipError_t LaunchFusedT(hipStream_t s, uint32_t units, uint32_t blockCap, size_t
         // Units past one round of resident waves: column quarters with several units per
         // workgroup put the whole matrix in flight at once (rows of 257..512 chunks, where a
         // quarter is two chunks per lane).
-        // (Not for an activation summed from partial vectors: the column kernel reads one vector.)
-        if constexpr (!SumsParts<Stage>::value)
+        if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
         {
-            if (blocks * kUnitsPerBlock < units && cols / 8 > 256 && cols / 8 <= 512)
+            const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
+                                                                        shapeOut);
+            if (status != hipErrorNotSupported)
             {
-                const hipError_t status = LaunchColumnsT<kNr, 3, Stage, Epi>(s, units, blockCap, cols, stage, epi,
-                                                                            shapeOut);
-                if (status != hipErrorNotSupported)
-                {
-                    return status;
-                }
+                return status;
             }
         }
     }

@@ -171,57 +171,6 @@ __device__ __forceinline__ float LoadActivationDirect(const float* __restrict__ 
     return ss;
 }
 
-/// LoadActivationDirect with a norm, over an activation held as kParts vectors of n floats laid
-/// end to end, whose sum (((p0 + p1) + p2) + ..., element by element) is x. Every part's loads go
-/// out before any is added: one latency for all of them.
-template <int kLpr, int kCpl, int kParts, class Between = NoOp>
-__device__ __forceinline__ float LoadActivationDirectParts(const float* __restrict__ parts,
-                                                           const float* __restrict__ w, uint32_t n, uint32_t lir,
-                                                           float4 (&xlo)[kCpl], float4 (&xhi)[kCpl],
-                                                           Between between = Between{})
-{
-    const uint32_t nchunks = n / 8;
-    const float4* p4 = reinterpret_cast<const float4*>(parts);
-    const float4* w4 = reinterpret_cast<const float4*>(w);
-    float4 plo[kParts][kCpl];
-    float4 phi[kParts][kCpl];
-    float4 glo[kCpl];
-    float4 ghi[kCpl];
-#pragma unroll
-    for (int i = 0; i < kCpl; ++i)
-    {
-        const uint32_t c = min(lir + i * kLpr, nchunks - 1);
-#pragma unroll
-        for (int p = 0; p < kParts; ++p)
-        {
-            plo[p][i] = p4[p * (n / 4) + 2 * c];
-            phi[p][i] = p4[p * (n / 4) + 2 * c + 1];
-        }
-        glo[i] = w4[2 * c];
-        ghi[i] = w4[2 * c + 1];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    between();
-    __builtin_amdgcn_sched_barrier(0);
-    float ss = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kCpl; ++i)
-    {
-        float4 lo = plo[0][i];
-        float4 hi = phi[0][i];
-#pragma unroll
-        for (int p = 1; p < kParts; ++p)
-        {
-            lo = float4{lo.x + plo[p][i].x, lo.y + plo[p][i].y, lo.z + plo[p][i].z, lo.w + plo[p][i].w};
-            hi = float4{hi.x + phi[p][i].x, hi.y + phi[p][i].y, hi.z + phi[p][i].z, hi.w + phi[p][i].w};
-        }
-        ss += lir + i * kLpr < nchunks ? SquaresOf(lo, hi) : 0.0f;
-        xlo[i] = MulF4(lo, glo[i]);
-        xhi[i] = MulF4(hi, ghi[i]);
-    }
-    return ss;
-}
-
 /// One loaded single-batch row against the activation in registers (chunks past the row add
 /// nothing). The summation order is DotBatch's.
 template <int kLpr, int kCpl>
