@@ -129,28 +129,6 @@ struct NormStage
     }
 };
 
-/// NormStage over an activation that arrives as `groups` partial vectors (the grouped o_proj's
-/// per-kv-group sums, the residual already in group 0): x = ((p0 + p1) + p2) + ..., rms_norm
-/// applied as NormStage does. Workgroup 0 also stores x to `sum`, the residual of the layer's
-/// down projection.
-struct PartsNormStage
-{
-    const float* parts;  // [groups][n]
-    uint32_t groups;
-    const float* w;
-    float eps;
-    float* sum;
-    static constexpr bool kCanDirect = false;  // the sum is stored once, through the staging path
-    static constexpr bool kDirect = false;
-    static constexpr bool kNorm = true;
-    template <int kThreads, int kVec, class Between = NoOp>
-    __device__ float Run(float4* xs, uint32_t n, Between between = Between{}) const
-    {
-        return StageSplit<kThreads, kVec, true>(parts, w, n, eps, xs, groups, blockIdx.x == 0 ? sum : nullptr,
-                                                between);
-    }
-};
-
 /// NormStage over a hidden state held as kResidualParts partial vectors laid end to end (the fused
 /// feed-forward kernel's output): x = ((p0 + p1) + p2) + ..., rms_norm applied as NormStage does.
 /// Always staged through LDS: every lane summing its own chunks of all the parts (the direct
@@ -928,6 +906,18 @@ struct ResidualEpi
     }
 };
 
+/// ResidualEpi that also zeroes row `unit` of `zero` (the next layer's o_proj target, which its kv
+/// groups add into).
+struct ResidualZeroEpi : ResidualEpi
+{
+    float* zero;
+    __device__ void Finish(uint32_t unit, const float* s, const Pre& pre, float& v, int32_t& i) const
+    {
+        ResidualEpi::Finish(unit, s, pre, v, i);
+        zero[unit] = 0.0f;
+    }
+};
+
 /// ResidualEpi for the decoders whose feed-forward block is one launch. The residual is either a
 /// single vector (inParts 1) or kResidualParts partial vectors laid end to end, added in order
 /// (p0 + p1) + ... before the dot; with `parts` set the output also seeds the feed-forward
@@ -1620,8 +1610,8 @@ __global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __rest
                                                           const int32_t* __restrict__ argIndex, uint32_t argBlocks,
                                                           const int32_t* sampled, int32_t* history,
                                                           uint32_t historyCap, float* __restrict__ x,
-                                                          int32_t* __restrict__ ids, uint32_t idsCap, uint32_t hidden,
-                                                          uint32_t vocab)
+                                                          float* __restrict__ zero, int32_t* __restrict__ ids,
+                                                          uint32_t idsCap, uint32_t hidden, uint32_t vocab)
 {
     const int32_t token = sampled != nullptr ? *sampled : ReduceArgMaxPartials(argValue, argIndex, argBlocks);
     if (blockIdx.x == 0 && threadIdx.x == 0)
@@ -1645,6 +1635,10 @@ __global__ __launch_bounds__(kBlock) void BeginStepKernel(const uint16_t* __rest
     for (uint32_t i = blockIdx.x * kBlock + threadIdx.x; i < hidden; i += gridDim.x * kBlock)
     {
         x[i] = ok ? HalfBitsToFloat(row[i]) : 0.0f;
+        if (zero != nullptr)
+        {
+            zero[i] = 0.0f;
+        }
     }
 }
 
@@ -2026,8 +2020,8 @@ struct Channels<4>
 /// group's partials instead of every head's: gridChunks * gw floats.
 template <int kRows, int kCh>
 __global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t* __restrict__ wo, DecodeScratch sc,
-                                                                  const float* __restrict__ residual,
-                                                                  float* __restrict__ parts, uint32_t hidden,
+                                                                  const float* __restrict__ residual, float* out,
+                                                                  uint32_t hidden,
                                                                   uint32_t qdim, uint32_t group, uint32_t headDim,
                                                                   uint32_t gridChunks)
 {
@@ -2105,9 +2099,11 @@ __global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t
         sums[k] = k < kRows ? DotRegisters<kWave, kCpl>(w[k < kRows ? k : 0], xlo, xhi, nchunks, lane) : 0.0f;
     }
     const float total = ScatterSum8(sums);
+    // The kvHeads groups' sums meet in `out` (zeroed by the previous kernel): one atomic add per
+    // group and row, so the adds to an element never queue more than kvHeads deep.
     if (lane < static_cast<uint32_t>(kRows) && myRow < hidden)
     {
-        parts[static_cast<uint64_t>(g) * hidden + myRow] = res + total;
+        __hip_atomic_fetch_add(out + myRow, res + total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -2191,11 +2187,11 @@ hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch
 
 hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* state, const DecodeScratch& scratch,
                            uint32_t argBlocks, float* x, int32_t* ids, uint32_t idsCap, uint32_t hidden,
-                           uint32_t vocab)
+                           uint32_t vocab, float* zero)
 {
     hipLaunchKernelGGL(BeginStepKernel, dim3(CeilDiv(hidden, kBlock)), dim3(kBlock), 0, s, table, state,
                        scratch.argValue, scratch.argIndex, argBlocks, scratch.sampled, scratch.history,
-                       scratch.historyCap, x, ids, idsCap, hidden, vocab);
+                       scratch.historyCap, x, zero, ids, idsCap, hidden, vocab);
     return hipGetLastError();
 }
 
@@ -2312,6 +2308,10 @@ hipError_t LaunchOProjPlain(hipStream_t s, const DecodeDims& dims, const uint16_
                           ResidualPartsEpi{wo, residual, out, parts, dims.hidden, qdim, residualParts});
 }
 
+/// Groups whose o_proj sums meet in one element by atomic adds: more would queue the adds to an
+/// element deeper (they serialise at the memory).
+constexpr uint32_t kMaxOProjGroups = 4;
+
 bool OProjInGroups(const DecodeDims& dims)
 {
     const uint32_t gw = dims.heads / dims.kvHeads * dims.headDim;
@@ -2319,16 +2319,16 @@ bool OProjInGroups(const DecodeDims& dims)
     const uint32_t group = dims.heads / dims.kvHeads;
     const uint32_t channels = dims.headDim / kWave;
     return !MergeInOProj(dims) && gw <= 2 * kWave * 8 && group <= kOProjWaves && dims.headDim % kWave == 0 &&
-           (channels == 1 || channels == 2 || channels == 4) && dims.kvHeads <= kMaxStageParts;
+           (channels == 1 || channels == 2 || channels == 4) && dims.kvHeads <= kMaxOProjGroups;
 }
 
 template <int kRows, int kCh>
 hipError_t LaunchOProjGroupsT(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
-                              const float* residual, float* parts)
+                              const float* residual, float* out)
 {
     const dim3 grid(CeilDiv(dims.hidden, kOProjWaves * kRows), dims.kvHeads);
     const auto kernel = &OProjGroupKernel<kRows, kCh>;
-    hipLaunchKernelGGL(kernel, grid, dim3(kOProjThreads), 0, s, wo, scratch, residual, parts, dims.hidden,
+    hipLaunchKernelGGL(kernel, grid, dim3(kOProjThreads), 0, s, wo, scratch, residual, out, dims.hidden,
                        dims.heads * dims.headDim, dims.heads / dims.kvHeads, dims.headDim,
                        AttnGridChunks(dims.maxSeq, dims.headDim, dims.attnChunks));
     return hipGetLastError();
@@ -2336,21 +2336,21 @@ hipError_t LaunchOProjGroupsT(hipStream_t s, const DecodeDims& dims, const uint1
 
 template <int kRows>
 hipError_t LaunchOProjGroupsRows(hipStream_t s, const DecodeDims& dims, const uint16_t* wo,
-                                 const DecodeScratch& scratch, const float* residual, float* parts)
+                                 const DecodeScratch& scratch, const float* residual, float* out)
 {
     switch (dims.headDim / kWave)
     {
         case 1:
-            return LaunchOProjGroupsT<kRows, 1>(s, dims, wo, scratch, residual, parts);
+            return LaunchOProjGroupsT<kRows, 1>(s, dims, wo, scratch, residual, out);
         case 2:
-            return LaunchOProjGroupsT<kRows, 2>(s, dims, wo, scratch, residual, parts);
+            return LaunchOProjGroupsT<kRows, 2>(s, dims, wo, scratch, residual, out);
         default:
-            return LaunchOProjGroupsT<kRows, 4>(s, dims, wo, scratch, residual, parts);
+            return LaunchOProjGroupsT<kRows, 4>(s, dims, wo, scratch, residual, out);
     }
 }
 
 hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
-                             const float* residual, float* parts)
+                             const float* residual, float* out)
 {
     if (!OProjInGroups(dims))
     {
@@ -2362,29 +2362,34 @@ hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16
     const uint32_t perWave = CeilDiv(dims.hidden, waves);
     if (perWave <= 1)
     {
-        return LaunchOProjGroupsRows<1>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<1>(s, dims, wo, scratch, residual, out);
     }
     if (perWave <= 2)
     {
-        return LaunchOProjGroupsRows<2>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<2>(s, dims, wo, scratch, residual, out);
     }
     if (perWave <= 4)
     {
-        return LaunchOProjGroupsRows<4>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<4>(s, dims, wo, scratch, residual, out);
     }
     if (perWave <= 7)
     {
-        return LaunchOProjGroupsRows<7>(s, dims, wo, scratch, residual, parts);
+        return LaunchOProjGroupsRows<7>(s, dims, wo, scratch, residual, out);
     }
-    return LaunchOProjGroupsRows<8>(s, dims, wo, scratch, residual, parts);
+    return LaunchOProjGroupsRows<8>(s, dims, wo, scratch, residual, out);
 }
 
-hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const float* parts, const float* normW,
-                                   const uint16_t* wgate, const uint16_t* wup, float* act, float* sum)
+hipError_t LaunchMatVecResidualZero(hipStream_t s, const uint16_t* w, const float* x, const float* residual,
+                                    float* out, float* zero, uint32_t rows, uint32_t cols)
 {
-    GateUpEpi epi{wgate, wup, act, dims.ffn, dims.hidden};
-    return LaunchFused<2>(s, dims.ffn, kNoLimit, dims.hidden, PartsNormStage{parts, dims.kvHeads, normW, dims.eps, sum},
-                          epi);
+    ResidualZeroEpi epi{};
+    epi.w = w;
+    epi.residual = residual;
+    epi.out = out;
+    epi.rows = rows;
+    epi.cols = cols;
+    epi.zero = zero;
+    return LaunchFused<1>(s, rows, kNoLimit, cols, PlainStage{x}, epi);
 }
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,

@@ -105,9 +105,11 @@ bool MergeInOProj(const DecodeDims& dims);
 hipError_t LaunchSetState(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, int32_t token,
                           int32_t position, uint32_t argBlocks, uint32_t step = 0);
 
+/// `zero` (optional): a [hidden] vector cleared at the same time (the first layer's grouped
+/// o_proj target).
 hipError_t LaunchBeginStep(hipStream_t s, const uint16_t* table, DecodeState* state, const DecodeScratch& scratch,
                            uint32_t argBlocks, float* x, int32_t* ids, uint32_t idsCap, uint32_t hidden,
-                           uint32_t vocab);
+                           uint32_t vocab, float* zero = nullptr);
 
 hipError_t LaunchFinalize(hipStream_t s, DecodeState* state, const DecodeScratch& scratch, uint32_t argBlocks,
                           int32_t* ids, uint32_t idsCap);
@@ -151,17 +153,19 @@ hipError_t LaunchTransposeF16(hipStream_t s, const uint16_t* src, uint16_t* dst,
 /// whose q dim is too wide for MergeInOProj but whose group is at most 1024 channels wide).
 bool OProjInGroups(const DecodeDims& dims);
 
-/// o_proj per kv group: parts[g][row] = (g == 0 ? residual[row] : 0) + W_o[row, group g's columns]
-/// . merged attention of group g. The layer's hidden state is the sum of the kvHeads parts.
+/// o_proj per kv group: out[row] += (g == 0 ? residual[row] : 0) + W_o[row, group g's columns]
+/// . merged attention of group g, one atomic add per group and row into `out`, which must hold
+/// zeros. The order of the kvHeads adds varies from run to run, so the sum does in its last bits.
 hipError_t LaunchOProjGroups(hipStream_t s, const DecodeDims& dims, const uint16_t* wo, const DecodeScratch& scratch,
-                             const float* residual, float* parts);
-
-/// LaunchGateUpSwiGlu on the sum of the kvHeads o_proj parts, which it also stores to `sum`.
-hipError_t LaunchGateUpSwiGluParts(hipStream_t s, const DecodeDims& dims, const float* parts, const float* normW,
-                                   const uint16_t* wgate, const uint16_t* wup, float* act, float* sum);
+                             const float* residual, float* out);
 
 hipError_t LaunchMatVecResidual(hipStream_t s, const uint16_t* w, const float* x, const float* residual, float* out,
                                 uint32_t rows, uint32_t cols);
+
+/// LaunchMatVecResidual that also stores zeros to zero[0..rows) (the next layer's grouped o_proj
+/// target).
+hipError_t LaunchMatVecResidualZero(hipStream_t s, const uint16_t* w, const float* x, const float* residual,
+                                    float* out, float* zero, uint32_t rows, uint32_t cols);
 
 /// out[row] = (W[row] . x + bias0[row]) + bias1[row] (null biases skipped) on the fused GEMV's
 /// launch shapes: W fp16 [rows][cols] with 16-byte aligned rows, x 16-byte aligned, cols % 8 == 0.

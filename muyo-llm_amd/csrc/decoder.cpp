@@ -99,7 +99,7 @@ struct MuyoDecoder
     float* xMid = nullptr;
     float* q = nullptr;
     float* attnOut = nullptr;
-    float* oParts = nullptr;  // [kvHeads][hidden] o_proj sums per kv group (oProjGroups)
+    float* xMid2 = nullptr;   // with o_proj split by kv group: odd layers' hidden state after attention
     float* act = nullptr;
     DecodeState* state = nullptr;
     int32_t* ids = nullptr;
@@ -238,10 +238,16 @@ int LaunchFailed(hipError_t status, const char* kernel, uint32_t layer)
                 hipGetErrorString(status), static_cast<int>(status));
 }
 
+/// The hidden state after layer l's attention. With o_proj split by kv group the groups add into
+/// it atomically, so it alternates between two buffers by layer: the kernel before o_proj (the
+/// step's BeginStep for layer 0, the previous layer's down projection otherwise) zeroes it while
+/// the other one is still being read.
+float* LayerMid(const MuyoDecoder* d, uint32_t l) { return d->oProjGroups && l % 2 == 1 ? d->xMid2 : d->xMid; }
+
 hipError_t EnqueueEmbed(MuyoDecoder* d, hipStream_t s)
 {
     return LaunchBeginStep(s, d->At<uint16_t>(d->tokenEmbd), d->state, d->scratch, d->argBlocks, d->xA, d->ids,
-                           kIdsCapacity, d->config.hidden, d->config.vocab);
+                           kIdsCapacity, d->config.hidden, d->config.vocab, d->oProjGroups ? LayerMid(d, 0) : nullptr);
 }
 
 /// The hidden state entering layer l: a single vector for layer 0 (the embedding) and on
@@ -293,21 +299,14 @@ hipError_t EnqueueOProj(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* 
     }
     if (d->oProjGroups)
     {
-        return LaunchOProjGroups(s, d->dims, wo, d->scratch, residual, d->oParts);  // gate/up writes `out`
+        return LaunchOProjGroups(s, d->dims, wo, d->scratch, residual, out);
     }
     return LaunchMatVecResidual(s, wo, d->attnOut, residual, out, d->config.hidden, d->config.heads * d->config.headDim);
 }
 
-/// `x` is the hidden state after attention: read, or, when o_proj leaves per-group parts,
-/// written as their sum.
+/// `x` is the hidden state after attention.
 hipError_t EnqueueGateUp(MuyoDecoder* d, hipStream_t s, uint32_t l, float* x)
 {
-    if (d->oProjGroups)
-    {
-        return LaunchGateUpSwiGluParts(s, d->dims, d->oParts, d->At<float>(d->Layer(l, kFfnNorm)),
-                                       d->At<uint16_t>(d->Layer(l, kGate)), d->At<uint16_t>(d->Layer(l, kUp)),
-                                       d->act, x);
-    }
     return LaunchGateUpSwiGlu(s, d->dims, x, d->At<float>(d->Layer(l, kFfnNorm)), d->At<uint16_t>(d->Layer(l, kGate)),
                               d->At<uint16_t>(d->Layer(l, kUp)), d->act);
 }
@@ -343,6 +342,12 @@ hipError_t PrepareDerived(MuyoDecoder* d, hipStream_t s)
 
 hipError_t EnqueueDown(MuyoDecoder* d, hipStream_t s, uint32_t l, const float* residual, float* out)
 {
+    if (d->oProjGroups && l + 1 < d->config.layers)
+    {
+        // Also zeroes the next layer's o_proj target.
+        return LaunchMatVecResidualZero(s, d->At<uint16_t>(d->Layer(l, kDown)), d->act, residual, out,
+                                        LayerMid(d, l + 1), d->config.hidden, d->config.feedForward);
+    }
     return LaunchMatVecResidual(s, d->At<uint16_t>(d->Layer(l, kDown)), d->act, residual, out, d->config.hidden,
                                 d->config.feedForward);
 }
@@ -374,7 +379,7 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
         {
             return LaunchFailed(status, "attention", l);
         }
-        if ((status = EnqueueOProj(d, s, l, x, d->xMid)) != hipSuccess)
+        if ((status = EnqueueOProj(d, s, l, x, LayerMid(d, l))) != hipSuccess)
         {
             return LaunchFailed(status, "o_proj", l);
         }
@@ -386,11 +391,11 @@ int Enqueue(MuyoDecoder* d, hipStream_t s)
             }
             continue;
         }
-        if ((status = EnqueueGateUp(d, s, l, d->xMid)) != hipSuccess)
+        if ((status = EnqueueGateUp(d, s, l, LayerMid(d, l))) != hipSuccess)
         {
             return LaunchFailed(status, "gate_up", l);
         }
-        if ((status = EnqueueDown(d, s, l, d->xMid, other)) != hipSuccess)
+        if ((status = EnqueueDown(d, s, l, LayerMid(d, l), other)) != hipSuccess)
         {
             return LaunchFailed(status, "down", l);
         }
@@ -582,7 +587,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     const TensorSlot xMid = place(c.hidden * 4);
     const TensorSlot q = place(qdim * 4);
     const TensorSlot attnOut = place(qdim * 4);
-    const TensorSlot oParts = place(static_cast<size_t>(c.kvHeads) * c.hidden * 4);
+    const TensorSlot xMid2 = place(c.hidden * 4);
     const TensorSlot act = place(static_cast<size_t>(c.feedForward) * 4);
     const TensorSlot resParts = place(d->ffnFused ? static_cast<size_t>(kResidualParts) * c.hidden * 4 : 0);
     if (d->ffnFused)
@@ -657,7 +662,7 @@ extern "C" int muyo_decoder_create(const MuyoQwen2Config* config, MuyoDecoder** 
     d->xMid = d->At<float>(xMid);
     d->q = d->At<float>(q);
     d->attnOut = d->At<float>(attnOut);
-    d->oParts = d->At<float>(oParts);
+    d->xMid2 = d->At<float>(xMid2);
     d->act = d->At<float>(act);
     d->resParts = d->ffnFused ? d->At<float>(resParts) : nullptr;
     d->state = d->At<DecodeState>(state);
@@ -1104,13 +1109,13 @@ extern "C" int muyo_decoder_enqueue_kernel(MuyoDecoder* d, uint32_t kernel, uint
             status = EnqueueAttention(d, s, layer);
             break;
         case MUYO_KERNEL_O_PROJ:
-            status = EnqueueOProj(d, s, layer, d->xA, d->xMid);
+            status = EnqueueOProj(d, s, layer, d->xA, LayerMid(d, layer));
             break;
         case MUYO_KERNEL_GATE_UP:
-            status = EnqueueGateUp(d, s, layer, d->xMid);
+            status = EnqueueGateUp(d, s, layer, LayerMid(d, layer));
             break;
         case MUYO_KERNEL_DOWN:
-            status = EnqueueDown(d, s, layer, d->xMid, d->xB);
+            status = EnqueueDown(d, s, layer, LayerMid(d, layer), d->xB);
             break;
         case MUYO_KERNEL_FFN:
             if (!LayerFfnFused(d, layer))
