@@ -1421,7 +1421,8 @@ __global__ __launch_bounds__(kBlock) void FfnFusedKernel(const float* __restrict
     __shared__ float total[8 * kFfnMaxChunks];
     const uint32_t t = threadIdx.x;
     const uint32_t lane = t & (kWave - 1);
-    const uint32_t wave = t / kWave;
+    // Wave-uniform, so the gate/up row addresses are scalar.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t / kWave);
     const uint32_t nchunks = hidden / 8;
     const uint32_t base = blockIdx.x * kFfnUnits;
     // Down rows: half h (0 or 1) takes units h, h + 2, ...; threads past 2 * nchunks load a copy
