@@ -1975,46 +1975,29 @@ __global__ __launch_bounds__(128) void AttentionMergeKernel(DecodeScratch sc, fl
 constexpr int kOProjThreads = 512;
 constexpr uint32_t kOProjWaves = kOProjThreads / kWave;
 
-/// kCh consecutive floats, loaded and stored as one access.
-template <int kCh>
-struct Channels;
-template <>
-struct Channels<1>
+/// v plus the value of the same lane in the paired 16-lane row (rows 0 and 1, 2 and 3).
+__device__ __forceinline__ float RowPairSum(float v)
 {
-    float v[1];
-    __device__ static Channels Load(const float* p) { return Channels{{*p}}; }
-    __device__ void Store(float* p) const { *p = v[0]; }
-};
-template <>
-struct Channels<2>
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
+
+/// v plus the value of the same lane in the other half of the wave.
+__device__ __forceinline__ float HalfPairSum(float v)
 {
-    float v[2];
-    __device__ static Channels Load(const float* p)
-    {
-        const float2 x = *reinterpret_cast<const float2*>(p);
-        return Channels{{x.x, x.y}};
-    }
-    __device__ void Store(float* p) const { *reinterpret_cast<float2*>(p) = float2{v[0], v[1]}; }
-};
-template <>
-struct Channels<4>
-{
-    float v[4];
-    __device__ static Channels Load(const float* p)
-    {
-        const float4 x = *reinterpret_cast<const float4*>(p);
-        return Channels{{x.x, x.y, x.z, x.w}};
-    }
-    __device__ void Store(float* p) const { *reinterpret_cast<float4*>(p) = float4{v[0], v[1], v[2], v[3]}; }
-};
+    const auto pair = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
 
 /// o_proj split by kv group, with the attention merge in its prologue. Workgroup (b, g) of 512
 /// threads owns group g's query heads, the W_o columns [g * gw, (g + 1) * gw) with gw = group *
 /// headDim (at most 1024), and rows b * 8 + w + k * 8 * gridDim.x (k < kRows <= 8) for its wave w.
-/// Wave h merges query head h (group <= 8, kCh = headDim / 64 channels per lane): lane c turns
-/// chunk c's (max, sum) into its weight 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c', and every lane
-/// adds its channels of the chunks' P.V rows with those weights, read from lane c, so the
-/// exponentials and the division run once per chunk rather than once per channel. The merge
+/// Wave h merges query head h (group <= 8, kCh = headDim / 64): lane c turns chunk c's (max, sum)
+/// into its weight 2^(m_c - M) / sum_c' 2^(m_c' - M) l_c', so the exponentials and the division
+/// run once per chunk rather than once per channel. The head's chunk rows arrive as 16-byte
+/// loads that each cover 4 / kCh chunks side by side (headDim 128: 8 loads instead of 16 of 8
+/// bytes); every lane weighs its chunks with the weights read from their lanes, and the lane
+/// groups' sums meet by lane swaps. The merge
 /// operands are requested before the weight rows (loads complete in order) and merged into LDS
 /// while the rows are in flight. The rows' dots, reduced by ScatterSum8, go to parts[g][row],
 /// group 0 adding the residual; the next kernel's prologue sums the groups. A workgroup reads one
@@ -2043,12 +2026,21 @@ __global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t
     const uint32_t lc = min(lane, gridChunks - 1);
     float m = sc.attnMax[headBase + static_cast<uint64_t>(lc) * group];
     const float l = sc.attnSum[headBase + static_cast<uint64_t>(lc) * group];
-    Channels<kCh> a[kMaxAttnChunks];
+    // A head's P.V row is kQuads float4s: each 16-byte load covers kPerLoad chunks side by side
+    // (lane group `sub` takes chunks sub, sub + kPerLoad, ...), so a wave requests its head's 16
+    // chunks in kLoads loads.
+    constexpr uint32_t kQuads = 16 * kCh;
+    constexpr uint32_t kPerLoad = kWave / kQuads;
+    constexpr uint32_t kLoads = kMaxAttnChunks / kPerLoad;
+    static_assert(kPerLoad * kLoads == kMaxAttnChunks, "chunks per load");
+    const uint32_t sub = lane / kQuads;
+    const uint32_t quad = lane % kQuads;
+    float4 a[kLoads];
 #pragma unroll
-    for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+    for (uint32_t i = 0; i < kLoads; ++i)
     {
-        const uint64_t slot = headBase + static_cast<uint64_t>(min(c, gridChunks - 1)) * group;
-        a[c] = Channels<kCh>::Load(sc.attnAcc + slot * headDim + lane * kCh);
+        const uint64_t slot = headBase + static_cast<uint64_t>(min(i * kPerLoad + sub, gridChunks - 1)) * group;
+        a[i] = *reinterpret_cast<const float4*>(sc.attnAcc + slot * headDim + 4 * quad);
     }
     half8 w[kRows][kCpl];
 #pragma unroll
@@ -2069,24 +2061,40 @@ __global__ __launch_bounds__(kOProjThreads) void OProjGroupKernel(const uint16_t
         const float e = top == -INFINITY || m == -INFINITY ? 0.0f : exp2f(m - top);
         const float den = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(GroupSum<16>(e * l))));
         const float weight = den > 0.0f ? e / den : 0.0f;
-        Channels<kCh> out{};
+        float4 merged = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (uint32_t c = 0; c < kMaxAttnChunks; ++c)
+        for (uint32_t i = 0; i < kLoads; ++i)
         {
-            const float wc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), c));
+            // Chunk i * kPerLoad + sub's weight, read from that chunk's lane.
+            float wc = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kCh; ++j)
+            for (uint32_t j = 0; j < kPerLoad; ++j)
             {
-                out.v[j] = fmaf(wc, a[c].v[j], out.v[j]);
+                const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(weight), i * kPerLoad + j));
+                wc = sub == j ? wj : wc;
             }
+            merged.x = fmaf(wc, a[i].x, merged.x);
+            merged.y = fmaf(wc, a[i].y, merged.y);
+            merged.z = fmaf(wc, a[i].z, merged.z);
+            merged.w = fmaf(wc, a[i].w, merged.w);
         }
-        if (wave < group)
+        // The lane groups' sums: rows 2r and 2r + 1 (16-lane groups), then the wave's halves.
+        if constexpr (kPerLoad == 4)
         {
-            // Channel ch of the group sits in chunk ch / 8: its low float4 for ch % 8 < 4.
-            const uint32_t ch = hh * headDim + lane * kCh;
-            const uint32_t pos = ch % 8;
-            const uint32_t at = pos < 4 ? 4 * (ch / 8) + pos : 4 * nchunks + 4 * (ch / 8) + pos - 4;
-            out.Store(reinterpret_cast<float*>(xs) + at);
+            merged = float4{RowPairSum(merged.x), RowPairSum(merged.y), RowPairSum(merged.z), RowPairSum(merged.w)};
+        }
+        if constexpr (kPerLoad >= 2)
+        {
+            merged = float4{HalfPairSum(merged.x), HalfPairSum(merged.y), HalfPairSum(merged.z),
+                            HalfPairSum(merged.w)};
+        }
+        if (wave < group && sub == 0)
+        {
+            // Channels ch .. ch + 3 of the group sit in chunk ch / 8: its low float4 for
+            // ch % 8 == 0, its high one for ch % 8 == 4.
+            const uint32_t ch = hh * headDim + 4 * quad;
+            const uint32_t at = ch % 8 == 0 ? 4 * (ch / 8) : 4 * nchunks + 4 * (ch / 8);
+            *reinterpret_cast<float4*>(reinterpret_cast<float*>(xs) + at) = merged;
         }
     }
     __syncthreads();
