@@ -49,8 +49,8 @@ MFMA_F16_PEAK = 2.5e15  # dense fp16 matrix-core flop/s of MI355X
 # WRITE_SIZE, each scaled by what the counter reads for a 256 MiB device copy, and its L2 hit rate
 # (TCC_HIT_sum / (TCC_HIT_sum + TCC_MISS_sum)), over whole steps launched kernel by kernel
 # (profiles/decode_step_counters_0.5b.md: `--kernel-only step_05b`, `--summarize-counters`).
-FFN_TRAFFIC_BYTES = 27_250_116
-FFN_L2_HIT_RATE = 0.193
+FFN_TRAFFIC_BYTES = 27_246_760
+FFN_L2_HIT_RATE = 0.192
 FFN_COUNTER_SOURCE = ("profiles/decode_step_counters_0.5b.md: rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE (each scaled "
                       "by a 256 MiB device copy) and TCC_HIT/TCC_MISS over whole steps, ffn rows")
 
