@@ -258,7 +258,10 @@ void muyo_decoder_destroy(MuyoDecoder* decoder);
 /* The configuration the decoder was created with. */
 int muyo_decoder_config(const MuyoDecoder* decoder, MuyoQwen2Config* out);
 
-/* Device address and byte size of one tensor. */
+/* Device address and byte size of one tensor. A request for MUYO_TENSOR_FFN_DOWN's address
+ * makes the next step rebuild the decoder's transposed copy of that matrix (decoders that run
+ * the feed-forward block as one launch): writes through an address requested before a step
+ * are seen by later steps only after another request or an upload. */
 int muyo_decoder_tensor(MuyoDecoder* decoder, uint32_t kind, uint32_t layer, void** device_ptr, uint64_t* bytes);
 
 /* Synchronous host<->device copies of a whole tensor (bytes must equal the tensor's size). */
